@@ -1,0 +1,219 @@
+/*
+ * uocr_moe — MI355X (gfx950) MoE feed-forward path of the Unlimited-OCR
+ * decoder behind a plain C ABI.
+ *
+ * The reference is the Rust crate `uocr`; this library replaces the body of
+ * `Decoder::experts` (src/decoder/mod.rs:124-220) and the CPU kernels it
+ * calls, and adds the GPU counterparts of the operator entry points the
+ * reference tests exercise. All pointers are plain host or device pointers
+ * with explicit sizes; no torch or Rust types cross the boundary.
+ *
+ * Status codes follow the order of the reference's OcrError variants
+ * (src/error.rs:1-19): Io, Json, Format, Shape, Unsupported, Resource,
+ * Numerical. A failing call leaves its outputs unspecified, like an Err.
+ */
+#ifndef UOCR_MOE_H
+#define UOCR_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum uocr_status {
+  UOCR_OK = 0,
+  UOCR_ERR_IO = 1,
+  UOCR_ERR_JSON = 2,
+  UOCR_ERR_FORMAT = 3,
+  UOCR_ERR_SHAPE = 4,
+  UOCR_ERR_UNSUPPORTED = 5,
+  UOCR_ERR_RESOURCE = 6,
+  UOCR_ERR_NUMERICAL = 7,
+} uocr_status;
+
+/* QuantizationMode (src/cpu/quantized.rs:242-247), plus "no overlay". */
+typedef enum uocr_quant_mode {
+  UOCR_QUANT_NONE = 0,                /* BF16 weights, FP32 activations */
+  UOCR_QUANT_WEIGHTS_ONLY = 1,        /* QuantizationMode::WeightsOnly */
+  UOCR_QUANT_DYNAMIC_ACTIVATIONS = 2, /* QuantizationMode::DynamicActivations */
+} uocr_quant_mode;
+
+/* Backend (src/cpu/mod.rs:10-16) with the GPU variant this library adds. */
+typedef enum uocr_backend {
+  UOCR_BACKEND_SCALAR = 0,
+  UOCR_BACKEND_NEON = 1,
+  UOCR_BACKEND_ACCELERATE = 2,
+  UOCR_BACKEND_AUTO = 3,
+  UOCR_BACKEND_GPU = 4,
+} uocr_backend;
+
+/* Where the pointers handed to uocr_moe_layer_create live. */
+typedef enum uocr_memory {
+  UOCR_MEMORY_HOST = 0,
+  UOCR_MEMORY_DEVICE = 1,
+} uocr_memory;
+
+/* Forward flags. The multi-row MFMA path rounds its FP32 activations to
+ * bf16 operands: FP32_CLASS splits each activation into two bf16 terms
+ * (relative error ~2^-17, the 1e-3 tolerance class); BF16 uses one term
+ * (the 2e-2 class). Decode GEMV paths always compute in FP32. */
+#define UOCR_FLAG_FP32_CLASS 0u
+#define UOCR_FLAG_BF16_ACTIVATIONS 1u
+/* Force one expert engine, for tests: 0 = choose by token count. */
+#define UOCR_FLAG_FORCE_GEMV 2u
+#define UOCR_FLAG_FORCE_MFMA 4u
+
+/* The MoE fields of ModelConfig (src/model/config.rs:35-54). */
+typedef struct uocr_moe_config {
+  uint32_t hidden_size;           /* 1280 */
+  uint32_t moe_intermediate_size; /* 896 */
+  uint32_t n_routed_experts;      /* 64 */
+  uint32_t n_shared_experts;      /* 2 */
+  uint32_t num_experts_per_tok;   /* 6 */
+  uint32_t norm_topk_prob;        /* bool */
+  float routed_scaling_factor;    /* 1.0 */
+  float rms_norm_eps;             /* 1e-6 */
+} uocr_moe_config;
+
+/* BF16 checkpoint tensors of one MoE layer, row-major [out, in] as stored
+ * under model.layers.N.mlp.* (src/decoder/mod.rs:58-80); raw bf16 bits.
+ * E = n_routed_experts, I = moe_intermediate_size, S = I * n_shared_experts,
+ * H = hidden_size. norm_weight (post_attention_layernorm) may be NULL unless
+ * uocr_moe_block_forward is used. */
+typedef struct uocr_moe_bf16_weights {
+  const uint16_t* router;      /* mlp.gate.weight               [E,H]   */
+  const uint16_t* expert_gate; /* mlp.experts.*.gate_proj       [E,I,H] */
+  const uint16_t* expert_up;   /* mlp.experts.*.up_proj         [E,I,H] */
+  const uint16_t* expert_down; /* mlp.experts.*.down_proj       [E,H,I] */
+  const uint16_t* shared_gate; /* mlp.shared_experts.gate_proj  [S,H]   */
+  const uint16_t* shared_up;   /* mlp.shared_experts.up_proj    [S,H]   */
+  const uint16_t* shared_down; /* mlp.shared_experts.down_proj  [H,S]   */
+  const uint16_t* norm_weight; /* post_attention_layernorm      [H]     */
+} uocr_moe_bf16_weights;
+
+/* INT8 block-32 overlay matrices (src/cpu/quantized.rs:9-42, 239-369):
+ * int8 [rows, cols] and f32 scales [rows, cols/32]. The router is never
+ * part of the overlay. */
+typedef struct uocr_moe_int8_weights {
+  const int8_t* expert_gate;
+  const float* expert_gate_scales;
+  const int8_t* expert_up;
+  const float* expert_up_scales;
+  const int8_t* expert_down;
+  const float* expert_down_scales;
+  const int8_t* shared_gate;
+  const float* shared_gate_scales;
+  const int8_t* shared_up;
+  const float* shared_up_scales;
+  const int8_t* shared_down;
+  const float* shared_down_scales;
+} uocr_moe_int8_weights;
+
+/* Optional per-forward trace, device pointers; NULL members are skipped.
+ * Routing order is route()'s: probability descending, id ascending. */
+typedef struct uocr_moe_trace {
+  float* logits;           /* [T,E] router logits */
+  int32_t* topk_ids;       /* [T,k] */
+  float* topk_weights;     /* [T,k] */
+  int32_t* expert_offsets; /* [E+1] start of each expert's assignments */
+  int32_t* perm_rows;      /* [T*k] token row of each assignment, expert-major */
+  float* perm_weights;     /* [T*k] routing weight of each assignment */
+} uocr_moe_trace;
+
+typedef struct uocr_gpu_ctx uocr_gpu_ctx;
+typedef struct uocr_moe_layer uocr_moe_layer;
+
+/* ---------------------------------------------------------------- context */
+
+/* CpuContext::new(Backend, threads, scratch_limit) (src/cpu/mod.rs:26-49),
+ * GPU flavour: binds `device`, creates the context's stream and reserves
+ * `scratch_limit` bytes of device scratch. 0 bytes -> Resource, like
+ * threads == 0 or scratch_limit == 0 in the reference. */
+int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out);
+void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx);
+/* The stream work is enqueued on (a hipStream_t). */
+void* uocr_gpu_ctx_stream(uocr_gpu_ctx* ctx);
+/* Waits for the context's stream and reports errors raised on the device
+ * (non-finite routing, normalisation or activation quantisation inputs ->
+ * Numerical), then clears them. */
+int uocr_gpu_ctx_synchronize(uocr_gpu_ctx* ctx);
+/* Message of the last failure on this thread (ctx may be NULL). */
+const char* uocr_last_error(const uocr_gpu_ctx* ctx);
+/* Bytes of scratch a forward of T tokens needs (CpuContext::check_elements,
+ * src/cpu/mod.rs:73-78); forwards above the context's limit fail with
+ * Resource. */
+size_t uocr_moe_scratch_bytes(const uocr_moe_config* cfg, size_t T);
+
+/* ------------------------------------------------------------------ layer */
+
+/* Decoder::new shape rules for one MoE layer (src/decoder/mod.rs:32-88) and
+ * ModelConfig validation (src/model/config.rs:74-115) for the MoE fields;
+ * uploads and repacks the BF16 weights once. The GPU layer supports
+ * hidden_size and moe_intermediate_size that are multiples of 64,
+ * n_routed_experts <= 64 and num_experts_per_tok <= 8 (else Unsupported). */
+int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
+                          const uocr_moe_bf16_weights* weights, uocr_memory where,
+                          uocr_moe_layer** out);
+/* Model::load_with_quantization overlay step (src/model/mod.rs:82-109,
+ * src/cpu/quantized.rs:306-366): validates and uploads the INT8 matrices and
+ * selects the mode. DynamicActivations without an overlay -> Format. */
+int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
+                               const uocr_moe_int8_weights* weights, uocr_memory where,
+                               uocr_quant_mode mode);
+/* Model::precision labels (src/model/mod.rs:65-73). */
+const char* uocr_moe_layer_precision(const uocr_moe_layer* layer);
+/* Device bytes held by the layer's weights. */
+size_t uocr_moe_layer_device_bytes(const uocr_moe_layer* layer);
+void uocr_moe_layer_destroy(uocr_moe_layer* layer);
+
+/* ---------------------------------------------------------------- forward */
+
+/* Decoder::experts (src/decoder/mod.rs:124-220): y[T,H] = shared(x) +
+ * sum over each row's top-k experts, ascending id, of p * expert(x).
+ * x and y are device pointers (FP32 row-major [T,H]). Enqueued on the
+ * context stream; the call returns once the work is queued. Device-side
+ * errors surface at uocr_gpu_ctx_synchronize. T == 0 is a no-op. */
+int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x,
+                           size_t T, float* y, uint32_t flags, const uocr_moe_trace* trace);
+/* The same, then synchronize: errors are reported by this call. */
+int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
+                     float* y, uint32_t flags, const uocr_moe_trace* trace);
+/* The post-attention half of Decoder::layer (src/decoder/mod.rs:351-363)
+ * over a stack of MoE layers: x <- x + experts(rms_norm(x, norm_weight)),
+ * layer after layer. x and y are device [T,H]; y may equal x. Synchronous. */
+int uocr_moe_block_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* const* layers,
+                           size_t n_layers, const float* x, size_t T, float* y, uint32_t flags);
+int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const* layers,
+                                 size_t n_layers, const float* x, size_t T, float* y,
+                                 uint32_t flags);
+
+/* ------------------------------------------------------------- operators */
+/* Device counterparts of the reference's CPU operators, on device pointers,
+ * synchronous. They back the operator-level parity tests. */
+
+/* moe::route over T rows of n logits (src/decoder/moe.rs:7-30). */
+int uocr_route(uocr_gpu_ctx* ctx, const float* logits, size_t T, size_t n, size_t count,
+               int normalize, float scale, int32_t* ids, float* weights);
+/* ops::linear_weight with a BF16 [n,k] matrix and no bias
+ * (src/cpu/ops.rs:62-133): y[m,n] = x[m,k] . w^T in FP32. */
+int uocr_linear_bf16(uocr_gpu_ctx* ctx, const float* x, size_t m, size_t k, const uint16_t* w,
+                     size_t n, float* y);
+/* Int8Matrix::linear (src/cpu/quantized.rs:99-150). */
+int uocr_int8_linear(uocr_gpu_ctx* ctx, const int8_t* q, const float* scales, size_t rows,
+                     size_t cols, const float* x, size_t batch, float* y);
+/* Int8Matrix::linear_dynamic_int8 (src/cpu/quantized.rs:155-236): one input
+ * row. block_sums (optional, [rows, cols/32]) receives the exact i32
+ * per-block accumulators. */
+int uocr_int8_linear_dynamic(uocr_gpu_ctx* ctx, const int8_t* q, const float* scales,
+                             size_t rows, size_t cols, const float* x, float* y,
+                             int32_t* block_sums);
+/* ops::rms_norm (src/cpu/ops.rs:362-423), rows x width. */
+int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
+                  const float* weight, float eps, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

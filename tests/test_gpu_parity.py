@@ -1,0 +1,315 @@
+"""GPU parity: the HIP library (through the C ABI) against the CPU oracle on
+the same seeded inputs.
+
+Bars: top-k ids and the dispatch permutation identical except where the
+oracle's logits tie within 1e-6; int8 x int8 block accumulators bit-exact;
+outputs within a normwise 1e-3 (max over rows of ||y - ref||_inf /
+||ref||_inf) on FP32-accumulate paths.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import oracle as orc  # noqa: E402
+import uocr_moe as um  # noqa: E402
+from uocr_moe import synthetic as syn  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-3
+TIE = 1e-6
+FULL = dict(hidden=1280, inter=896, experts=64, shared=2)
+SMALL = dict(hidden=128, inter=64, experts=16, shared=2)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = um.Context(0, 2 << 30)
+    yield c
+    c.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+class Case:
+    """A layer in oracle form and uploaded to the GPU."""
+
+    def __init__(self, ctx, shape, top_k, seed, quant=orc.QUANT_NONE, normalize=True, scale=1.0,
+                 router_scale=None):
+        self.shape = shape
+        self.top_k = top_k
+        w = syn.moe_weights(seed=seed, router_scale=router_scale, norm=True, **shape)
+        self.w = w
+        self.orc = orc.MoeWeights(
+            hidden=shape["hidden"], inter=shape["inter"], n_experts=shape["experts"],
+            top_k=top_k, n_shared=shape["shared"], normalize=normalize, scale=scale,
+            router=w["router"], gate=w["gate"], up=w["up"], down=w["down"],
+            shared_gate=w["shared_gate"], shared_up=w["shared_up"],
+            shared_down=w["shared_down"])
+        cfg = um.config(shape["hidden"], shape["inter"], shape["experts"], shape["shared"], top_k,
+                        normalize=normalize, scale=scale)
+        self.layer = um.MoeLayer(ctx, cfg, w, um.MEMORY_HOST)
+        if quant != orc.QUANT_NONE:
+            q = syn.int8_overlay(seed=seed + 1, **shape)
+            self.orc.quant_mode = quant
+            self.orc.q = q
+            self.layer.attach_int8(ctx, q, um.MEMORY_HOST, quant)
+
+    def run(self, ctx, x, flags=0):
+        T = x.shape[0]
+        E, K = self.shape["experts"], self.top_k
+        tr = {"logits": torch.zeros((T, E), device="cuda"),
+              "topk_ids": torch.zeros((T, K), dtype=torch.int32, device="cuda"),
+              "topk_weights": torch.zeros((T, K), device="cuda"),
+              "expert_offsets": torch.zeros(E + 1, dtype=torch.int32, device="cuda"),
+              "perm_rows": torch.zeros(T * K, dtype=torch.int32, device="cuda"),
+              "perm_weights": torch.zeros(T * K, device="cuda")}
+        xd = dev(x)
+        yd = torch.full_like(xd, float("nan"))
+        torch.cuda.synchronize()
+        um.forward(ctx, self.layer, xd, yd, flags=flags, trace=tr)
+        torch.cuda.synchronize()
+        return yd.cpu().numpy(), {k: v.cpu().numpy() for k, v in tr.items()}
+
+
+def tie_tokens(ref_tr, gpu_tr, K):
+    """Tokens whose selected set differs; asserts each is a tie within 1e-6."""
+    bad = []
+    for t in range(ref_tr.topk_ids.shape[0]):
+        a, b = set(ref_tr.topk_ids[t].tolist()), set(gpu_tr["topk_ids"][t].tolist())
+        if a == b:
+            continue
+        lg = ref_tr.logits[t]
+        kth = np.sort(lg)[::-1][K - 1]
+        for e in a ^ b:
+            assert abs(float(lg[e]) - float(kth)) <= TIE, (t, e, lg[e], kth)
+        bad.append(t)
+    return bad
+
+
+def normwise(a, b):
+    num = np.abs(a - b).max(axis=1)
+    den = np.maximum(np.abs(b).max(axis=1), 1e-30)
+    return float((num / den).max())
+
+
+def check_layer(case, ctx, x, tol=FP32_TOL, flags=0):
+    y, tr = case.run(ctx, x, flags)
+    ref, rtr = orc.moe_experts(case.orc, x, trace=True)
+    K = case.top_k
+    ties = tie_tokens(rtr, tr, K)
+    keep = np.setdiff1d(np.arange(x.shape[0]), ties)
+    # Routing weights of agreeing tokens: same probabilities up to exp/sum rounding.
+    np.testing.assert_allclose(tr["topk_weights"][keep], rtr.topk_weights[keep], rtol=2e-5,
+                               atol=1e-7)
+    assert np.array_equal(tr["topk_ids"][keep], rtr.topk_ids[keep])
+    if not ties:
+        assert np.array_equal(tr["expert_offsets"], rtr.expert_offsets)
+        assert np.array_equal(tr["perm_rows"], rtr.perm_rows)
+    assert np.all(np.isfinite(y))
+    err = normwise(y[keep], ref[keep])
+    say(f"  T={x.shape[0]} ties={len(ties)} normwise={err:.3e}")
+    assert err <= tol, err
+    return y
+
+
+# ---------------------------------------------------------------- operators
+
+def test_route_kat(ctx):
+    say("route KAT (tests/moe.rs:4-13)")
+    logits = dev(np.zeros((1, 4), np.float32))
+    ids = torch.zeros((1, 2), dtype=torch.int32, device="cuda")
+    w = torch.zeros((1, 2), device="cuda")
+    um.route(ctx, logits, 2, False, 1.0, ids, w)
+    assert ids.cpu().tolist() == [[0, 1]] and w.cpu().tolist() == [[0.25, 0.25]]
+    um.route(ctx, logits, 2, True, 2.0, ids, w)
+    assert ids.cpu().tolist() == [[0, 1]] and w.cpu().tolist() == [[1.0, 1.0]]
+    with pytest.raises(um.UocrError) as e:
+        um.route(ctx, dev(np.array([[0.0, np.nan]], np.float32)), 1, False, 1.0, ids, w)
+    assert e.value.status == um.NUMERICAL
+    with pytest.raises(um.UocrError) as e:
+        um.route(ctx, dev(np.zeros((1, 1), np.float32)), 2, False, 1.0, ids, w)
+    assert e.value.status == um.SHAPE
+
+
+def test_route_matches_oracle_on_random_rows(ctx):
+    say("route vs oracle, 512 rows of 64 logits")
+    rng = np.random.default_rng(1)
+    lg = (rng.standard_normal((512, 64)) * 0.7).astype(np.float32)
+    lg[7, :] = 0.0  # all tied: ids 0..5
+    ids = torch.zeros((512, 6), dtype=torch.int32, device="cuda")
+    w = torch.zeros((512, 6), device="cuda")
+    um.route(ctx, dev(lg), 6, True, 1.0, ids, w)
+    gi, gw = ids.cpu().numpy(), w.cpu().numpy()
+    for t in range(512):
+        ri, rw = orc.route_arrays(lg[t], 6, True, 1.0)
+        assert np.array_equal(gi[t], ri), t
+        np.testing.assert_allclose(gw[t], rw, rtol=2e-6)
+
+
+def test_linear_kats(ctx):
+    say("linear KAT (tests/ops.rs:23-33 without bias) and BF16 tails (tests/weights.rs:9-50)")
+    x = dev(np.array([[1, 2, 3], [-1, 0, 2]], np.float32))
+    wb = dev(orc.f32_to_bf16(np.array([[1, 0, -1], [2, 1, 0]], np.float32)).view(np.int16))
+    y = torch.zeros((2, 2), device="cuda")
+    um.linear_bf16(ctx, x, wb, y)
+    assert y.cpu().numpy().ravel().tolist() == [-2.0, 4.0, -1.0, -2.0]
+    for rows, cols in [(37, 131), (1025, 131), (96, 1280), (7, 64)]:
+        w = np.array([((i % 29) - 14) / 16 for i in range(rows * cols)], np.float32)
+        w = w.reshape(rows, cols)
+        for batch in [1, 3, 20]:
+            xs = np.array([((i % 13) - 6) / 8 for i in range(batch * cols)], np.float32)
+            xs = xs.reshape(batch, cols)
+            want = orc.linear(xs, w)
+            yd = torch.zeros((batch, rows), device="cuda")
+            um.linear_bf16(ctx, dev(xs), dev(orc.f32_to_bf16(w).view(np.int16)), yd)
+            assert np.all(np.abs(yd.cpu().numpy() - want) < 1e-5), (rows, cols, batch)
+
+
+def test_int8_linear_matches_f64(ctx):
+    say("INT8 weight-only linear (tests/quantized.rs:31-73)")
+    for cols in [1, 31, 32, 33, 131, 513, 64, 1280]:
+        rows = 257 if cols == 513 else 7
+        vals = np.sin(np.arange(rows * cols, dtype=np.float32) * np.float32(0.37)) * 3
+        vals = vals.astype(np.float32).reshape(rows, cols)
+        vals[0] = 0
+        q, s = orc.int8_quantize(vals)
+        restored = orc.int8_dequantize(q, s)
+        for batch in [1, 3]:
+            x = np.cos(np.arange(batch * cols, dtype=np.float32) * np.float32(0.13))
+            x = x.astype(np.float32).reshape(batch, cols)
+            want = x.astype(np.float64) @ restored.astype(np.float64).T
+            yd = torch.zeros((batch, rows), device="cuda")
+            um.int8_linear(ctx, dev(q), dev(s), dev(x), yd)
+            assert np.all(np.abs(yd.cpu().numpy() - want) < 2e-5), (cols, batch)
+
+
+def test_dynamic_int8_block_sums_bit_exact(ctx):
+    say("W8A8 block sums bit-exact, outputs (tests/quantized.rs:89-120)")
+    for cols in [1, 15, 31, 32, 33, 131, 1280, 64, 896, 1792]:
+        rows = 129 if cols >= 64 else 9
+        m = np.sin(np.arange(rows * cols, dtype=np.float32) * np.float32(0.41))
+        q, s = orc.int8_quantize(m.astype(np.float32).reshape(rows, cols))
+        x = (np.cos(np.arange(cols, dtype=np.float32) * np.float32(0.17)) * 2).astype(np.float32)
+        ry, rsums = orc.int8_linear_dynamic(q, s, x.reshape(1, cols), with_block_sums=True)
+        yd = torch.zeros((1, rows), device="cuda")
+        sums = torch.zeros(rsums.shape, dtype=torch.int32, device="cuda")
+        um.int8_linear_dynamic(ctx, dev(q), dev(s), dev(x.reshape(1, cols)), yd, sums)
+        assert np.array_equal(sums.cpu().numpy(), rsums), cols
+        assert np.all(np.abs(yd.cpu().numpy() - ry) < 2e-4), cols
+    with pytest.raises(um.UocrError) as e:
+        bad = np.zeros((1, 64), np.float32)
+        bad[0, 5] = np.inf
+        um.int8_linear_dynamic(ctx, dev(np.zeros((2, 64), np.int8)),
+                               dev(np.ones((2, 2), np.float32)), dev(bad),
+                               torch.zeros((1, 2), device="cuda"))
+    assert e.value.status == um.NUMERICAL
+
+
+def test_rms_norm_kat(ctx):
+    say("RMSNorm KAT (tests/ops.rs:55-64)")
+    out = torch.zeros((1, 2), device="cuda")
+    um.rms_norm(ctx, dev(np.array([[1.0, 3.0]], np.float32)), dev(np.ones(2, np.float32)), 1e-6,
+                out)
+    o = out.cpu().numpy().ravel()
+    assert abs(o[0] - 0.44721355) < 1e-6 and abs(o[1] - 1.3416406) < 1e-6
+    x = syn.activations(5, 1280, seed=3)
+    w = np.linspace(0.5, 1.5, 1280).astype(np.float32)
+    out = torch.zeros((5, 1280), device="cuda")
+    um.rms_norm(ctx, dev(x), dev(w), 1e-6, out)
+    assert normwise(out.cpu().numpy(), orc.rms_norm(x, w, 1e-6)) < 1e-6
+
+
+# -------------------------------------------------------------- MoE layer
+
+@pytest.mark.parametrize("T", [1, 2, 7, 16, 33, 100])
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY, orc.QUANT_DYNAMIC])
+def test_small_layer(ctx, T, quant):
+    say(f"small layer T={T} quant={quant}")
+    case = Case(ctx, SMALL, 4, seed=20 + T, quant=quant, normalize=(T % 2 == 0), scale=1.25)
+    check_layer(case, ctx, syn.activations(T, SMALL["hidden"], seed=T))
+
+
+@pytest.fixture(scope="module")
+def full_bf16(ctx):
+    return Case(ctx, FULL, 6, seed=0)
+
+
+@pytest.fixture(scope="module")
+def full_int8(ctx):
+    return Case(ctx, FULL, 6, seed=0, quant=orc.QUANT_WEIGHTS_ONLY)
+
+
+@pytest.fixture(scope="module")
+def full_dynamic(ctx):
+    return Case(ctx, FULL, 6, seed=0, quant=orc.QUANT_DYNAMIC)
+
+
+@pytest.mark.parametrize("T", [1, 4, 64])
+def test_full_bf16(ctx, full_bf16, T):
+    say(f"full BF16 layer T={T}")
+    check_layer(full_bf16, ctx, syn.activations(T, 1280, seed=100 + T))
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_full_int8_weights_only(ctx, full_int8, T):
+    say(f"full INT8 weight-only layer T={T}")
+    check_layer(full_int8, ctx, syn.activations(T, 1280, seed=200 + T))
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_full_dynamic(ctx, full_dynamic, T):
+    say(f"full W8A8 layer T={T}")
+    check_layer(full_dynamic, ctx, syn.activations(T, 1280, seed=300 + T))
+
+
+def test_deterministic_and_row_independent(ctx, full_bf16):
+    say("determinism and row independence, T=256")
+    x = syn.activations(256, 1280, seed=7)
+    y1, _ = full_bf16.run(ctx, x)
+    y2, _ = full_bf16.run(ctx, x)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    rows = [0, 17, 255]
+    ref = orc.moe_experts(full_bf16.orc, x[rows])
+    assert normwise(y1[rows], ref) <= FP32_TOL
+
+
+def test_layer_errors(ctx):
+    say("layer errors: non-finite input, scratch budget, overlay")
+    case = Case(ctx, SMALL, 4, seed=5)
+    x = syn.activations(3, SMALL["hidden"], seed=6)
+    x[1, 2] = np.nan
+    with pytest.raises(um.UocrError) as e:
+        case.run(ctx, x)
+    assert e.value.status == um.NUMERICAL
+    # The context recovers after the error.
+    case.run(ctx, syn.activations(3, SMALL["hidden"], seed=6))
+    tiny = um.Context(0, 4096)
+    xd = dev(syn.activations(64, SMALL["hidden"], seed=6))
+    with pytest.raises(um.UocrError) as e:
+        um.forward(tiny, case.layer, xd, torch.empty_like(xd))
+    assert e.value.status == um.RESOURCE
+    tiny.close()
+    with pytest.raises(um.UocrError) as e:
+        case.layer.attach_int8(ctx, {}, um.MEMORY_HOST, um.QUANT_DYNAMIC)
+    assert e.value.status == um.FORMAT
+    q = syn.int8_overlay(seed=9, **SMALL)
+    qb = dict(q)
+    g, s = q["gate"]
+    g = g.copy()
+    g[0, 0, 0] = -128
+    qb["gate"] = (g, s)
+    with pytest.raises(um.UocrError) as e:
+        case.layer.attach_int8(ctx, qb, um.MEMORY_HOST, um.QUANT_WEIGHTS_ONLY)
+    assert e.value.status == um.FORMAT
+    assert case.layer.precision == "bf16_weights_fp32"

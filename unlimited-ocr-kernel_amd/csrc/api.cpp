@@ -1,0 +1,622 @@
+// C-ABI implementation: context, layer upload/repack, forward orchestration.
+//
+// The layer handle replaces what Decoder::experts reads through projection()
+// (src/decoder/mod.rs:99-220): the router, the routed experts and the fused
+// shared expert, BF16 or INT8 block-32. The context mirrors CpuContext
+// (src/cpu/mod.rs:18-79): a device, a stream and a scratch budget.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/uocr_moe.h"
+#include "moe_kernels.hpp"
+
+using uocr::DeviceLayer;
+using uocr::Scratch;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  int status = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? UOCR_ERR_RESOURCE
+               : (e == hipErrorInvalidDevice || e == hipErrorNoDevice ||
+                  e == hipErrorNoBinaryForGpu)
+                   ? UOCR_ERR_UNSUPPORTED
+                   : UOCR_ERR_RESOURCE;
+  return fail(status, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                   \
+  do {                                        \
+    hipError_t _e = (expr);                   \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+std::once_flag g_attr_once;
+
+}  // namespace
+
+struct uocr_gpu_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  char* scratch = nullptr;
+  size_t scratch_limit = 0;
+  int* err = nullptr;       // device error flag
+  int* err_host = nullptr;  // pinned readback
+};
+
+struct uocr_moe_layer {
+  uocr_moe_config cfg{};
+  DeviceLayer dev{};
+  int device = 0;
+  int quant_mode = UOCR_QUANT_NONE;
+  std::vector<void*> allocations;
+  size_t bytes = 0;
+};
+
+namespace {
+
+struct ScratchPlan {
+  size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, h, hs, y, ys, xn,
+      qrow, total;
+};
+
+ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
+  const size_t E = c.n_routed_experts, K = c.num_experts_per_tok, H = c.hidden_size;
+  const size_t I = c.moe_intermediate_size, S = I * c.n_shared_experts;
+  ScratchPlan p{};
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    size_t here = at;
+    at += align256(bytes ? bytes : 1);
+    return here;
+  };
+  p.logits = take(T * E * 4);
+  p.ids = take(T * K * 4);
+  p.w = take(T * K * 4);
+  p.offsets = take((E + 1) * 4);
+  p.perm_rows = take(T * K * 4);
+  p.perm_w = take(T * K * 4);
+  p.inv_pos = take(T * K * 4);
+  // Worst tile count over both engines (one-row tiles for decode).
+  p.tiles = take((size_t)uocr::max_tiles((int)T, (int)K, (int)E, 1) * 2 * 4);
+  p.counters = take(16);
+  p.h = take(T * K * I * 4);
+  p.hs = take(T * S * 4);
+  p.y = take(T * K * H * 4);
+  p.ys = take(T * H * 4);
+  p.xn = take(T * H * 4);
+  p.qrow = take(0);
+  p.total = at;
+  return p;
+}
+
+Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
+  Scratch s{};
+  char* b = ctx->scratch;
+  s.logits = reinterpret_cast<float*>(b + p.logits);
+  s.topk_ids = reinterpret_cast<int*>(b + p.ids);
+  s.topk_w = reinterpret_cast<float*>(b + p.w);
+  s.offsets = reinterpret_cast<int*>(b + p.offsets);
+  s.perm_rows = reinterpret_cast<int*>(b + p.perm_rows);
+  s.perm_w = reinterpret_cast<float*>(b + p.perm_w);
+  s.inv_pos = reinterpret_cast<int*>(b + p.inv_pos);
+  s.tiles = reinterpret_cast<int*>(b + p.tiles);
+  s.counters = reinterpret_cast<int*>(b + p.counters);
+  s.h = reinterpret_cast<float*>(b + p.h);
+  s.hs = reinterpret_cast<float*>(b + p.hs);
+  s.y = reinterpret_cast<float*>(b + p.y);
+  s.ys = reinterpret_cast<float*>(b + p.ys);
+  s.xn = reinterpret_cast<float*>(b + p.xn);
+  s.err = ctx->err;
+  return s;
+}
+
+int validate_config(const uocr_moe_config* c) {
+  if (!c) return fail(UOCR_ERR_SHAPE, "missing config");
+  // ModelConfig::from_json (src/model/config.rs:88-111) for the MoE fields.
+  if (c->hidden_size == 0 || c->moe_intermediate_size == 0 || c->n_shared_experts == 0 ||
+      c->num_experts_per_tok == 0 || c->num_experts_per_tok > c->n_routed_experts ||
+      !std::isfinite(c->rms_norm_eps) || c->rms_norm_eps <= 0.f ||
+      !std::isfinite(c->routed_scaling_factor) || c->routed_scaling_factor <= 0.f)
+    return fail(UOCR_ERR_SHAPE, "invalid decoder configuration");
+  if (c->hidden_size % 64 || c->moe_intermediate_size % 64 || c->n_routed_experts > 64 ||
+      c->num_experts_per_tok > 8)
+    return fail(UOCR_ERR_UNSUPPORTED,
+                "GPU layer needs hidden and intermediate sizes that are multiples of 64, "
+                "<= 64 experts and <= 8 experts per token");
+  return UOCR_OK;
+}
+
+hipMemcpyKind kind_of(uocr_memory where) {
+  return where == UOCR_MEMORY_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+}
+
+// Gate/up rows interleaved in blocks of 32: destination rows
+// [64b, 64b+32) <- gate [32b, 32b+32), [64b+32, 64b+64) <- up.
+int upload_interleaved(char* dst, const void* gate, const void* up, size_t rows, size_t row_bytes,
+                       hipMemcpyKind kind, hipStream_t s) {
+  const size_t blk = 32 * row_bytes;
+  HIP_TRY(hipMemcpy2DAsync(dst, 2 * blk, gate, blk, blk, rows / 32, kind, s), "upload gate");
+  HIP_TRY(hipMemcpy2DAsync(dst + blk, 2 * blk, up, blk, blk, rows / 32, kind, s), "upload up");
+  return UOCR_OK;
+}
+
+__global__ void widen_bf16_kernel(const uint16_t* in, float* out, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = __uint_as_float((uint32_t)in[i] << 16);
+}
+
+// Int8Matrix::from_parts / QuantizedWeights::load value rules
+// (src/cpu/quantized.rs:31-35, 351): byte 0x80 (-128) is rejected as
+// Format, non-finite or negative scales as Numerical.
+__global__ void check_int8_kernel(const int8_t* q, size_t nq, const float* s, size_t ns,
+                                  int* flag) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nq; i += stride)
+    if (q[i] == -128) atomicMax(flag, UOCR_ERR_FORMAT);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ns; i += stride)
+    if (!isfinite(s[i]) || s[i] < 0.f) atomicMax(flag, UOCR_ERR_NUMERICAL);
+}
+
+int read_and_clear_error(uocr_gpu_ctx* ctx) {
+  HIP_TRY(hipMemcpyAsync(ctx->err_host, ctx->err, sizeof(int), hipMemcpyDeviceToHost,
+                         ctx->stream),
+          "read device error flag");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
+  int e = *ctx->err_host;
+  if (e != 0) {
+    HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), ctx->stream), "clear device error flag");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
+    return fail(e, e == UOCR_ERR_NUMERICAL ? "nonfinite numerical input on device"
+                                            : "device reported an error");
+  }
+  return UOCR_OK;
+}
+
+int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
+                    const float* residual, float* y, uint32_t flags,
+                    const uocr_moe_trace* trace, bool x_in_scratch) {
+  const uocr_moe_config& c = layer->cfg;
+  const ScratchPlan plan = plan_scratch(c, T);
+  if (plan.total > ctx->scratch_limit)
+    return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit (%zu > %zu bytes)",
+                plan.total, ctx->scratch_limit);
+  Scratch S = carve(ctx, plan);
+  if (!x_in_scratch) S.xn = const_cast<float*>(x);
+  const DeviceLayer& L = layer->dev;
+  const int Ti = (int)T;
+  hipStream_t st = ctx->stream;
+  uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
+  uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w, S.err,
+                    st);
+  const bool gemv = true;  // the MFMA engine is selected here once available
+  (void)flags;
+  const int bm = gemv ? (T == 1 ? 1 : uocr::kGemvChunk) : uocr::kMfmaBM;
+  uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows, S.perm_w,
+                        S.inv_pos, S.tiles, S.counters, st);
+  const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
+  if (tiles_bound > 65535)
+    return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
+  uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+  uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, st);
+  uocr::launch_combine(S, residual, Ti, L.H, L.K, y, st);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  if (trace) {
+    const size_t TK = T * L.K;
+    auto copy = [&](void* dst, const void* src, size_t bytes) -> int {
+      if (dst) HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st), "trace copy");
+      return UOCR_OK;
+    };
+    int r;
+    if ((r = copy(trace->logits, S.logits, T * L.E * 4))) return r;
+    if ((r = copy(trace->topk_ids, S.topk_ids, TK * 4))) return r;
+    if ((r = copy(trace->topk_weights, S.topk_w, TK * 4))) return r;
+    if ((r = copy(trace->expert_offsets, S.offsets, (L.E + 1) * 4))) return r;
+    if ((r = copy(trace->perm_rows, S.perm_rows, TK * 4))) return r;
+    if ((r = copy(trace->perm_weights, S.perm_w, TK * 4))) return r;
+  }
+  return UOCR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
+  if (!out) return fail(UOCR_ERR_SHAPE, "null output handle");
+  *out = nullptr;
+  if (scratch_limit == 0) return fail(UOCR_ERR_RESOURCE, "scratch limit must be nonzero");
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n), "device count");
+  if (device < 0 || device >= n) return fail(UOCR_ERR_UNSUPPORTED, "no GPU device %d", device);
+  HIP_TRY(hipSetDevice(device), "set device");
+  std::call_once(g_attr_once, [] { uocr::gemv_init_attributes(); });
+  auto* ctx = new uocr_gpu_ctx();
+  ctx->device = device;
+  ctx->scratch_limit = scratch_limit;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&ctx->scratch, scratch_limit);
+  if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
+  if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
+  if (e != hipSuccess) {
+    uocr_gpu_ctx_destroy(ctx);
+    return hip_fail(e, "context allocation");
+  }
+  *out = ctx;
+  return UOCR_OK;
+}
+
+void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->err) (void)hipFree(ctx->err);
+  if (ctx->err_host) (void)hipHostFree(ctx->err_host);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+void* uocr_gpu_ctx_stream(uocr_gpu_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int uocr_gpu_ctx_synchronize(uocr_gpu_ctx* ctx) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  return read_and_clear_error(ctx);
+}
+
+const char* uocr_last_error(const uocr_gpu_ctx* ctx) {
+  (void)ctx;
+  return g_last_error.c_str();
+}
+
+size_t uocr_moe_scratch_bytes(const uocr_moe_config* cfg, size_t T) {
+  if (!cfg) return 0;
+  return plan_scratch(*cfg, T).total;
+}
+
+int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
+                          const uocr_moe_bf16_weights* w, uocr_memory where,
+                          uocr_moe_layer** out) {
+  if (!out) return fail(UOCR_ERR_SHAPE, "null output handle");
+  *out = nullptr;
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  int r = validate_config(cfg);
+  if (r) return r;
+  if (!w || !w->router || !w->expert_gate || !w->expert_up || !w->expert_down ||
+      !w->shared_gate || !w->shared_up || !w->shared_down)
+    return fail(UOCR_ERR_FORMAT, "missing MoE weight tensor");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  auto* layer = new uocr_moe_layer();
+  layer->cfg = *cfg;
+  layer->device = ctx->device;
+  DeviceLayer& L = layer->dev;
+  L.H = (int)cfg->hidden_size;
+  L.I = (int)cfg->moe_intermediate_size;
+  L.S = L.I * (int)cfg->n_shared_experts;
+  L.E = (int)cfg->n_routed_experts;
+  L.K = (int)cfg->num_experts_per_tok;
+  L.normalize = cfg->norm_topk_prob ? 1 : 0;
+  L.scale = cfg->routed_scaling_factor;
+  L.eps = cfg->rms_norm_eps;
+  L.quant_mode = UOCR_QUANT_NONE;
+  const size_t H = L.H, I = L.I, S = L.S, E = L.E;
+  const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
+  auto alloc = [&](size_t bytes, void** p) -> hipError_t {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) {
+      layer->allocations.push_back(*p);
+      layer->bytes += bytes;
+    }
+    return e;
+  };
+  void *router = nullptr, *w13 = nullptr, *w2 = nullptr, *norm = nullptr;
+  hipError_t e = alloc(E * H * 2, &router);
+  if (e == hipSuccess) e = alloc(n13 * 2, &w13);
+  if (e == hipSuccess) e = alloc(n2 * 2, &w2);
+  if (e == hipSuccess) e = alloc(H * 4, &norm);
+  if (e != hipSuccess) {
+    uocr_moe_layer_destroy(layer);
+    return hip_fail(e, "layer allocation");
+  }
+  const hipMemcpyKind kind = kind_of(where);
+  hipStream_t st = ctx->stream;
+  auto finish = [&](int status) {
+    if (status) uocr_moe_layer_destroy(layer);
+    return status;
+  };
+  if ((e = hipMemcpyAsync(router, w->router, E * H * 2, kind, st)) != hipSuccess)
+    return finish(hip_fail(e, "upload router"));
+  char* d13 = static_cast<char*>(w13);
+  for (size_t g = 0; g < E; g++) {
+    r = upload_interleaved(d13 + g * 2 * I * H * 2, w->expert_gate + g * I * H,
+                           w->expert_up + g * I * H, I, H * 2, kind, st);
+    if (r) return finish(r);
+  }
+  r = upload_interleaved(d13 + E * 2 * I * H * 2, w->shared_gate, w->shared_up, S, H * 2, kind,
+                         st);
+  if (r) return finish(r);
+  if ((e = hipMemcpyAsync(w2, w->expert_down, E * H * I * 2, kind, st)) != hipSuccess)
+    return finish(hip_fail(e, "upload down"));
+  if ((e = hipMemcpyAsync(static_cast<char*>(w2) + E * H * I * 2, w->shared_down, H * S * 2, kind,
+                          st)) != hipSuccess)
+    return finish(hip_fail(e, "upload shared down"));
+  if (w->norm_weight) {
+    void* tmp = nullptr;
+    if ((e = hipMalloc(&tmp, H * 2)) != hipSuccess) return finish(hip_fail(e, "norm staging"));
+    e = hipMemcpyAsync(tmp, w->norm_weight, H * 2, kind, st);
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(widen_bf16_kernel, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, st,
+                         (const uint16_t*)tmp, (float*)norm, (int)H);
+      e = hipStreamSynchronize(st);
+    }
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return finish(hip_fail(e, "upload norm"));
+    L.norm_w = static_cast<const float*>(norm);
+  } else {
+    L.norm_w = nullptr;
+  }
+  if ((e = hipStreamSynchronize(st)) != hipSuccess) return finish(hip_fail(e, "upload"));
+  L.router = static_cast<const uint16_t*>(router);
+  L.w13 = static_cast<const uint16_t*>(w13);
+  L.w2 = static_cast<const uint16_t*>(w2);
+  *out = layer;
+  return UOCR_OK;
+}
+
+int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
+                               const uocr_moe_int8_weights* w, uocr_memory where,
+                               uocr_quant_mode mode) {
+  if (!ctx || !layer) return fail(UOCR_ERR_SHAPE, "null handle");
+  if (mode != UOCR_QUANT_WEIGHTS_ONLY && mode != UOCR_QUANT_DYNAMIC_ACTIVATIONS) {
+    if (mode == UOCR_QUANT_NONE && !w) {
+      layer->quant_mode = UOCR_QUANT_NONE;
+      layer->dev.quant_mode = UOCR_QUANT_NONE;
+      return UOCR_OK;
+    }
+    return fail(UOCR_ERR_UNSUPPORTED, "unknown quantization mode");
+  }
+  if (!w || !w->expert_gate || !w->expert_up || !w->expert_down || !w->shared_gate ||
+      !w->shared_up || !w->shared_down || !w->expert_gate_scales || !w->expert_up_scales ||
+      !w->expert_down_scales || !w->shared_gate_scales || !w->shared_up_scales ||
+      !w->shared_down_scales)
+    return fail(UOCR_ERR_FORMAT, "dynamic INT8 requires a quantized weight overlay");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  DeviceLayer& L = layer->dev;
+  const size_t H = L.H, I = L.I, S = L.S, E = L.E;
+  const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
+  void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr;
+  std::vector<void*> fresh;
+  auto alloc = [&](size_t bytes, void** p) -> hipError_t {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) fresh.push_back(*p);
+    return e;
+  };
+  auto release = [&](int status) {
+    for (void* p : fresh) (void)hipFree(p);
+    return status;
+  };
+  hipError_t e = alloc(n13, &q13);
+  if (e == hipSuccess) e = alloc(n13 / 32 * 4, &s13);
+  if (e == hipSuccess) e = alloc(n2, &q2);
+  if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2);
+  if (e != hipSuccess) return release(hip_fail(e, "INT8 allocation"));
+  const hipMemcpyKind kind = kind_of(where);
+  hipStream_t st = ctx->stream;
+  char* dq = static_cast<char*>(q13);
+  char* ds = static_cast<char*>(s13);
+  int r;
+  for (size_t g = 0; g < E; g++) {
+    if ((r = upload_interleaved(dq + g * 2 * I * H, w->expert_gate + g * I * H,
+                                w->expert_up + g * I * H, I, H, kind, st)))
+      return release(r);
+    if ((r = upload_interleaved(ds + g * 2 * I * (H / 32) * 4,
+                                w->expert_gate_scales + g * I * (H / 32),
+                                w->expert_up_scales + g * I * (H / 32), I, (H / 32) * 4, kind,
+                                st)))
+      return release(r);
+  }
+  if ((r = upload_interleaved(dq + E * 2 * I * H, w->shared_gate, w->shared_up, S, H, kind, st)))
+    return release(r);
+  if ((r = upload_interleaved(ds + E * 2 * I * (H / 32) * 4, w->shared_gate_scales,
+                              w->shared_up_scales, S, (H / 32) * 4, kind, st)))
+    return release(r);
+  if ((e = hipMemcpyAsync(q2, w->expert_down, E * H * I, kind, st)) != hipSuccess ||
+      (e = hipMemcpyAsync(static_cast<char*>(q2) + E * H * I, w->shared_down, H * S, kind, st)) !=
+          hipSuccess ||
+      (e = hipMemcpyAsync(s2, w->expert_down_scales, E * H * (I / 32) * 4, kind, st)) !=
+          hipSuccess ||
+      (e = hipMemcpyAsync(static_cast<char*>(s2) + E * H * (I / 32) * 4, w->shared_down_scales,
+                          H * (S / 32) * 4, kind, st)) != hipSuccess)
+    return release(hip_fail(e, "upload INT8 down"));
+  // Validate the uploaded values on the device.
+  HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), st), "clear flag");
+  hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q13, n13,
+                     (const float*)s13, n13 / 32, ctx->err);
+  hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q2, n2,
+                     (const float*)s2, n2 / 32, ctx->err);
+  r = read_and_clear_error(ctx);
+  if (r) {
+    return release(fail(r, r == UOCR_ERR_FORMAT ? "invalid INT8 matrix (byte 128)"
+                                                 : "INT8 scales must be finite and nonnegative"));
+  }
+  // Replace any previous overlay.
+  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2}) {
+    if (!p) continue;
+    for (auto it = layer->allocations.begin(); it != layer->allocations.end(); ++it)
+      if (*it == p) {
+        layer->allocations.erase(it);
+        break;
+      }
+    (void)hipFree(p);
+  }
+  for (void* p : fresh) layer->allocations.push_back(p);
+  layer->bytes += n13 + n13 / 32 * 4 + n2 + n2 / 32 * 4;
+  L.q13 = static_cast<const int8_t*>(q13);
+  L.s13 = static_cast<const float*>(s13);
+  L.q2 = static_cast<const int8_t*>(q2);
+  L.s2 = static_cast<const float*>(s2);
+  L.quant_mode = mode;
+  layer->quant_mode = mode;
+  return UOCR_OK;
+}
+
+const char* uocr_moe_layer_precision(const uocr_moe_layer* layer) {
+  if (!layer) return "";
+  switch (layer->quant_mode) {
+    case UOCR_QUANT_WEIGHTS_ONLY:
+      return "int8_weights_fp32";
+    case UOCR_QUANT_DYNAMIC_ACTIVATIONS:
+      return "int8_weights_dynamic_activations";
+    default:
+      return "bf16_weights_fp32";
+  }
+}
+
+size_t uocr_moe_layer_device_bytes(const uocr_moe_layer* layer) { return layer ? layer->bytes : 0; }
+
+void uocr_moe_layer_destroy(uocr_moe_layer* layer) {
+  if (!layer) return;
+  (void)hipSetDevice(layer->device);
+  for (void* p : layer->allocations) (void)hipFree(p);
+  delete layer;
+}
+
+int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x,
+                           size_t T, float* y, uint32_t flags, const uocr_moe_trace* trace) {
+  if (!ctx || !layer) return fail(UOCR_ERR_SHAPE, "null handle");
+  if (T == 0) return UOCR_OK;
+  if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
+  if (T > (size_t)(1 << 24)) return fail(UOCR_ERR_RESOURCE, "token count too large");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  return enqueue_experts(ctx, layer, x, T, nullptr, y, flags, trace, false);
+}
+
+int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
+                     float* y, uint32_t flags, const uocr_moe_trace* trace) {
+  int r = uocr_moe_forward_async(ctx, layer, x, T, y, flags, trace);
+  if (r) return r;
+  return read_and_clear_error(ctx);
+}
+
+int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const* layers,
+                                 size_t n_layers, const float* x, size_t T, float* y,
+                                 uint32_t flags) {
+  if (!ctx || (!layers && n_layers)) return fail(UOCR_ERR_SHAPE, "null handle");
+  if (T == 0 || n_layers == 0) return UOCR_OK;
+  if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  const float* cur = x;
+  for (size_t l = 0; l < n_layers; l++) {
+    const uocr_moe_layer* layer = layers[l];
+    if (!layer) return fail(UOCR_ERR_SHAPE, "null layer %zu", l);
+    if (!layer->dev.norm_w) return fail(UOCR_ERR_FORMAT, "layer %zu has no norm weight", l);
+    const ScratchPlan plan = plan_scratch(layer->cfg, T);
+    if (plan.total > ctx->scratch_limit)
+      return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
+    Scratch S = carve(ctx, plan);
+    uocr::launch_rms_norm(cur, (int)T, layer->dev.H, layer->dev.norm_w, layer->dev.eps, S.xn,
+                          S.err, ctx->stream);
+    int r = enqueue_experts(ctx, layer, S.xn, T, cur, y, flags, nullptr, true);
+    if (r) return r;
+    cur = y;
+  }
+  return UOCR_OK;
+}
+
+int uocr_moe_block_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* const* layers,
+                           size_t n_layers, const float* x, size_t T, float* y, uint32_t flags) {
+  int r = uocr_moe_block_forward_async(ctx, layers, n_layers, x, T, y, flags);
+  if (r) return r;
+  return read_and_clear_error(ctx);
+}
+
+int uocr_route(uocr_gpu_ctx* ctx, const float* logits, size_t T, size_t n, size_t count,
+               int normalize, float scale, int32_t* ids, float* weights) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  // moe::route argument rules (src/decoder/moe.rs:13-15).
+  if (count == 0 || count > n || !std::isfinite(scale) || scale <= 0.f)
+    return fail(UOCR_ERR_SHAPE, "invalid expert routing");
+  if (n > 64 || count > 64) return fail(UOCR_ERR_UNSUPPORTED, "GPU routing supports <= 64 logits");
+  if (T == 0) return UOCR_OK;
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  uocr::launch_topk(logits, (int)T, (int)n, (int)count, normalize, scale, ids, weights, ctx->err,
+                    ctx->stream);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return read_and_clear_error(ctx);
+}
+
+int uocr_linear_bf16(uocr_gpu_ctx* ctx, const float* x, size_t m, size_t k, const uint16_t* w,
+                     size_t n, float* y) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  if (k == 0 || n == 0) return fail(UOCR_ERR_SHAPE, "linear weight must be [out,in]");
+  if (m == 0) return UOCR_OK;
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  uocr::launch_linear_bf16(x, (int)m, (int)k, w, (int)n, y, ctx->stream);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return read_and_clear_error(ctx);
+}
+
+int uocr_int8_linear(uocr_gpu_ctx* ctx, const int8_t* q, const float* scales, size_t rows,
+                     size_t cols, const float* x, size_t batch, float* y) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  if (rows == 0 || cols == 0) return fail(UOCR_ERR_SHAPE, "INT8 matrix storage");
+  if (batch == 0) return UOCR_OK;
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  uocr::launch_int8_linear(q, scales, (int)rows, (int)cols, x, (int)batch, y, ctx->stream);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return read_and_clear_error(ctx);
+}
+
+int uocr_int8_linear_dynamic(uocr_gpu_ctx* ctx, const int8_t* q, const float* scales,
+                             size_t rows, size_t cols, const float* x, float* y,
+                             int32_t* block_sums) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  if (rows == 0 || cols == 0) return fail(UOCR_ERR_SHAPE, "INT8 matrix storage");
+  const size_t blocks = (cols + 31) / 32;
+  // src/cpu/quantized.rs:162-168 scratch: the quantised row and its scales.
+  if (align256(cols) + blocks * 4 > ctx->scratch_limit)
+    return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  int8_t* xq = reinterpret_cast<int8_t*>(ctx->scratch);
+  float* xs = reinterpret_cast<float*>(ctx->scratch + align256(cols));
+  uocr::launch_int8_dynamic(q, scales, (int)rows, (int)cols, x, y, block_sums, xq, xs, ctx->err,
+                            ctx->stream);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return read_and_clear_error(ctx);
+}
+
+int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
+                  const float* weight, float eps, float* out) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  if (width == 0 || !std::isfinite(eps) || eps <= 0.f)
+    return fail(UOCR_ERR_SHAPE, "invalid normalization parameters");
+  if (rows == 0) return UOCR_OK;
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  uocr::launch_rms_norm(x, (int)rows, (int)width, weight, eps, out, ctx->err, ctx->stream);
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return read_and_clear_error(ctx);
+}
+
+}  // extern "C"

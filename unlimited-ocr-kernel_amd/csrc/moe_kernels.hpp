@@ -1,0 +1,99 @@
+// Internal interface between the C-ABI layer (api.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace uocr {
+
+// Expert "groups": 0..E-1 are the routed experts, E is the fused shared
+// expert (width S = I * n_shared_experts).
+struct DeviceLayer {
+  int H, I, S, E, K;
+  int normalize;
+  float scale;
+  float eps;
+  int quant_mode;            // uocr_quant_mode
+  const uint16_t* router;    // [E,H] bf16
+  // BF16 expert weights. w13 holds per group [2W,H]: gate and up rows
+  // interleaved in blocks of 32 (gate j..j+31, then up j..j+31, ...).
+  // w2 holds per group the down matrix [H,W] unchanged.
+  const uint16_t* w13;
+  const uint16_t* w2;
+  // INT8 overlay with the same row order; scales [rows, cols/32].
+  const int8_t* q13;
+  const float* s13;
+  const int8_t* q2;
+  const float* s2;
+  const float* norm_w;       // [H] post-attention RMSNorm weight (f32)
+
+  __host__ __device__ int width(int g) const { return g < E ? I : S; }
+  __host__ __device__ size_t w13_offset(int g) const { return (size_t)g * 2 * I * H; }
+  __host__ __device__ size_t w2_offset(int g) const { return (size_t)g * H * I; }
+  __host__ __device__ size_t s13_offset(int g) const { return (size_t)g * 2 * I * (H / 32); }
+  __host__ __device__ size_t s2_offset(int g) const { return (size_t)g * H * (I / 32); }
+};
+
+// Per-forward device scratch carved from the context's reservation.
+struct Scratch {
+  float* logits;    // [T,E]
+  int* topk_ids;    // [T,K]
+  float* topk_w;    // [T,K]
+  int* offsets;     // [E+1] expert start in the dispatched order
+  int* perm_rows;   // [T*K] token of each assignment
+  float* perm_w;    // [T*K]
+  int* inv_pos;     // [T*K] position of (token, slot) in the dispatched order
+  int* tiles;       // [max_tiles*2] (group, first row) per row tile
+  int* counters;    // [4]: tile count
+  float* h;         // [T*K, I] routed hidden in dispatched order
+  float* hs;        // [T, S] shared hidden
+  float* y;         // [T*K, H] routed expert outputs in dispatched order
+  float* ys;        // [T, H] shared expert output
+  float* xn;        // [T, H] normalised block input
+  int* err;         // device error flag
+};
+
+int max_tiles(int T, int K, int E, int bm);
+
+// route.hip
+void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E, float* logits,
+                          hipStream_t s);
+void launch_topk(const float* logits, int T, int E, int K, int normalize, float scale, int* ids,
+                 float* weights, int* err, hipStream_t s);
+
+// dispatch.hip
+void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,
+                     int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
+                     hipStream_t s);
+
+// gemv.hip: row-chunk engine (FP32 math, INT8 weight-only and W8A8).
+void launch_gemv_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
+                        int mchunk, hipStream_t s);
+void launch_gemv_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
+                      hipStream_t s);
+// Operator entry points (single matrix).
+void launch_linear_bf16(const float* x, int m, int k, const uint16_t* w, int n, float* y,
+                        hipStream_t s);
+void launch_int8_linear(const int8_t* q, const float* sc, int rows, int cols, const float* x,
+                        int batch, float* y, hipStream_t s);
+void launch_int8_dynamic(const int8_t* q, const float* sc, int rows, int cols, const float* x,
+                         float* y, int32_t* block_sums, int8_t* xq, float* xs, int* err,
+                         hipStream_t s);
+void gemv_init_attributes();
+
+// gemm.hip: MFMA grouped GEMM engine.
+void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
+                        bool bf16_only, hipStream_t s);
+void launch_mfma_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
+                      bool bf16_only, hipStream_t s);
+constexpr int kMfmaBM = 128;
+constexpr int kGemvChunk = 16;
+
+// combine.hip
+void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
+                    hipStream_t s);
+void launch_rms_norm(const float* x, int rows, int width, const float* w, float eps, float* out,
+                     int* err, hipStream_t s);
+
+}  // namespace uocr

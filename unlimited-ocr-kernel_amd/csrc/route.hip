@@ -1,0 +1,176 @@
+// Router: gate logits (x . W_gate^T) and softmax top-k per token.
+//
+// Reference: Decoder::experts computes the logits with linear_weight
+// (src/decoder/mod.rs:126) and routes each row with moe::route
+// (src/decoder/moe.rs:7-30), whose softmax is ops::softmax
+// (src/cpu/ops.rs:139-187).
+#include "common.hpp"
+#include "moe_kernels.hpp"
+
+namespace uocr {
+
+// Few tokens: one wave per expert row streams that row once (coalesced
+// 256-byte loads of bf16 pairs) and dots it with every token.
+template <int TMAX>
+__global__ __launch_bounds__(256) void router_rows_kernel(const float* __restrict__ x,
+                                                          const uint16_t* __restrict__ w, int T,
+                                                          int H, int E,
+                                                          float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= E) return;
+  const uint32_t* row = reinterpret_cast<const uint32_t*>(w + (size_t)e * H);
+  const int pairs = H / 2;  // H is a multiple of 128
+  float acc[TMAX];
+#pragma unroll
+  for (int t = 0; t < TMAX; t++) acc[t] = 0.0f;
+  for (int p = lane; p < pairs; p += 64) {
+    uint32_t wp = row[p];
+    float w0 = bf16_lo(wp), w1 = bf16_hi(wp);
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+      if (t < T) {
+        float2 xv = reinterpret_cast<const float2*>(x + (size_t)t * H)[p];
+        acc[t] = fmaf(w0, xv.x, acc[t]);
+        acc[t] = fmaf(w1, xv.y, acc[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TMAX; t++) {
+    if (t < T) {
+      float s = wave_sum(acc[t]);
+      if (lane == 0) logits[(size_t)t * E + e] = s;
+    }
+  }
+}
+
+// Many tokens: lane = expert, a workgroup owns 16 tokens (4 per wave) and
+// stages K-chunks of the router (transposed, bf16 pairs) and of the token
+// rows in LDS.
+constexpr int kRouterKC = 256;  // K elements per chunk
+constexpr int kRouterTok = 16;  // tokens per workgroup
+
+__global__ __launch_bounds__(256) void router_tile_kernel(const float* __restrict__ x,
+                                                          const uint16_t* __restrict__ w, int T,
+                                                          int H, int E,
+                                                          float* __restrict__ logits) {
+  __shared__ uint32_t wl[(kRouterKC / 2) * 65];  // [k/2][expert], padded
+  __shared__ float xl[kRouterTok][kRouterKC];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int t0 = blockIdx.x * kRouterTok;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < H; k0 += kRouterKC) {
+    const int kc = min(kRouterKC, H - k0);  // a multiple of 64
+    // Router chunk: E rows x KC/2 pairs (zero past kc).
+    for (int i = tid; i < 64 * (kRouterKC / 2); i += 256) {
+      int e = i / (kRouterKC / 2), p = i % (kRouterKC / 2);
+      uint32_t v = 0;
+      if (e < E && 2 * p < kc) v = reinterpret_cast<const uint32_t*>(w + (size_t)e * H + k0)[p];
+      wl[p * 65 + e] = v;
+    }
+    for (int i = tid; i < kRouterTok * (kRouterKC / 4); i += 256) {
+      int t = i / (kRouterKC / 4), q = i % (kRouterKC / 4);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t0 + t < T && 4 * q < kc)
+        v = reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + k0)[q];
+      reinterpret_cast<float4*>(&xl[t][0])[q] = v;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int p = 0; p < kRouterKC / 2; p++) {
+      uint32_t wp = wl[p * 65 + lane];
+      float w0 = bf16_lo(wp), w1 = bf16_hi(wp);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float2 xv = *reinterpret_cast<const float2*>(&xl[wave * 4 + j][2 * p]);
+        acc[j] = fmaf(w0, xv.x, acc[j]);
+        acc[j] = fmaf(w1, xv.y, acc[j]);
+      }
+    }
+    __syncthreads();
+  }
+  if (lane < E) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int t = t0 + wave * 4 + j;
+      if (t < T) logits[(size_t)t * E + lane] = acc[j];
+    }
+  }
+}
+
+void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E, float* logits,
+                          hipStream_t s) {
+  if (T <= 0) return;
+  if (T <= 4) {
+    hipLaunchKernelGGL(router_rows_kernel<4>, dim3((E + 3) / 4), dim3(256), 0, s, x, w, T, H, E,
+                       logits);
+  } else if (T <= 16) {
+    hipLaunchKernelGGL(router_rows_kernel<16>, dim3((E + 3) / 4), dim3(256), 0, s, x, w, T, H, E,
+                       logits);
+  } else {
+    hipLaunchKernelGGL(router_tile_kernel, dim3((T + kRouterTok - 1) / kRouterTok), dim3(256), 0,
+                       s, x, w, T, H, E, logits);
+  }
+}
+
+// One wave per token, lane = expert. Softmax as ops::softmax: reject NaN and
+// +inf, subtract the maximum, exp, sum, divide. Then k rounds of wave
+// arg-max ordered by (probability desc, id asc) — the reference's sort key
+// (src/decoder/moe.rs:19) — and the optional renormalisation
+// sum(top-k, in selection order) + 1e-20 (:21-25) and scale (:26-28).
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int n,
+                                                   int K, int normalize, float scale,
+                                                   int* __restrict__ ids,
+                                                   float* __restrict__ weights, int* err) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v = lane < n ? logits[(size_t)t * n + lane] : -INFINITY;
+  bool bad = lane < n && (isnan(v) || v == INFINITY);
+  float m = wave_max(v);
+  if (__any(bad) || !isfinite(m)) {
+    if (lane == 0) raise_error(err, kErrNumerical);
+    if (lane < K) {
+      ids[(size_t)t * K + lane] = 0;
+      weights[(size_t)t * K + lane] = 0.0f;
+    }
+    return;
+  }
+  float e = lane < n ? expf(v - m) : 0.0f;
+  float sum = wave_sum(e);
+  float p = e / sum;
+  unsigned long long key =
+      lane < n ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane)
+               : 0ull;
+  int my_id = 0;
+  float my_p = 0.0f;
+  float den = -0.0f;
+  for (int j = 0; j < K; j++) {
+    unsigned long long best = wave_max_u64(key);
+    int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    float pj = __uint_as_float((uint32_t)(best >> 32));
+    if (lane == id) key = 0ull;
+    if (lane == j) {
+      my_id = id;
+      my_p = pj;
+    }
+    den += pj;
+  }
+  den = normalize ? den + 1e-20f : 1.0f;
+  if (lane < K) {
+    ids[(size_t)t * K + lane] = my_id;
+    weights[(size_t)t * K + lane] = my_p / den * scale;
+  }
+}
+
+void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
+                 float* weights, int* err, hipStream_t s) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, n, K, normalize,
+                     scale, ids, weights, err);
+}
+
+}  // namespace uocr

@@ -1,0 +1,268 @@
+"""ctypes binding of libuocr_moe.so (the C ABI in include/uocr_moe.h).
+
+Python here is plumbing for tests, the benchmark and the smoke check: device
+memory comes from torch tensors, every computation runs in the HIP library.
+Importing fails loudly when the library is not built — there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libuocr_moe.so")
+
+OK, IO, JSON, FORMAT, SHAPE, UNSUPPORTED, RESOURCE, NUMERICAL = range(8)
+STATUS_NAMES = ["Ok", "Io", "Json", "Format", "Shape", "Unsupported", "Resource", "Numerical"]
+QUANT_NONE, QUANT_WEIGHTS_ONLY, QUANT_DYNAMIC = 0, 1, 2
+MEMORY_HOST, MEMORY_DEVICE = 0, 1
+FLAG_FP32_CLASS = 0
+FLAG_BF16_ACTIVATIONS = 1
+FLAG_FORCE_GEMV = 2
+FLAG_FORCE_MFMA = 4
+
+# Every symbol include/uocr_moe.h declares.
+EXPORTS = [
+    "uocr_gpu_ctx_create", "uocr_gpu_ctx_destroy", "uocr_gpu_ctx_stream",
+    "uocr_gpu_ctx_synchronize", "uocr_last_error", "uocr_moe_scratch_bytes",
+    "uocr_moe_layer_create", "uocr_moe_layer_attach_int8", "uocr_moe_layer_precision",
+    "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
+    "uocr_moe_forward", "uocr_moe_block_forward", "uocr_moe_block_forward_async", "uocr_route",
+    "uocr_linear_bf16", "uocr_int8_linear", "uocr_int8_linear_dynamic", "uocr_rms_norm",
+]
+
+
+class UocrError(RuntimeError):
+    """A non-zero status from the library (the reference's OcrError)."""
+
+    def __init__(self, status: int, message: str):
+        name = STATUS_NAMES[status] if 0 <= status < len(STATUS_NAMES) else str(status)
+        super().__init__(f"{name}: {message}")
+        self.status = status
+
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_U32 = ctypes.c_uint32
+
+
+class MoeConfig(ctypes.Structure):
+    _fields_ = [("hidden_size", _U32), ("moe_intermediate_size", _U32),
+                ("n_routed_experts", _U32), ("n_shared_experts", _U32),
+                ("num_experts_per_tok", _U32), ("norm_topk_prob", _U32),
+                ("routed_scaling_factor", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
+
+
+class Bf16Weights(ctypes.Structure):
+    _fields_ = [(n, _P) for n in ("router", "expert_gate", "expert_up", "expert_down",
+                                  "shared_gate", "shared_up", "shared_down", "norm_weight")]
+
+
+class Int8Weights(ctypes.Structure):
+    _fields_ = [(n, _P) for n in (
+        "expert_gate", "expert_gate_scales", "expert_up", "expert_up_scales", "expert_down",
+        "expert_down_scales", "shared_gate", "shared_gate_scales", "shared_up",
+        "shared_up_scales", "shared_down", "shared_down_scales")]
+
+
+class Trace(ctypes.Structure):
+    _fields_ = [(n, _P) for n in ("logits", "topk_ids", "topk_weights", "expert_offsets",
+                                  "perm_rows", "perm_weights")]
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make)")
+    lib = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "uocr_gpu_ctx_create": (ctypes.c_int, [ctypes.c_int, _SZ, ctypes.POINTER(_P)]),
+        "uocr_gpu_ctx_destroy": (None, [_P]),
+        "uocr_gpu_ctx_stream": (_P, [_P]),
+        "uocr_gpu_ctx_synchronize": (ctypes.c_int, [_P]),
+        "uocr_last_error": (ctypes.c_char_p, [_P]),
+        "uocr_moe_scratch_bytes": (_SZ, [ctypes.POINTER(MoeConfig), _SZ]),
+        "uocr_moe_layer_create": (ctypes.c_int, [_P, ctypes.POINTER(MoeConfig),
+                                                 ctypes.POINTER(Bf16Weights), ctypes.c_int,
+                                                 ctypes.POINTER(_P)]),
+        "uocr_moe_layer_attach_int8": (ctypes.c_int, [_P, _P, ctypes.POINTER(Int8Weights),
+                                                      ctypes.c_int, ctypes.c_int]),
+        "uocr_moe_layer_precision": (ctypes.c_char_p, [_P]),
+        "uocr_moe_layer_device_bytes": (_SZ, [_P]),
+        "uocr_moe_layer_destroy": (None, [_P]),
+        "uocr_moe_forward_async": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _U32,
+                                                  ctypes.POINTER(Trace)]),
+        "uocr_moe_forward": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _U32, ctypes.POINTER(Trace)]),
+        "uocr_moe_block_forward": (ctypes.c_int, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ, _P,
+                                                  _U32]),
+        "uocr_moe_block_forward_async": (ctypes.c_int, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ,
+                                                        _P, _U32]),
+        "uocr_route": (ctypes.c_int, [_P, _P, _SZ, _SZ, _SZ, ctypes.c_int, ctypes.c_float, _P,
+                                      _P]),
+        "uocr_linear_bf16": (ctypes.c_int, [_P, _P, _SZ, _SZ, _P, _SZ, _P]),
+        "uocr_int8_linear": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, _SZ, _P]),
+        "uocr_int8_linear_dynamic": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, _P, _P]),
+        "uocr_rms_norm": (ctypes.c_int, [_P, _P, _SZ, _SZ, _P, ctypes.c_float, _P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _check(status: int):
+    if status != OK:
+        raise UocrError(status, lib.uocr_last_error(None).decode())
+
+
+def _ptr(t):
+    """Device (or host) address of a torch tensor / numpy array, None for None."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def config(hidden=1280, inter=896, experts=64, shared=2, top_k=6, normalize=True, scale=1.0,
+           eps=1e-6) -> MoeConfig:
+    return MoeConfig(hidden, inter, experts, shared, top_k, int(bool(normalize)), scale, eps)
+
+
+class Context:
+    """GPU counterpart of CpuContext: a device, a stream and a scratch budget."""
+
+    def __init__(self, device: int = 0, scratch_bytes: int = 1 << 30):
+        h = _P()
+        _check(lib.uocr_gpu_ctx_create(device, scratch_bytes, ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+        self.scratch_bytes = scratch_bytes
+
+    @property
+    def stream(self) -> int:
+        return lib.uocr_gpu_ctx_stream(self.handle)
+
+    def synchronize(self):
+        _check(lib.uocr_gpu_ctx_synchronize(self.handle))
+
+    def close(self):
+        if self.handle:
+            lib.uocr_gpu_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoeLayer:
+    """One uploaded MoE layer (router, 64 routed experts, fused shared expert)."""
+
+    def __init__(self, ctx: Context, cfg: MoeConfig, weights: dict, where: int):
+        self._keep = []
+        self.cfg = cfg
+        w = Bf16Weights(*[self._hold(weights.get(n)) for n in (
+            "router", "gate", "up", "down", "shared_gate", "shared_up", "shared_down",
+            "norm_weight")])
+        h = _P()
+        _check(lib.uocr_moe_layer_create(ctx.handle, ctypes.byref(cfg), ctypes.byref(w), where,
+                                         ctypes.byref(h)))
+        self.handle = h
+        self._keep = []
+
+    def _hold(self, a):
+        if a is None:
+            return None
+        self._keep.append(a)
+        return _ptr(a)
+
+    def attach_int8(self, ctx: Context, q: dict, where: int, mode: int):
+        self._keep = []
+        names = []
+        for n in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
+            qa, sa = q.get(n, (None, None))
+            names += [self._hold(qa), self._hold(sa)]
+        w = Int8Weights(*names)
+        _check(lib.uocr_moe_layer_attach_int8(ctx.handle, self.handle, ctypes.byref(w), where,
+                                              mode))
+        self._keep = []
+
+    @property
+    def precision(self) -> str:
+        return lib.uocr_moe_layer_precision(self.handle).decode()
+
+    @property
+    def device_bytes(self) -> int:
+        return lib.uocr_moe_layer_device_bytes(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib.uocr_moe_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | None = None,
+            sync: bool = True):
+    """Decoder::experts on device tensors x [T,H] -> y [T,H] (float32, cuda)."""
+    T = x.shape[0]
+    tr = None
+    if trace is not None:
+        tr = Trace(*[_ptr(trace.get(n)) for n in ("logits", "topk_ids", "topk_weights",
+                                                  "expert_offsets", "perm_rows",
+                                                  "perm_weights")])
+    fn = lib.uocr_moe_forward if sync else lib.uocr_moe_forward_async
+    _check(fn(ctx.handle, layer.handle, _ptr(x), T, _ptr(y), flags,
+              ctypes.byref(tr) if tr is not None else None))
+
+
+def block_forward(ctx: Context, layers, x, y, flags: int = 0, sync: bool = True):
+    arr = (_P * len(layers))(*[l.handle.value for l in layers])
+    fn = lib.uocr_moe_block_forward if sync else lib.uocr_moe_block_forward_async
+    _check(fn(ctx.handle, arr, len(layers), _ptr(x), x.shape[0], _ptr(y), flags))
+
+
+def scratch_bytes(cfg: MoeConfig, T: int) -> int:
+    return lib.uocr_moe_scratch_bytes(ctypes.byref(cfg), T)
+
+
+def route(ctx: Context, logits, count: int, normalize: bool, scale: float, ids, weights):
+    T, n = logits.shape
+    _check(lib.uocr_route(ctx.handle, _ptr(logits), T, n, count, int(normalize), scale,
+                          _ptr(ids), _ptr(weights)))
+
+
+def linear_bf16(ctx: Context, x, w_bits, y):
+    m, k = x.shape
+    n = w_bits.shape[0]
+    _check(lib.uocr_linear_bf16(ctx.handle, _ptr(x), m, k, _ptr(w_bits), n, _ptr(y)))
+
+
+def int8_linear(ctx: Context, q, scales, x, y):
+    rows, cols = q.shape
+    batch = x.shape[0]
+    _check(lib.uocr_int8_linear(ctx.handle, _ptr(q), _ptr(scales), rows, cols, _ptr(x), batch,
+                                _ptr(y)))
+
+
+def int8_linear_dynamic(ctx: Context, q, scales, x, y, block_sums=None):
+    rows, cols = q.shape
+    _check(lib.uocr_int8_linear_dynamic(ctx.handle, _ptr(q), _ptr(scales), rows, cols, _ptr(x),
+                                        _ptr(y), _ptr(block_sums)))
+
+
+def rms_norm(ctx: Context, x, weight, eps: float, out):
+    rows, width = x.shape
+    _check(lib.uocr_rms_norm(ctx.handle, _ptr(x), rows, width, _ptr(weight), eps, _ptr(out)))
