@@ -141,6 +141,20 @@ void* uocr_gpu_ctx_stream(uocr_gpu_ctx* ctx);
 int uocr_gpu_ctx_synchronize(uocr_gpu_ctx* ctx);
 /* Message of the last failure on this thread (ctx may be NULL). */
 const char* uocr_last_error(const uocr_gpu_ctx* ctx);
+/* Phase timing with HIP events on the context stream (the GPU side of the
+ * reference's per-phase Timings, src/model/mod.rs:36-45). Bit i of
+ * phase_mask brackets every launch of phase i with events; totals
+ * accumulate until read. Phases, in bit order: router, topk, dispatch,
+ * split, gateup, down, combine, norm. 0 disables timing. */
+typedef struct uocr_phase_time {
+  const char* name;
+  uint64_t launches;
+  double total_ms;
+} uocr_phase_time;
+int uocr_gpu_ctx_set_timing(uocr_gpu_ctx* ctx, uint32_t phase_mask);
+/* Synchronises, then copies up to `cap` phase totals (all phases when cap
+ * allows) and resets them. *count receives the number of phases. */
+int uocr_gpu_ctx_timings(uocr_gpu_ctx* ctx, uocr_phase_time* out, size_t cap, size_t* count);
 /* Bytes of scratch a forward of T tokens needs (CpuContext::check_elements,
  * src/cpu/mod.rs:73-78); forwards above the context's limit fail with
  * Resource. */

