@@ -351,7 +351,10 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   HIP_TRY(hipGetDeviceCount(&n), "device count");
   if (device < 0 || device >= n) return fail(UOCR_ERR_UNSUPPORTED, "no GPU device %d", device);
   HIP_TRY(hipSetDevice(device), "set device");
-  std::call_once(g_attr_once, [] { uocr::gemv_init_attributes(); });
+  std::call_once(g_attr_once, [] {
+    uocr::gemv_init_attributes();
+    uocr::mfma_init_attributes();
+  });
   auto* ctx = new uocr_gpu_ctx();
   ctx->device = device;
   ctx->scratch_limit = scratch_limit;

@@ -77,7 +77,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       tiles[2 * (routed_tiles + i)] = E;
       tiles[2 * (routed_tiles + i) + 1] = i * bm;
     }
-    if (lane == 0) counters[0] = routed_tiles + shared_tiles;
+    if (lane == 0) {
+      counters[0] = routed_tiles + shared_tiles;
+      counters[1] = routed_tiles;
+    }
   }
   __syncthreads();
   for (int c0 = 0; c0 < T; c0 += kDispatchThreads) {

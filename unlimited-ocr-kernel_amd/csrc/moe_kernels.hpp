@@ -98,7 +98,8 @@ void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
                         int tiles_bound, bool bf16_only, hipStream_t s);
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                       int tiles_bound, bool bf16_only, hipStream_t s);
-constexpr int kMfmaBM = 128;
+constexpr int kMfmaBM = 256;
+void mfma_init_attributes();
 constexpr int kGemvChunk = 16;
 
 // combine.hip
