@@ -137,8 +137,8 @@ struct uocr_moe_layer {
 namespace {
 
 struct ScratchPlan {
-  size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, h, hs, y, ys, xn,
-      xb, total;
+  size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
+      chunk_base, h, hs, y, ys, xn, xb, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -161,6 +161,8 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   // Worst tile count over both engines (one-row tiles for decode).
   p.tiles = take((size_t)uocr::max_tiles((int)T, (int)K, (int)E, 1) * 2 * 4);
   p.counters = take(16);
+  p.chunk_counts = take((T + 15) / 16 * 64 * 4);
+  p.chunk_base = take((T + 15) / 16 * 64 * 4);
   p.h = take(T * K * I * 4);
   p.hs = take(T * S * 4);
   p.y = take(T * K * H * 4);
@@ -183,6 +185,8 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.inv_pos = reinterpret_cast<int*>(b + p.inv_pos);
   s.tiles = reinterpret_cast<int*>(b + p.tiles);
   s.counters = reinterpret_cast<int*>(b + p.counters);
+  s.chunk_counts = reinterpret_cast<int*>(b + p.chunk_counts);
+  s.chunk_base = reinterpret_cast<int*>(b + p.chunk_base);
   s.h = reinterpret_cast<float*>(b + p.h);
   s.hs = reinterpret_cast<float*>(b + p.hs);
   s.y = reinterpret_cast<float*>(b + p.y);
@@ -268,13 +272,6 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
   hipStream_t st = ctx->stream;
-  phase_begin(ctx, kRouter);
-  uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
-  phase_end(ctx);
-  phase_begin(ctx, kTopk);
-  uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w, S.err,
-                    st);
-  phase_end(ctx);
   // Engine: the row-chunk GEMV engine for small batches (bandwidth-bound),
   // the MFMA grouped GEMM for larger BF16 batches.
   bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
@@ -289,10 +286,30 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
-  phase_begin(ctx, kDispatch);
-  uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows, S.perm_w,
-                        S.inv_pos, S.tiles, S.counters, st);
-  phase_end(ctx);
+  if (T > (size_t)uocr::kGemvChunk) {
+    // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
+    phase_begin(ctx, kRouter);
+    uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
+                                  S.logits, S.topk_ids, S.topk_w, S.chunk_counts, S.err, st);
+    phase_end(ctx);
+    phase_begin(ctx, kDispatch);
+    uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.chunk_counts,
+                                  S.chunk_base, S.offsets, S.perm_rows, S.perm_w, S.inv_pos,
+                                  S.tiles, S.counters, st);
+    phase_end(ctx);
+  } else {
+    phase_begin(ctx, kRouter);
+    uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
+    phase_end(ctx);
+    phase_begin(ctx, kTopk);
+    uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w, S.err,
+                      st);
+    phase_end(ctx);
+    phase_begin(ctx, kDispatch);
+    uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows,
+                          S.perm_w, S.inv_pos, S.tiles, S.counters, st);
+    phase_end(ctx);
+  }
   if (mfma) {
     uocr::MfmaPlanes P;
     P.x_hi = S.xb;

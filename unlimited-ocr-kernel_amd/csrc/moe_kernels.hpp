@@ -45,7 +45,9 @@ struct Scratch {
   float* perm_w;    // [T*K]
   int* inv_pos;     // [T*K] position of (token, slot) in the dispatched order
   int* tiles;       // [max_tiles*2] (group, first row) per row tile
-  int* counters;    // [4]: tile count
+  int* counters;    // [4]: row tiles, routed row tiles
+  int* chunk_counts;  // [ceil(T/16), 64] per-chunk expert counts (router)
+  int* chunk_base;    // [ceil(T/16), 64] first dispatched slot per (chunk, expert)
   float* h;         // [T*K, I] routed hidden in dispatched order
   float* hs;        // [T, S] shared hidden
   float* y;         // [T*K, H] routed expert outputs in dispatched order
@@ -63,7 +65,15 @@ void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E
 void launch_topk(const float* logits, int T, int E, int K, int normalize, float scale, int* ids,
                  float* weights, int* err, hipStream_t s);
 
+void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
+                             int normalize, float scale, float* logits, int* ids, float* weights,
+                             int* chunk_counts, int* err, hipStream_t s);
+
 // dispatch.hip
+void launch_dispatch_chunked(const int* ids, const float* w, int T, int E, int K, int bm,
+                             const int* chunk_counts, int* chunk_base, int* offsets,
+                             int* perm_rows, float* perm_w, int* inv_pos, int* tiles,
+                             int* counters, hipStream_t s);
 void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,
                      int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
                      hipStream_t s);

@@ -116,44 +116,44 @@ void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E
   }
 }
 
-// One wave per token, lane = expert. Softmax as ops::softmax: reject NaN and
-// +inf, subtract the maximum, exp, sum, divide. Then k rounds of wave
-// arg-max ordered by (probability desc, id asc) — the reference's sort key
+// Routes one token held one logit per lane (lane = expert, n <= 64 valid
+// lanes). Softmax as ops::softmax: reject NaN and +inf, subtract the
+// maximum, exp, sum, divide. Then k rounds of wave arg-max ordered by
+// (probability desc, id asc) — the reference's sort key
 // (src/decoder/moe.rs:19) — and the optional renormalisation
 // sum(top-k, in selection order) + 1e-20 (:21-25) and scale (:26-28).
-__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int n,
-                                                   int K, int normalize, float scale,
-                                                   int* __restrict__ ids,
-                                                   float* __restrict__ weights, int* err) {
+// Lanes j < K write slot j; returns the id written by this lane (-1 for
+// lanes >= K).
+__device__ int route_token(float v, int n, int K, int normalize, float scale, int* ids,
+                           float* weights, int* err) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float v = lane < n ? logits[(size_t)t * n + lane] : -INFINITY;
-  bool bad = lane < n && (isnan(v) || v == INFINITY);
-  float m = wave_max(v);
+  if (lane >= n) v = -INFINITY;
+  const bool bad = lane < n && (isnan(v) || v == INFINITY);
+  const float m = wave_max(v);
   if (__any(bad) || !isfinite(m)) {
     if (lane == 0) raise_error(err, kErrNumerical);
     // The forward fails; still emit k distinct ids so the dispatch stays a
     // permutation (its ranks assume distinct experts per token).
     if (lane < K) {
-      ids[(size_t)t * K + lane] = lane;
-      weights[(size_t)t * K + lane] = 0.0f;
+      ids[lane] = lane;
+      weights[lane] = 0.0f;
+      return lane;
     }
-    return;
+    return -1;
   }
-  float e = lane < n ? expf(v - m) : 0.0f;
-  float sum = wave_sum(e);
-  float p = e / sum;
+  const float e = lane < n ? expf(v - m) : 0.0f;
+  const float sum = wave_sum(e);
+  const float p = e / sum;
   unsigned long long key =
       lane < n ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane)
                : 0ull;
-  int my_id = 0;
+  int my_id = -1;
   float my_p = 0.0f;
   float den = -0.0f;
   for (int j = 0; j < K; j++) {
-    unsigned long long best = wave_max_u64(key);
-    int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-    float pj = __uint_as_float((uint32_t)(best >> 32));
+    const unsigned long long best = wave_max_u64(key);
+    const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    const float pj = __uint_as_float((uint32_t)(best >> 32));
     if (lane == id) key = 0ull;
     if (lane == j) {
       my_id = id;
@@ -163,9 +163,117 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   }
   den = normalize ? den + 1e-20f : 1.0f;
   if (lane < K) {
-    ids[(size_t)t * K + lane] = my_id;
-    weights[(size_t)t * K + lane] = my_p / den * scale;
+    ids[lane] = my_id;
+    weights[lane] = my_p / den * scale;
   }
+  return my_id;
+}
+
+// One wave per token.
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int n,
+                                                   int K, int normalize, float scale,
+                                                   int* __restrict__ ids,
+                                                   float* __restrict__ weights, int* err) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float v = lane < n ? logits[(size_t)t * n + lane] : -INFINITY;
+  route_token(v, n, K, normalize, scale, ids + (size_t)t * K, weights + (size_t)t * K, err);
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Many tokens: logits on MFMA (v_mfma_f32_16x16x32_bf16), then softmax
+// top-k, fused. Each FP32 activation splits exactly into three bf16 terms
+// (hi + mid + lo carry its 24 significand bits) and the router weights are
+// bf16, so every product is exact and the logits are FP32-accurate sums.
+// A workgroup owns 16 tokens and all <= 64 experts; its 4 waves take every
+// 4th 32-wide K step and their partial sums are added in wave order
+// (deterministic). It also emits the chunk's per-expert assignment counts
+// for the dispatch scan.
+constexpr int kRouteChunk = 16;
+
+__global__ __launch_bounds__(256) void router_mfma_kernel(
+    const float* __restrict__ x, const uint16_t* __restrict__ w, int T, int H, int E, int K,
+    int normalize, float scale, float* __restrict__ logits, int* __restrict__ ids,
+    float* __restrict__ weights, int* __restrict__ chunk_counts, int* err) {
+  __shared__ float part[4][kRouteChunk][65];
+  __shared__ int cnt[64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int t0 = blockIdx.x * kRouteChunk;
+  if (tid < 64) cnt[tid] = 0;
+  const int ar = lane & 15;        // fragment row (token) / column (expert)
+  const int aq = (lane >> 4) * 8;  // fragment k offset within a 32-wide step
+  const int token = t0 + ar;
+  const bool tok_ok = token < T;
+  const float* xrow = x + (size_t)(tok_ok ? token : 0) * H + aq;
+  floatx4 acc[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ni++) acc[ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int steps = H / 32;
+#pragma unroll 2
+  for (int st = wave; st < steps; st += 4) {
+    const int k0 = st * 32;
+    const float4 v0 = *reinterpret_cast<const float4*>(xrow + k0);
+    const float4 v1 = *reinterpret_cast<const float4*>(xrow + k0 + 4);
+    uint4 bv[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) {
+      const int e = ni * 16 + ar;
+      bv[ni] = e < E ? *reinterpret_cast<const uint4*>(w + (size_t)e * H + k0 + aq)
+                     : make_uint4(0, 0, 0, 0);
+    }
+    const float xv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    bf16x8 hi, mid, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float f = tok_ok ? xv[i] : 0.0f;
+      const __bf16 h = (__bf16)f;
+      const float r1 = f - (float)h;
+      const __bf16 m = (__bf16)r1;
+      hi[i] = h;
+      mid[i] = m;
+      lo[i] = (__bf16)(r1 - (float)m);
+    }
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) {
+      const bf16x8 b = __builtin_bit_cast(bf16x8, bv[ni]);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[ni], 0, 0, 0);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[ni], 0, 0, 0);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[ni], 0, 0, 0);
+    }
+  }
+  // acc[ni][r]: token 4 (lane / 16) + r, expert 16 ni + lane % 16.
+#pragma unroll
+  for (int ni = 0; ni < 4; ni++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) part[wave][4 * (lane >> 4) + r][ni * 16 + ar] = acc[ni][r];
+  __syncthreads();
+  for (int j = 0; j < kRouteChunk / 4; j++) {
+    const int tl = wave * (kRouteChunk / 4) + j;
+    const int t = t0 + tl;
+    if (t >= T) break;
+    const float v = ((part[0][tl][lane] + part[1][tl][lane]) + part[2][tl][lane]) +
+                    part[3][tl][lane];
+    if (lane < E) logits[(size_t)t * E + lane] = v;
+    const int id = route_token(v, E, K, normalize, scale, ids + (size_t)t * K,
+                               weights + (size_t)t * K, err);
+    if (lane < K) atomicAdd(&cnt[id], 1);
+  }
+  __syncthreads();
+  if (tid < 64) chunk_counts[(size_t)blockIdx.x * 64 + tid] = cnt[tid];
+}
+
+void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
+                             int normalize, float scale, float* logits, int* ids, float* weights,
+                             int* chunk_counts, int* err, hipStream_t s) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(router_mfma_kernel, dim3((T + kRouteChunk - 1) / kRouteChunk), dim3(256), 0,
+                     s, x, w, T, H, E, K, normalize, scale, logits, ids, weights, chunk_counts,
+                     err);
 }
 
 void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
