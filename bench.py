@@ -51,6 +51,12 @@ def parse():
                     help="comma list of secondary workloads, or 'none'")
     ap.add_argument("--cpu-sample", type=int, default=512,
                     help="tokens of the headline workload timed on the CPU oracle (0: skip)")
+    ap.add_argument("--layers", type=int, default=12,
+                    help="layers in the headline stack (12 for the measured workload; fewer "
+                         "only to shorten counter-collection runs)")
+    ap.add_argument("--profile-copy", action="store_true",
+                    help="after timing, copy 256 MiB once so that counter runs can scale "
+                         "FETCH_SIZE/WRITE_SIZE against a plain copy of known size")
     return ap.parse_args()
 
 
@@ -95,7 +101,7 @@ def main():
     log("generating the 12-layer stack (T=4096, 80% to 8 hot experts)")
     hot = syn.route_profile(syn.hot_share(E, K, 8, 0.8), K)
     layers, host_layer0 = [], None
-    for l in range(12):
+    for l in range(args.layers):
         w = syn.moe_weights_device(H, I, E, SH, seed=1000 + l, router_scale=hot, norm=True)
         torch.cuda.synchronize()  # the library copies on its own stream
         layers.append(um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE))
@@ -124,7 +130,7 @@ def main():
     gate_t = ctx.timings()["gateup"]
     ctx.set_timing([])
     ms_step = (t1 - t0) * 1e3 / args.steps
-    value = T * 12 / (ms_step / 1e3)
+    value = T * args.layers / (ms_step / 1e3)
     gate_avg_ms = gate_t[1] / max(gate_t[0], 1)
     achieved = GATEUP_FLOP_PER_TOKEN * T / (gate_avg_ms / 1e3) / 1e12
     # Phase breakdown (separate pass, every phase bracketed).
@@ -140,13 +146,19 @@ def main():
         um.block_forward(ctx, layers, x, y, flags=um.FLAG_FP32_CLASS, sync=False)
     sync()
     ms_fp32 = (time.perf_counter() - t0) * 1e3 / args.steps
-    layer_s_flop = FLOP_PER_TOKEN * T / (ms_step / 12 / 1e3) / 1e12
+    layer_s_flop = FLOP_PER_TOKEN * T / (ms_step / args.layers / 1e3) / 1e12
     log(f"stack: {ms_step:.3f} ms/step, {value:,.0f} layer-tokens/s, gateup {gate_avg_ms:.4f} ms "
         f"= {achieved:.1f} TFLOP/s; fp32-class {ms_fp32:.3f} ms/step")
     for l in layers:
         l.close()
     del layers, x, y
     torch.cuda.empty_cache()
+    if args.profile_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     secondary = []
     wanted = [] if args.secondary == "none" else args.secondary.split(",")
@@ -280,11 +292,11 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "moe-stack-12x-prefill-T4096-hot8", "tokens": 4096,
-                   "layers": 12, "hidden": H, "experts": E, "top_k": K,
+        "config": {"workload": f"moe-stack-{args.layers}x-prefill-T4096-hot8", "tokens": 4096,
+                   "layers": args.layers, "hidden": H, "experts": E, "top_k": K,
                    "shared_width": S, "expert_width": I,
                    "activations": "bf16 operands, fp32 accumulate (2e-2 class)",
-                   "value_is": "4096 tokens x 12 layers / step time",
+                   "value_is": f"4096 tokens x {args.layers} layers / step time",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -21,8 +21,8 @@
 //
 // Work items are (row tile, column tile) pairs enumerated on the device.
 // Workgroup ids reach the 8 XCDs round-robin; they are remapped so each XCD
-// takes a contiguous range of items, keeping an expert's weights in that
-// XCD's L2.
+// takes a contiguous range of the existing items, keeping an expert's
+// weights in that XCD's L2.
 #include "common.hpp"
 #include "moe_kernels.hpp"
 
@@ -94,9 +94,10 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   uint16_t* const stage1 = lds + (SPLIT ? 3 : 2) * kPlane;
   __shared__ int arow[kTileM];
 
-  // ---- work item (XCD-contiguous remap of the workgroup id)
-  const int per_xcd = gridDim.x / kXcds;  // gridDim.x is a multiple of 8
-  const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8); XCD
+  // x takes the contiguous item range [x * chunk, (x + 1) * chunk) of the
+  // items that exist, so all 8 XCDs share the work and neighbouring items
+  // (same expert) meet in one L2.
   const int routed_tiles = S.counters[1];
   const int all_tiles = S.counters[0];
   const int n_routed = GATEUP ? 2 * L.I : L.H;
@@ -104,6 +105,11 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   const int nt_routed = (n_routed + kTileN - 1) / kTileN;
   const int nt_shared = (n_shared + kTileN - 1) / kTileN;
   const int routed_items = routed_tiles * nt_routed;
+  const int n_items = routed_items + (all_tiles - routed_tiles) * nt_shared;
+  const int chunk = (n_items + kXcds - 1) / kXcds;
+  const int slot = blockIdx.x / kXcds;
+  const int item = (blockIdx.x % kXcds) * chunk + slot;
+  if (slot >= chunk || item >= n_items) return;
   int tile, ntile;
   if (item < routed_items) {
     tile = item / nt_routed;
@@ -112,7 +118,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
     const int rest = item - routed_items;
     tile = routed_tiles + rest / nt_shared;
     ntile = rest % nt_shared;
-    if (tile >= all_tiles) return;
   }
   const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
   const bool routed = g < L.E;
@@ -239,7 +244,8 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
       for (int r = 0; r < 16; r++) {
         const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < mrows) {
-          const float h = silu(acc[mi][0][r]) * acc[mi][1][r];
+          const float gv = acc[mi][0][r];
+          const float h = __fdividef(gv, 1.0f + __expf(-gv)) * acc[mi][1][r];
           const size_t at = (size_t)(base + r0 + row) * W + col;
           const uint16_t hb = bf16_bits(h);
           h_hi[at] = hb;
