@@ -655,7 +655,9 @@ int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const
   if (!ctx || !layer) return fail(UOCR_ERR_SHAPE, "null handle");
   if (T == 0) return UOCR_OK;
   if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
-  if (T > (size_t)(1 << 24)) return fail(UOCR_ERR_RESOURCE, "token count too large");
+  // The MFMA engine addresses activation rows with 32-bit element offsets
+  // (T * k * max(I, S) < 2^32); 262,144 tokens per forward keeps that safe.
+  if (T > (size_t)262144) return fail(UOCR_ERR_RESOURCE, "token count too large");
   HIP_TRY(hipSetDevice(ctx->device), "set device");
   return enqueue_experts(ctx, layer, x, T, nullptr, y, flags, trace, false);
 }
@@ -673,6 +675,7 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
   if (!ctx || (!layers && n_layers)) return fail(UOCR_ERR_SHAPE, "null handle");
   if (T == 0 || n_layers == 0) return UOCR_OK;
   if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
+  if (T > (size_t)262144) return fail(UOCR_ERR_RESOURCE, "token count too large");
   HIP_TRY(hipSetDevice(ctx->device), "set device");
   const float* cur = x;
   for (size_t l = 0; l < n_layers; l++) {
