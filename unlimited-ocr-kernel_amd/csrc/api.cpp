@@ -66,6 +66,7 @@ struct uocr_gpu_ctx {
   size_t scratch_limit = 0;
   int* err = nullptr;       // device error flag
   int* err_host = nullptr;  // pinned readback
+  int* sync = nullptr;      // election counters (zero between forwards)
   // Phase timing: bit i of timing_mask enables phase i.
   uint32_t timing_mask = 0;
   std::vector<hipEvent_t> free_events;
@@ -138,7 +139,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
-      chunk_base, h, hs, y, ys, xn, xb, total;
+      chunk_base, h, hs, y, ys, xn, xb, gu, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -169,6 +170,7 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   p.ys = take(T * H * 4);
   p.xn = take(T * H * 4);
   p.xb = take(T * H * 4);
+  p.gu = take((T * K * 2 * I + T * 2 * S) * 4);
   p.total = at;
   return p;
 }
@@ -193,7 +195,9 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.ys = reinterpret_cast<float*>(b + p.ys);
   s.xn = reinterpret_cast<float*>(b + p.xn);
   s.xb = reinterpret_cast<uint16_t*>(b + p.xb);
+  s.gu = reinterpret_cast<float*>(b + p.gu);
   s.err = ctx->err;
+  s.sync = ctx->sync;
   return s;
 }
 
@@ -286,58 +290,83 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
-  if (T > (size_t)uocr::kGemvChunk) {
-    // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
+  // The small-batch router holds a router row in registers (H <= 2048).
+  const bool small = !mfma && T <= (size_t)uocr::kGemvChunk && L.H <= 2048;
+  if (small) {
+    // Few tokens: three launches. Router + top-k + dispatch, gate/up, and
+    // down with the ordered combine fused in.
     phase_begin(ctx, kRouter);
-    uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
-                                  S.logits, S.topk_ids, S.topk_w, S.chunk_counts, S.err, st);
+    uocr::launch_route_small(S.xn, L, S, Ti, bm, st);
     phase_end(ctx);
-    phase_begin(ctx, kDispatch);
-    uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.chunk_counts,
-                                  S.chunk_base, S.offsets, S.perm_rows, S.perm_w, S.inv_pos,
-                                  S.tiles, S.counters, st);
-    phase_end(ctx);
+    if (T == 1 && uocr::decode_supported(L)) {
+      phase_begin(ctx, kGateUp);
+      uocr::launch_decode_gateup(L, S, tiles_bound, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDown);
+      uocr::launch_decode_down(L, S, tiles_bound, residual, y, st);
+      phase_end(ctx);
+    } else {
+      phase_begin(ctx, kGateUp);
+      uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDown);
+      uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, residual, y, st);
+      phase_end(ctx);
+    }
   } else {
-    phase_begin(ctx, kRouter);
-    uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
-    phase_end(ctx);
-    phase_begin(ctx, kTopk);
-    uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w, S.err,
-                      st);
-    phase_end(ctx);
-    phase_begin(ctx, kDispatch);
-    uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows,
-                          S.perm_w, S.inv_pos, S.tiles, S.counters, st);
+    if (T > (size_t)uocr::kGemvChunk) {
+      // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
+      phase_begin(ctx, kRouter);
+      uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
+                                    S.logits, S.topk_ids, S.topk_w, S.chunk_counts, S.err, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDispatch);
+      uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.chunk_counts,
+                                    S.chunk_base, S.offsets, S.perm_rows, S.perm_w, S.inv_pos,
+                                    S.tiles, S.counters, st);
+      phase_end(ctx);
+    } else {
+      phase_begin(ctx, kRouter);
+      uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
+      phase_end(ctx);
+      phase_begin(ctx, kTopk);
+      uocr::launch_topk(S.logits, Ti, L.E, L.K, L.normalize, L.scale, S.topk_ids, S.topk_w,
+                        S.err, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDispatch);
+      uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows,
+                            S.perm_w, S.inv_pos, S.tiles, S.counters, st);
+      phase_end(ctx);
+    }
+    if (mfma) {
+      uocr::MfmaPlanes P;
+      P.x_hi = S.xb;
+      P.x_lo = S.xb + T * L.H;
+      P.h_hi = reinterpret_cast<uint16_t*>(S.h);
+      P.h_lo = P.h_hi + T * L.K * L.I;
+      P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
+      P.hs_lo = P.hs_hi + T * L.S;
+      phase_begin(ctx, kSplit);
+      uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+      phase_end(ctx);
+      phase_begin(ctx, kGateUp);
+      uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDown);
+      uocr::launch_mfma_down(L, S, P, Ti, tiles_bound, bf16_only, st);
+      phase_end(ctx);
+    } else {
+      phase_begin(ctx, kGateUp);
+      uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDown);
+      uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, nullptr, nullptr, st);
+      phase_end(ctx);
+    }
+    phase_begin(ctx, kCombine);
+    uocr::launch_combine(S, residual, Ti, L.H, L.K, y, st);
     phase_end(ctx);
   }
-  if (mfma) {
-    uocr::MfmaPlanes P;
-    P.x_hi = S.xb;
-    P.x_lo = S.xb + T * L.H;
-    P.h_hi = reinterpret_cast<uint16_t*>(S.h);
-    P.h_lo = P.h_hi + T * L.K * L.I;
-    P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
-    P.hs_lo = P.hs_hi + T * L.S;
-    phase_begin(ctx, kSplit);
-    uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
-    phase_end(ctx);
-    phase_begin(ctx, kGateUp);
-    uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, st);
-    phase_end(ctx);
-    phase_begin(ctx, kDown);
-    uocr::launch_mfma_down(L, S, P, Ti, tiles_bound, bf16_only, st);
-    phase_end(ctx);
-  } else {
-    phase_begin(ctx, kGateUp);
-    uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
-    phase_end(ctx);
-    phase_begin(ctx, kDown);
-    uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, st);
-    phase_end(ctx);
-  }
-  phase_begin(ctx, kCombine);
-  uocr::launch_combine(S, residual, Ti, L.H, L.K, y, st);
-  phase_end(ctx);
   HIP_TRY(hipGetLastError(), "kernel launch");
   if (trace) {
     const size_t TK = T * L.K;
@@ -380,6 +409,8 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&ctx->sync, uocr::kSyncSize * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->sync, 0, uocr::kSyncSize * sizeof(int));
   if (e != hipSuccess) {
     uocr_gpu_ctx_destroy(ctx);
     return hip_fail(e, "context allocation");
@@ -394,6 +425,7 @@ void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->err) (void)hipFree(ctx->err);
+  if (ctx->sync) (void)hipFree(ctx->sync);
   if (ctx->err_host) (void)hipHostFree(ctx->err_host);
   collect_timings(ctx);
   for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);

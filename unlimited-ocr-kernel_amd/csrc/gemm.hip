@@ -324,6 +324,7 @@ void mfma_init_attributes() {
   (void)hipFuncSetAttribute((const void*)mfma_group_kernel<32, true, false>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)mfma_lds_bytes<32, true>());
+  (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
 
 }  // namespace uocr

@@ -54,8 +54,16 @@ struct Scratch {
   float* ys;        // [T, H] shared expert output
   float* xn;        // [T, H] normalised block input
   uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
+  float* gu;        // one token: raw gate/up values, [T*K*2I + T*2S] (decode)
   int* err;         // device error flag
+  // Persistent per-context counters for "last workgroup" elections: [0] the
+  // small-batch router, [64 + b] feature block b of the fused down/combine.
+  // Each election resets its counter, so they are zero between forwards.
+  int* sync;
 };
+constexpr int kSyncRouter = 0;
+constexpr int kSyncDown = 64;
+constexpr int kSyncSize = 64 + 1024;
 
 int max_tiles(int T, int K, int E, int bm);
 
@@ -65,6 +73,10 @@ void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E
 void launch_topk(const float* logits, int T, int E, int K, int normalize, float scale, int* ids,
                  float* weights, int* err, hipStream_t s);
 
+// Few tokens (T <= 16): router logits, softmax top-k and the dispatch in one
+// launch (bm = 1 for one token, else 16: one row tile per group).
+void launch_route_small(const float* x, const DeviceLayer& L, const Scratch& S, int T, int bm,
+                        hipStream_t s);
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, int* err, hipStream_t s);
@@ -82,7 +94,7 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 void launch_gemv_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, hipStream_t s);
 void launch_gemv_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                      hipStream_t s);
+                      const float* residual, float* out, hipStream_t s);
 // Operator entry points (single matrix).
 void launch_linear_bf16(const float* x, int m, int k, const uint16_t* w, int n, float* y,
                         hipStream_t s);
@@ -111,6 +123,13 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
 constexpr int kMfmaBM = 256;
 void mfma_init_attributes();
 constexpr int kGemvChunk = 16;
+
+// decode.hip: one-token expert engine (3 launches per layer with the
+// small-batch router).
+bool decode_supported(const DeviceLayer& L);
+void launch_decode_gateup(const DeviceLayer& L, const Scratch& S, int tiles_bound, hipStream_t s);
+void launch_decode_down(const DeviceLayer& L, const Scratch& S, int tiles_bound,
+                        const float* residual, float* out, hipStream_t s);
 
 // combine.hip
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
