@@ -292,27 +292,30 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
   // The small-batch router holds a router row in registers (H <= 2048).
   const bool small = !mfma && T <= (size_t)uocr::kGemvChunk && L.H <= 2048;
-  if (small) {
+  if (small && T == 1 && uocr::decode_supported(L)) {
+    // One token: three launches with no routing launch of their own (the
+    // router rides with the shared gate/up, top-k with the routed gate/up).
+    phase_begin(ctx, kRouter);
+    uocr::launch_decode_stage(1, L, S, residual, y, st);
+    phase_end(ctx);
+    phase_begin(ctx, kGateUp);
+    uocr::launch_decode_stage(2, L, S, residual, y, st);
+    phase_end(ctx);
+    phase_begin(ctx, kDown);
+    uocr::launch_decode_stage(3, L, S, residual, y, st);
+    phase_end(ctx);
+  } else if (small) {
     // Few tokens: three launches. Router + top-k + dispatch, gate/up, and
     // down with the ordered combine fused in.
     phase_begin(ctx, kRouter);
     uocr::launch_route_small(S.xn, L, S, Ti, bm, st);
     phase_end(ctx);
-    if (T == 1 && uocr::decode_supported(L)) {
-      phase_begin(ctx, kGateUp);
-      uocr::launch_decode_gateup(L, S, tiles_bound, st);
-      phase_end(ctx);
-      phase_begin(ctx, kDown);
-      uocr::launch_decode_down(L, S, tiles_bound, residual, y, st);
-      phase_end(ctx);
-    } else {
-      phase_begin(ctx, kGateUp);
-      uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
-      phase_end(ctx);
-      phase_begin(ctx, kDown);
-      uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, residual, y, st);
-      phase_end(ctx);
-    }
+    phase_begin(ctx, kGateUp);
+    uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+    phase_end(ctx);
+    phase_begin(ctx, kDown);
+    uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, residual, y, st);
+    phase_end(ctx);
   } else {
     if (T > (size_t)uocr::kGemvChunk) {
       // Many tokens: fused MFMA router + top-k, then the chunked dispatch.

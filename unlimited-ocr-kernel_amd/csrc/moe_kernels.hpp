@@ -54,7 +54,7 @@ struct Scratch {
   float* ys;        // [T, H] shared expert output
   float* xn;        // [T, H] normalised block input
   uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
-  float* gu;        // one token: raw gate/up values, [T*K*2I + T*2S] (decode)
+  float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
   int* err;         // device error flag
   // Persistent per-context counters for "last workgroup" elections: [0] the
   // small-batch router, [64 + b] feature block b of the fused down/combine.
@@ -124,12 +124,12 @@ constexpr int kMfmaBM = 256;
 void mfma_init_attributes();
 constexpr int kGemvChunk = 16;
 
-// decode.hip: one-token expert engine (3 launches per layer with the
-// small-batch router).
+// decode.hip: one-token expert engine, three launches (stage 1: router
+// logits + shared gate/up; stage 2: routed gate/up + shared down; stage 3:
+// routed down + ordered combine into out).
 bool decode_supported(const DeviceLayer& L);
-void launch_decode_gateup(const DeviceLayer& L, const Scratch& S, int tiles_bound, hipStream_t s);
-void launch_decode_down(const DeviceLayer& L, const Scratch& S, int tiles_bound,
-                        const float* residual, float* out, hipStream_t s);
+void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
+                         float* out, hipStream_t s);
 
 // combine.hip
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,

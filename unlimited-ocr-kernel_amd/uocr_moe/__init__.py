@@ -10,6 +10,15 @@ import ctypes
 import os
 from dataclasses import dataclass
 
+# torch ships its own HIP and HSA runtimes. Loading it first lets this
+# library's libamdhip64 / libhsa-runtime64 dependencies resolve into the
+# same process-wide HSA runtime; loading the library first would bring in
+# a second HSA runtime, and torch then finds no GPU.
+try:
+    import torch  # noqa: F401
+except ImportError:  # the library itself does not need torch
+    pass
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libuocr_moe.so")
 
