@@ -53,7 +53,7 @@ def parse():
                     help="tokens of the headline workload timed on the CPU oracle (0: skip)")
     ap.add_argument("--layers", type=int, default=12,
                     help="layers in the headline stack (12 for the measured workload; fewer "
-                         "only to shorten counter-collection runs)")
+                         "only to shorten counter-collection runs; 0 skips the headline)")
     ap.add_argument("--profile-copy", action="store_true",
                     help="after timing, copy 256 MiB once so that counter runs can scale "
                          "FETCH_SIZE/WRITE_SIZE against a plain copy of known size")
@@ -98,61 +98,66 @@ def main():
         ctx.synchronize()
 
     # ------------------------------------------------------------ headline
-    log("generating the 12-layer stack (T=4096, 80% to 8 hot experts)")
-    hot = syn.route_profile(syn.hot_share(E, K, 8, 0.8), K)
-    layers, host_layer0 = [], None
-    for l in range(args.layers):
-        w = syn.moe_weights_device(H, I, E, SH, seed=1000 + l, router_scale=hot, norm=True)
-        torch.cuda.synchronize()  # the library copies on its own stream
-        layers.append(um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE))
-        if l == 0 and args.cpu_sample > 0:
-            host_layer0 = {k: v.cpu().numpy().view(np.uint16) for k, v in w.items()}
-        del w
-    torch.cuda.empty_cache()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(1)
-    T = 4096
-    x = torch.randn((T, H), generator=g, device="cuda")
-    y = torch.empty_like(x)
-    flags = um.FLAG_BF16_ACTIVATIONS
-    sync()
-    for _ in range(args.warmup):
-        um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
-    sync()
-    # Timed region: K steps; events bracket only the dominant kernel.
-    ctx.set_timing(["gateup"])
-    sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
-    sync()
-    t1 = time.perf_counter()
-    gate_t = ctx.timings()["gateup"]
-    ctx.set_timing([])
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    value = T * args.layers / (ms_step / 1e3)
-    gate_avg_ms = gate_t[1] / max(gate_t[0], 1)
-    achieved = GATEUP_FLOP_PER_TOKEN * T / (gate_avg_ms / 1e3) / 1e12
-    # Phase breakdown (separate pass, every phase bracketed).
-    ctx.set_timing("all")
-    for _ in range(2):
-        um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
-    phases = {k: round(v[1] / 2, 4) for k, v in ctx.timings().items() if v[0]}
-    ctx.set_timing([])
-    # FP32-class activations on the same stack.
-    sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        um.block_forward(ctx, layers, x, y, flags=um.FLAG_FP32_CLASS, sync=False)
-    sync()
-    ms_fp32 = (time.perf_counter() - t0) * 1e3 / args.steps
-    layer_s_flop = FLOP_PER_TOKEN * T / (ms_step / args.layers / 1e3) / 1e12
-    log(f"stack: {ms_step:.3f} ms/step, {value:,.0f} layer-tokens/s, gateup {gate_avg_ms:.4f} ms "
-        f"= {achieved:.1f} TFLOP/s; fp32-class {ms_fp32:.3f} ms/step")
-    for l in layers:
-        l.close()
-    del layers, x, y
-    torch.cuda.empty_cache()
+    # --layers 0 skips it (runs that profile only the secondary workloads).
+    host_layer0 = None
+    value = ms_step = achieved = gate_avg_ms = layer_s_flop = ms_fp32 = None
+    phases = {}
+    if args.layers > 0:
+        log("generating the 12-layer stack (T=4096, 80% to 8 hot experts)")
+        hot = syn.route_profile(syn.hot_share(E, K, 8, 0.8), K)
+        layers, host_layer0 = [], None
+        for l in range(args.layers):
+            w = syn.moe_weights_device(H, I, E, SH, seed=1000 + l, router_scale=hot, norm=True)
+            torch.cuda.synchronize()  # the library copies on its own stream
+            layers.append(um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE))
+            if l == 0 and args.cpu_sample > 0:
+                host_layer0 = {k: v.cpu().numpy().view(np.uint16) for k, v in w.items()}
+            del w
+        torch.cuda.empty_cache()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(1)
+        T = 4096
+        x = torch.randn((T, H), generator=g, device="cuda")
+        y = torch.empty_like(x)
+        flags = um.FLAG_BF16_ACTIVATIONS
+        sync()
+        for _ in range(args.warmup):
+            um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
+        sync()
+        # Timed region: K steps; events bracket only the dominant kernel.
+        ctx.set_timing(["gateup"])
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
+        sync()
+        t1 = time.perf_counter()
+        gate_t = ctx.timings()["gateup"]
+        ctx.set_timing([])
+        ms_step = (t1 - t0) * 1e3 / args.steps
+        value = T * args.layers / (ms_step / 1e3)
+        gate_avg_ms = gate_t[1] / max(gate_t[0], 1)
+        achieved = GATEUP_FLOP_PER_TOKEN * T / (gate_avg_ms / 1e3) / 1e12
+        # Phase breakdown (separate pass, every phase bracketed).
+        ctx.set_timing("all")
+        for _ in range(2):
+            um.block_forward(ctx, layers, x, y, flags=flags, sync=False)
+        phases = {k: round(v[1] / 2, 4) for k, v in ctx.timings().items() if v[0]}
+        ctx.set_timing([])
+        # FP32-class activations on the same stack.
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            um.block_forward(ctx, layers, x, y, flags=um.FLAG_FP32_CLASS, sync=False)
+        sync()
+        ms_fp32 = (time.perf_counter() - t0) * 1e3 / args.steps
+        layer_s_flop = FLOP_PER_TOKEN * T / (ms_step / args.layers / 1e3) / 1e12
+        log(f"stack: {ms_step:.3f} ms/step, {value:,.0f} layer-tokens/s, gateup {gate_avg_ms:.4f} ms "
+            f"= {achieved:.1f} TFLOP/s; fp32-class {ms_fp32:.3f} ms/step")
+        for l in layers:
+            l.close()
+        del layers, x, y
+        torch.cuda.empty_cache()
     if args.profile_copy:
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -281,12 +286,12 @@ def main():
 
     result = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": round(value, 1) if value else None,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "ms_per_step": round(ms_step, 4) if ms_step else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -298,13 +303,14 @@ def main():
                    "activations": "bf16 operands, fp32 accumulate (2e-2 class)",
                    "value_is": f"4096 tokens x {args.layers} layers / step time",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "mfma_group_kernel gate/up (SiLU-gated), one launch per layer",
-                     "kernel_ms": round(gate_avg_ms, 4),
-                     "layer_frac": round(layer_s_flop / BF16_PEAK_TFLOPS, 4)},
-        "fp32_class_ms_per_step": round(ms_fp32, 4),
+        "roofline": None if value is None else {
+            "bound": "mfma", "achieved": round(achieved, 2),
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "mfma_group_kernel gate/up (SiLU-gated), one launch per layer",
+            "kernel_ms": round(gate_avg_ms, 4),
+            "layer_frac": round(layer_s_flop / BF16_PEAK_TFLOPS, 4)},
+        "fp32_class_ms_per_step": round(ms_fp32, 4) if ms_fp32 else None,
         "phases_ms_per_step": phases,
         "cpu_baseline": cpu,
         "secondary": secondary,

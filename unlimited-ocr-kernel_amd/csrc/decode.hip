@@ -282,42 +282,40 @@ __global__ __launch_bounds__(64) void decode_stage1_kernel(DeviceLayer L, Scratc
 template <int KIND, int KH>
 __global__ __launch_bounds__(64) void decode_stage2_kernel(DeviceLayer L, Scratch S) {
   __shared__ __align__(16) RowSmem sm;
+  __shared__ __align__(16) RouteSmem rs;
   const int lane = threadIdx.x;
   const int q = lane >> 4;
   const int per_expert = L.I / 4;
   const int nrouted = L.K * per_expert;
   const int b = blockIdx.x;
   if (b < nrouted) {
+    // The logit load goes first: routing waits for it alone, while the
+    // activation row is still in flight.
+    const float logit = lane < L.E ? S.logits[lane] : 0.0f;
     RowStage<KH> X;
     load_row(X, S.xn, L.H, lane);
-    const float logit = lane < L.E ? S.logits[lane] : 0.0f;
-    const WaveRoute r = route_wave(logit, L.E, L.K, L.normalize, L.scale);
-    // Ascending rank of each selected expert: its slot in the dispatch.
-    int rank = 0;
-    for (int m = 0; m < L.K; m++) rank += __shfl(r.id, m) < r.id ? 1 : 0;
+    const LdsRoute r = route_lds(logit, L.E, L.K, rs);
     const int slot = b / per_expert;
-    const unsigned long long hit = __ballot(lane < L.K && rank == slot);
-    const int g = clamp_group(
-        __builtin_amdgcn_readfirstlane(__shfl(r.id, __ffsll((long long)hit) - 1)), L.E);
+    const int g = clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(r.mask, slot)), L.E);
     const int k = 4 * (b - slot * per_expert) + q;
     const int ra = gate_row(k);
     RowPair<KIND, KH> P;
     issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
     if (b == 0) {
+      const float w = route_lds_weight(r, L.K, L.normalize, L.scale, rs);
       if (!r.ok && lane == 0) raise_error(S.err, kErrNumerical);
-      if (lane < L.K) {
-        S.topk_ids[lane] = r.id;
-        S.topk_w[lane] = r.w;
-        S.perm_rows[rank] = 0;
-        S.perm_w[rank] = r.w;
-        S.inv_pos[lane] = rank;
-        S.tiles[2 * rank] = r.id;
-        S.tiles[2 * rank + 1] = 0;
+      const unsigned long long below_mask = r.mask & ((1ull << lane) - 1ull);
+      const int asc = __popcll(below_mask);  // ascending slot / selected ids below lane
+      if ((r.mask >> lane) & 1ull) {
+        S.topk_ids[r.rank] = lane;
+        S.topk_w[r.rank] = w;
+        S.inv_pos[r.rank] = asc;
+        S.perm_rows[asc] = 0;
+        S.perm_w[asc] = w;
+        S.tiles[2 * asc] = lane;
+        S.tiles[2 * asc + 1] = 0;
       }
-      // offsets[e] = number of selected experts with id < e.
-      int below = 0;
-      for (int m = 0; m < L.K; m++) below += __shfl(r.id, m) < lane ? 1 : 0;
-      if (lane < L.E) S.offsets[lane] = below;
+      if (lane < L.E) S.offsets[lane] = asc;
       if (lane == 0) {
         S.offsets[L.E] = L.K;
         S.tiles[2 * L.K] = L.E;
@@ -376,12 +374,19 @@ __global__ __launch_bounds__(64 * kMaxK) void decode_stage3_kernel(DeviceLayer L
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int f0 = 8 * blockIdx.x;
+  // Hidden row first, then the expert id (scalar load) and its weights;
+  // the combine inputs are loaded now and used last.
+  RowStage<kNarrow> Hr;
+  load_row(Hr, S.gu + (size_t)wave * L.I, L.I, lane);
   const int g = clamp_group(__builtin_amdgcn_readfirstlane(S.tiles[2 * wave]), L.E);
   const int ra = f0 + q, rb = ra + 4;
   RowPair<KIND, kNarrow> P;
   issue_rows(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, ra, rb);
-  RowStage<kNarrow> Hr;
-  load_row(Hr, S.gu + (size_t)wave * L.I, L.I, lane);
+  const float ys_f = S.ys[f0 + (lane & 7)];
+  const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
+  float pw[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; j++) pw[j] = j < L.K ? S.perm_w[j] : 0.0f;
   store_row(Hr, sm.hl[wave], L.I, lane);
   __syncthreads();
   if constexpr (KIND == kW8A8) {
@@ -396,11 +401,12 @@ __global__ __launch_bounds__(64 * kMaxK) void decode_stage3_kernel(DeviceLayer L
   }
   __syncthreads();
   if (wave == 0 && lane < 8) {
-    const int f = f0 + lane;
-    float acc = S.ys[f];
-    for (int j = 0; j < L.K; j++) acc = acc + S.perm_w[j] * sm.yl[j][lane];
-    if (residual) acc = residual[f] + acc;
-    out[f] = acc;
+    float acc = ys_f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; j++)
+      if (j < L.K) acc = acc + pw[j] * sm.yl[j][lane];
+    if (residual) acc = res_f + acc;
+    out[f0 + lane] = acc;
   }
 }
 

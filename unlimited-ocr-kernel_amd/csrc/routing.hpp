@@ -58,3 +58,86 @@ __device__ inline WaveRoute route_wave(float v, int n, int K, int normalize, flo
 }
 
 }  // namespace uocr
+
+namespace uocr {
+
+// LDS staging for route_lds (one token per wave).
+struct RouteSmem {
+  float v[64];
+  unsigned long long key[64];
+  float selp[64];
+};
+
+struct LdsRoute {
+  bool ok;                   // false: non-finite logits (then ids 0..K-1, weights 0)
+  int rank;                  // this lane's position in (probability desc, id asc)
+  float p;                   // this lane's probability
+  unsigned long long mask;   // bit e set: expert e selected
+};
+
+// The same routing as route_wave with every reduction done through LDS, for
+// a workgroup of exactly one wave: the maximum and the softmax sum are read
+// back sequentially (expert 0 first, the order of ops::softmax), and each
+// lane's rank is the number of larger (probability, -id) keys. v holds the
+// lane's logit (lanes >= n unused).
+__device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  sm.v[lane] = lane < n ? v : 0.0f;
+  __syncthreads();
+  float m = -INFINITY;
+  bool bad = false;
+  for (int e = 0; e < n; e++) {
+    const float u = sm.v[e];
+    bad |= isnan(u) || u == INFINITY;
+    m = fmaxf(m, u);
+  }
+  LdsRoute r;
+  if (bad || !isfinite(m)) {
+    r.ok = false;
+    r.rank = lane;
+    r.p = 0.0f;
+    r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
+    return r;
+  }
+  const float ex = lane < n ? expf(v - m) : 0.0f;
+  __syncthreads();
+  sm.v[lane] = ex;
+  __syncthreads();
+  float sum = -0.0f;
+  for (int e = 0; e < n; e++) sum += sm.v[e];
+  const float p = ex / sum;
+  const unsigned long long key =
+      lane < n ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane)
+               : 0ull;
+  sm.key[lane] = key;
+  __syncthreads();
+  int rank = 0;
+  for (int e = 0; e < 64; e++) rank += sm.key[e] > key ? 1 : 0;
+  r.ok = true;
+  r.rank = rank;
+  r.p = p;
+  r.mask = __ballot(lane < n && rank < K);
+  return r;
+}
+
+// Routing weights of the selected lanes (route_lds ranks < K): the
+// renormalisation sums the top-k probabilities in selection order
+// (src/decoder/moe.rs:21-25), then scales (:26-28).
+__device__ inline float route_lds_weight(const LdsRoute& r, int K, int normalize, float scale,
+                                         RouteSmem& sm) {
+  if (!r.ok) return 0.0f;
+  if (r.rank < K) sm.selp[r.rank] = r.p;
+  __syncthreads();
+  float den = -0.0f;
+  for (int j = 0; j < K; j++) den += sm.selp[j];
+  den = normalize ? den + 1e-20f : 1.0f;
+  return r.p / den * scale;
+}
+
+// Expert of ascending slot s (the s-th set bit of the selection mask).
+__device__ __forceinline__ int slot_expert(unsigned long long mask, int s) {
+  for (int i = 0; i < s; i++) mask &= mask - 1;
+  return __ffsll((long long)mask) - 1;
+}
+
+}  // namespace uocr
