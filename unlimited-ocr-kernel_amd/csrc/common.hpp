@@ -41,6 +41,21 @@ __device__ __forceinline__ float group16_sum(float v) {
   return v;
 }
 
+// The same sum with DPP lane moves inside each 16-lane row (no LDS
+// crossbar): quad swaps, then the half-row and row mirrors; every lane of
+// the row ends with the row's sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return v;
+}
+
 __device__ __forceinline__ void raise_error(int* err, int code) {
   if (err) atomicMax(err, code);
 }

@@ -88,14 +88,17 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)rows * row_bytes);
   const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes : kOut;
   const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes : kOut;
+  if constexpr (KIND == kBF16) {
 #pragma unroll
-  for (int m = 0; m < RP::kC; m++) {
-    const int c = j + kLpr * m;
-    const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
-    P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
-    P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
-  }
-  if constexpr (KIND != kBF16) {
+    for (int m = 0; m < RP::kC; m++) {
+      const int c = j + kLpr * m;
+      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
+    }
+  } else {
+    // Each chunk's scales are issued with its weights, so chunk m can be
+    // used as soon as its four loads are back.
     const int nblk = K / kQBlock;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)rows * nblk * 4u);
     const uint32_t sa = ra >= 0 && ra < rows ? (uint32_t)ra * nblk * 4u : kOut;
@@ -103,7 +106,10 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
 #pragma unroll
     for (int m = 0; m < RP::kC; m++) {
       const int c = j + kLpr * m;
+      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
       const uint32_t bo = c < nchunks ? (uint32_t)(c >> 1) * 4u : kOut;
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
       P.sa[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sa + bo, 0, 0));
       P.sb[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sb + bo, 0, 0));
     }
@@ -171,8 +177,8 @@ __device__ __forceinline__ void dot_rows(const RowPair<KIND, KMAX>& P, int K, co
       }
     }
   }
-  r0 = group16_sum(a0);
-  r1 = group16_sum(a1);
+  r0 = row16_sum(a0);
+  r1 = row16_sum(a1);
 }
 
 // An FP32 row of n <= N values (n % 4 == 0) held in registers of one wave

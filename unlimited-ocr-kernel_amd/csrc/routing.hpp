@@ -63,8 +63,8 @@ namespace uocr {
 
 // LDS staging for route_lds (one token per wave).
 struct RouteSmem {
-  float v[64];
-  unsigned long long key[64];
+  __attribute__((aligned(16))) float v[64];
+  __attribute__((aligned(16))) unsigned long long key[64];
   float selp[64];
 };
 
@@ -82,14 +82,21 @@ struct LdsRoute {
 // lane's logit (lanes >= n unused).
 __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
   const int lane = threadIdx.x & 63;
-  sm.v[lane] = lane < n ? v : 0.0f;
+  // Every pass reads all 64 entries with the loop fully unrolled (reads in
+  // flight together); padding entries are neutral: -inf for the maximum,
+  // +0 for the sum (adding +0 to a positive sum changes nothing), key 0 for
+  // the ranks.
+  sm.v[lane] = lane < n ? v : -INFINITY;
   __syncthreads();
   float m = -INFINITY;
   bool bad = false;
-  for (int e = 0; e < n; e++) {
-    const float u = sm.v[e];
-    bad |= isnan(u) || u == INFINITY;
-    m = fmaxf(m, u);
+#pragma unroll
+  for (int e = 0; e < 64; e += 4) {
+    const float4 u = *reinterpret_cast<const float4*>(&sm.v[e]);
+    bad |= isnan(u.x) || u.x == INFINITY || isnan(u.y) || u.y == INFINITY;
+    bad |= isnan(u.z) || u.z == INFINITY || isnan(u.w) || u.w == INFINITY;
+    m = fmaxf(fmaxf(m, u.x), u.y);
+    m = fmaxf(fmaxf(m, u.z), u.w);
   }
   LdsRoute r;
   if (bad || !isfinite(m)) {
@@ -104,7 +111,14 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
   sm.v[lane] = ex;
   __syncthreads();
   float sum = -0.0f;
-  for (int e = 0; e < n; e++) sum += sm.v[e];
+#pragma unroll
+  for (int e = 0; e < 64; e += 4) {
+    const float4 u = *reinterpret_cast<const float4*>(&sm.v[e]);
+    sum += u.x;
+    sum += u.y;
+    sum += u.z;
+    sum += u.w;
+  }
   const float p = ex / sum;
   const unsigned long long key =
       lane < n ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane)
@@ -112,7 +126,11 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
   sm.key[lane] = key;
   __syncthreads();
   int rank = 0;
-  for (int e = 0; e < 64; e++) rank += sm.key[e] > key ? 1 : 0;
+#pragma unroll
+  for (int e = 0; e < 64; e += 2) {
+    const ulonglong2 u = *reinterpret_cast<const ulonglong2*>(&sm.key[e]);
+    rank += (u.x > key ? 1 : 0) + (u.y > key ? 1 : 0);
+  }
   r.ok = true;
   r.rank = rank;
   r.p = p;
