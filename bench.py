@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--secondary", default="decode_int8,decode_bf16,prefill1024",
+    ap.add_argument("--secondary", default="decode_int8,decode_bf16,decode_int8_t16,prefill1024",
                     help="comma list of secondary workloads, or 'none'")
     ap.add_argument("--cpu-sample", type=int, default=512,
                     help="tokens of the headline workload timed on the CPU oracle (0: skip)")
@@ -64,16 +64,16 @@ def expert_bytes_int8(rows, cols):
     return rows * cols + rows * (cols // 32) * 4
 
 
-def decode_bytes(int8: bool, unique_experts: int) -> int:
-    """Algorithmic HBM bytes of one decode token-layer: unique active experts,
-    shared expert, router, x and y."""
+def decode_bytes(int8: bool, unique_experts: float, T: int = 1) -> float:
+    """Algorithmic HBM bytes of one small-batch layer call: unique active
+    experts, shared expert, router, x and y."""
     if int8:
         ex = 2 * expert_bytes_int8(I, H) + expert_bytes_int8(H, I)
         sh = 2 * expert_bytes_int8(S, H) + expert_bytes_int8(H, S)
     else:
         ex = 3 * I * H * 2
         sh = 3 * S * H * 2
-    return unique_experts * ex + sh + ROUTER_BYTES + 2 * H * 4
+    return unique_experts * ex + sh + ROUTER_BYTES + 2 * T * H * 4
 
 
 def main():
@@ -169,30 +169,37 @@ def main():
     wanted = [] if args.secondary == "none" else args.secondary.split(",")
 
     # ------------------------------------------------------------- decode
-    def decode(int8: bool):
-        name = "decode-int8-T1" if int8 else "decode-bf16-T1"
+    def decode(quant: int, T: int):
+        kind = {um.QUANT_NONE: "bf16", um.QUANT_WEIGHTS_ONLY: "int8",
+                um.QUANT_DYNAMIC: "w8a8"}[quant]
+        name = f"decode-{kind}-T{T}"
         log(f"{name}: 12 distinct layers, rotating")
         dl = []
         for l in range(12):
             w = syn.moe_weights_device(H, I, E, SH, seed=l)
             torch.cuda.synchronize()
             layer = um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE)
-            if int8:
+            if quant != um.QUANT_NONE:
                 q = syn.int8_overlay_device(H, I, E, SH, seed=100 + l)
                 torch.cuda.synchronize()
-                layer.attach_int8(ctx, q, um.MEMORY_DEVICE, um.QUANT_WEIGHTS_ONLY)
+                layer.attach_int8(ctx, q, um.MEMORY_DEVICE, quant)
                 del q
             del w
             dl.append(layer)
         torch.cuda.empty_cache()
         gen = torch.Generator(device="cuda")
         gen.manual_seed(0)
-        xs = torch.randn((64, 1, H), generator=gen, device="cuda")
+        xs = torch.randn((64, T, H), generator=gen, device="cuda")
         ys = torch.empty_like(xs)
-        steps = max(args.steps, 1) * 24
-        sync()
+        # Unique experts each call touches (algorithmic bytes), from one
+        # traced pass over the same (layer, input) pairs as the timing.
+        ids = torch.empty((T, K), dtype=torch.int32, device="cuda")
+        uniq = []
         for i in range(24):
-            um.forward(ctx, dl[i % 12], xs[i % 64], ys[i % 64], sync=False)
+            um.forward(ctx, dl[i % 12], xs[i % 64], ys[i % 64], trace={"topk_ids": ids})
+            uniq.append(len(set(ids.flatten().tolist())))
+        n_uniq = statistics.mean(uniq)
+        steps = max(args.steps, 1) * 24
         sync()
         t0 = time.perf_counter()
         for i in range(steps):
@@ -206,27 +213,27 @@ def main():
         ph = ctx.timings()
         ctx.set_timing([])
         gpu_ms = sum(v[1] for v in ph.values()) / steps
-        gate = ph["gateup"]
         for l in dl:
             l.close()
         torch.cuda.empty_cache()
-        nbytes = decode_bytes(int8, K)
-        out = {"workload": name, "tokens": 1, "layers_rotated": 12,
-               "value": round(1e3 / wall_ms, 1), "unit": "tokens/s (one layer)",
-               "ms_per_token_layer": round(wall_ms, 4),
+        nbytes = decode_bytes(quant != um.QUANT_NONE, n_uniq, T)
+        out = {"workload": name, "tokens": T, "layers_rotated": 12,
+               "value": round(T * 1e3 / wall_ms, 1), "unit": "tokens/s (one layer)",
+               "ms_per_call": round(wall_ms, 4),
                "kernel_ms_sum": round(gpu_ms, 4),
-               "algorithmic_bytes": nbytes,
+               "unique_experts": round(n_uniq, 2),
+               "algorithmic_bytes": int(nbytes),
                "hbm_frac_wall": round(nbytes / (wall_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-               "hbm_frac_kernels": round(nbytes / (gpu_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                "phases_ms": {k: round(v[1] / steps, 5) for k, v in ph.items() if v[0]}}
-        log(f"{name}: {wall_ms*1e3:.1f} us wall, kernels {gpu_ms*1e3:.1f} us, "
-            f"gateup {gate[1]/max(gate[0],1)*1e3:.1f} us")
+        log(f"{name}: {wall_ms*1e3:.1f} us wall ({n_uniq:.1f} experts), kernels "
+            f"{gpu_ms*1e3:.1f} us with events")
         return out
 
-    if "decode_int8" in wanted:
-        secondary.append(decode(True))
-    if "decode_bf16" in wanted:
-        secondary.append(decode(False))
+    for key, quant, T in (("decode_int8", um.QUANT_WEIGHTS_ONLY, 1),
+                          ("decode_bf16", um.QUANT_NONE, 1),
+                          ("decode_int8_t16", um.QUANT_WEIGHTS_ONLY, 16)):
+        if key in wanted:
+            secondary.append(decode(quant, T))
 
     # ------------------------------------------------------ 1024-token Zipf
     if "prefill1024" in wanted:

@@ -66,7 +66,6 @@ struct uocr_gpu_ctx {
   size_t scratch_limit = 0;
   int* err = nullptr;       // device error flag
   int* err_host = nullptr;  // pinned readback
-  int* sync = nullptr;      // election counters (zero between forwards)
   // Phase timing: bit i of timing_mask enables phase i.
   uint32_t timing_mask = 0;
   std::vector<hipEvent_t> free_events;
@@ -197,7 +196,6 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.xb = reinterpret_cast<uint16_t*>(b + p.xb);
   s.gu = reinterpret_cast<float*>(b + p.gu);
   s.err = ctx->err;
-  s.sync = ctx->sync;
   return s;
 }
 
@@ -276,8 +274,9 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
   hipStream_t st = ctx->stream;
-  // Engine: the row-chunk GEMV engine for small batches (bandwidth-bound),
-  // the MFMA grouped GEMM for larger BF16 batches.
+  // Engines: the one-token decode engine; the small-batch engine (row tiles
+  // of <= 16 tokens, bandwidth-bound) for T <= 16 and for INT8 weights; the
+  // MFMA grouped GEMM for larger BF16 batches.
   bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
               (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
   if (L.quant_mode != UOCR_QUANT_NONE) {
@@ -285,14 +284,14 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       return fail(UOCR_ERR_UNSUPPORTED, "the MFMA engine takes BF16 weights only");
     mfma = false;
   }
+  if (!mfma && !uocr::batch_supported(L))
+    return fail(UOCR_ERR_UNSUPPORTED, "small-batch engine needs hidden and shared widths <= 2048");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
-  const int bm = mfma ? uocr::kMfmaBM : (T == 1 ? 1 : uocr::kGemvChunk);
+  const int bm = mfma ? uocr::kMfmaBM : uocr::kGemvChunk;
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
-  // The small-batch router holds a router row in registers (H <= 2048).
-  const bool small = !mfma && T <= (size_t)uocr::kGemvChunk && L.H <= 2048;
-  if (small && T == 1 && uocr::decode_supported(L)) {
+  if (!mfma && T == 1 && uocr::decode_supported(L)) {
     // One token: three launches with no routing launch of their own (the
     // router rides with the shared gate/up, top-k with the routed gate/up).
     phase_begin(ctx, kRouter);
@@ -304,20 +303,14 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     phase_begin(ctx, kDown);
     uocr::launch_decode_stage(3, L, S, residual, y, st);
     phase_end(ctx);
-  } else if (small) {
-    // Few tokens: three launches. Router + top-k + dispatch, gate/up, and
-    // down with the ordered combine fused in.
-    phase_begin(ctx, kRouter);
-    uocr::launch_route_small(S.xn, L, S, Ti, bm, st);
-    phase_end(ctx);
-    phase_begin(ctx, kGateUp);
-    uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
-    phase_end(ctx);
-    phase_begin(ctx, kDown);
-    uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, residual, y, st);
-    phase_end(ctx);
   } else {
-    if (T > (size_t)uocr::kGemvChunk) {
+    if (T <= (size_t)uocr::kGemvChunk && !mfma) {
+      // Few tokens: logits with every token staged once, then one
+      // workgroup routes them and builds the dispatch.
+      phase_begin(ctx, kRouter);
+      uocr::launch_small_route(S.xn, L, S, Ti, st);
+      phase_end(ctx);
+    } else if (T > (size_t)uocr::kGemvChunk) {
       // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
       phase_begin(ctx, kRouter);
       uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
@@ -329,6 +322,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
                                     S.tiles, S.counters, st);
       phase_end(ctx);
     } else {
+      // MFMA engine forced on a small batch.
       phase_begin(ctx, kRouter);
       uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
       phase_end(ctx);
@@ -360,10 +354,10 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_end(ctx);
     } else {
       phase_begin(ctx, kGateUp);
-      uocr::launch_gemv_gateup(L, S, Ti, tiles_bound, bm, st);
+      uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);
       phase_begin(ctx, kDown);
-      uocr::launch_gemv_down(L, S, Ti, tiles_bound, bm, nullptr, nullptr, st);
+      uocr::launch_batch_down(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);
     }
     phase_begin(ctx, kCombine);
@@ -412,8 +406,6 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
-  if (e == hipSuccess) e = hipMalloc(&ctx->sync, uocr::kSyncSize * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(ctx->sync, 0, uocr::kSyncSize * sizeof(int));
   if (e != hipSuccess) {
     uocr_gpu_ctx_destroy(ctx);
     return hip_fail(e, "context allocation");
@@ -428,7 +420,6 @@ void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->err) (void)hipFree(ctx->err);
-  if (ctx->sync) (void)hipFree(ctx->sync);
   if (ctx->err_host) (void)hipHostFree(ctx->err_host);
   collect_timings(ctx);
   for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);

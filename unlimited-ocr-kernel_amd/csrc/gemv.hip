@@ -150,109 +150,6 @@ __device__ __forceinline__ void gemv_rows64(const void* __restrict__ wbase,
   }
 }
 
-// One activation row (decode): the same mapping as gemv_rows64, but each
-// wave issues the loads of two row iterations (8 rows) before using them,
-// up to kMaxC chunks per lane per pass, so several kilobytes per wave are in
-// flight at once.
-template <int KIND>
-__device__ __forceinline__ void gemv_rows64_one(const void* __restrict__ wbase,
-                                                const float* __restrict__ sbase, int K,
-                                                int rows_total, int row_begin,
-                                                const float* __restrict__ xl,
-                                                const int8_t* __restrict__ xq,
-                                                const float* __restrict__ xqs, float* out) {
-  constexpr int kElems = KIND == kKindBF16 ? 8 : 16;
-  constexpr int kBytes = KIND == kKindBF16 ? 2 : 1;
-  constexpr int kMaxC = KIND == kKindBF16 ? 14 : 7;  // K <= 1792 in one pass
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int q = lane >> 4;
-  const int j = lane & 15;
-  const int nchunks = K / kElems;
-  const int nblk = K / kQBlock;
-#pragma unroll 1
-  for (int it = 0; it < 4; it += 2) {
-    const int r0 = wave * 16 + it * 4 + q, r1 = r0 + 4;
-    const int row0 = row_begin + r0, row1 = row_begin + r1;
-    const bool ok0 = row0 < rows_total, ok1 = row1 < rows_total;
-    const uint4* w0 = reinterpret_cast<const uint4*>(static_cast<const char*>(wbase) +
-                                                     (size_t)(ok0 ? row0 : 0) * K * kBytes);
-    const uint4* w1 = reinterpret_cast<const uint4*>(static_cast<const char*>(wbase) +
-                                                     (size_t)(ok1 ? row1 : 0) * K * kBytes);
-    float a0 = 0.0f, a1 = 0.0f;
-    for (int c0 = 0; c0 < nchunks; c0 += 16 * kMaxC) {
-      uint4 v0[kMaxC], v1[kMaxC];
-#pragma unroll
-      for (int m = 0; m < kMaxC; m++) {
-        const int c = c0 + j + 16 * m;
-        v0[m] = c < nchunks ? w0[c] : make_uint4(0, 0, 0, 0);
-        v1[m] = c < nchunks ? w1[c] : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int m = 0; m < kMaxC; m++) {
-        const int c = c0 + j + 16 * m;
-        if (c >= nchunks) break;
-        if constexpr (KIND == kKindBF16) {
-          const float4* xp = reinterpret_cast<const float4*>(xl + c * 8);
-          const float4 xa = xp[0], xb = xp[1];
-          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-          const uint32_t u0[4] = {v0[m].x, v0[m].y, v0[m].z, v0[m].w};
-          const uint32_t u1[4] = {v1[m].x, v1[m].y, v1[m].z, v1[m].w};
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            a0 = fmaf(bf16_lo(u0[i]), xv[2 * i], a0);
-            a0 = fmaf(bf16_hi(u0[i]), xv[2 * i + 1], a0);
-            a1 = fmaf(bf16_lo(u1[i]), xv[2 * i], a1);
-            a1 = fmaf(bf16_hi(u1[i]), xv[2 * i + 1], a1);
-          }
-        } else if constexpr (KIND == kKindInt8) {
-          const float s0 = sbase[(size_t)(ok0 ? row0 : 0) * nblk + (c >> 1)];
-          const float s1 = sbase[(size_t)(ok1 ? row1 : 0) * nblk + (c >> 1)];
-          const uint32_t u0[4] = {v0[m].x, v0[m].y, v0[m].z, v0[m].w};
-          const uint32_t u1[4] = {v1[m].x, v1[m].y, v1[m].z, v1[m].w};
-          const float4* xp = reinterpret_cast<const float4*>(xl + c * 16);
-#pragma unroll
-          for (int v4 = 0; v4 < 4; v4++) {
-            const float4 xv = xp[v4];
-            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-              const float d0 = (float)(int8_t)((u0[v4] >> (8 * b)) & 0xff) * s0;
-              const float d1 = (float)(int8_t)((u1[v4] >> (8 * b)) & 0xff) * s1;
-              a0 = fmaf(d0, xs[b], a0);
-              a1 = fmaf(d1, xs[b], a1);
-            }
-          }
-        } else {
-          const int4 xv = *reinterpret_cast<const int4*>(xq + c * 16);
-          int p0 = __builtin_amdgcn_sdot4((int)v0[m].x, xv.x, 0, false);
-          p0 = __builtin_amdgcn_sdot4((int)v0[m].y, xv.y, p0, false);
-          p0 = __builtin_amdgcn_sdot4((int)v0[m].z, xv.z, p0, false);
-          p0 = __builtin_amdgcn_sdot4((int)v0[m].w, xv.w, p0, false);
-          int p1 = __builtin_amdgcn_sdot4((int)v1[m].x, xv.x, 0, false);
-          p1 = __builtin_amdgcn_sdot4((int)v1[m].y, xv.y, p1, false);
-          p1 = __builtin_amdgcn_sdot4((int)v1[m].z, xv.z, p1, false);
-          p1 = __builtin_amdgcn_sdot4((int)v1[m].w, xv.w, p1, false);
-          // Chunks 2b and 2b+1 form block b and sit in lanes j and j^1.
-          const int s0 = p0 + __shfl_xor(p0, 1);
-          const int s1 = p1 + __shfl_xor(p1, 1);
-          if ((j & 1) == 0) {
-            const int b = c >> 1;
-            a0 += (float)s0 * sbase[(size_t)(ok0 ? row0 : 0) * nblk + b] * xqs[b];
-            a1 += (float)s1 * sbase[(size_t)(ok1 ? row1 : 0) * nblk + b] * xqs[b];
-          }
-        }
-      }
-    }
-    const float v0s = group16_sum(a0);
-    const float v1s = group16_sum(a1);
-    if (j == 0) {
-      if (ok0) out[r0] = v0s;
-      if (ok1) out[r1] = v1s;
-    }
-  }
-}
-
 struct GemvLds {
   float* xl;      // [NMAX, Kmax]
   float* out;     // [64, NMAX]
@@ -285,199 +182,6 @@ __device__ void stage_rows(const float* __restrict__ src, const int* __restrict_
     reinterpret_cast<float4*>(xl + (size_t)m * K)[v] =
         reinterpret_cast<const float4*>(src + (size_t)row * K)[v];
   }
-}
-
-template <int NMAX>
-__device__ void gemv_dispatch_kind(int kind, const void* w, const float* s, int K, int rows_total,
-                                   int row_begin, const GemvLds& l, int n) {
-  if constexpr (NMAX == 1) {
-    if (kind == kKindBF16)
-      gemv_rows64_one<kKindBF16>(w, s, K, rows_total, row_begin, l.xl, l.xq, l.xqs, l.out);
-    else if (kind == kKindInt8)
-      gemv_rows64_one<kKindInt8>(w, s, K, rows_total, row_begin, l.xl, l.xq, l.xqs, l.out);
-    else
-      gemv_rows64_one<kKindW8A8>(w, s, K, rows_total, row_begin, l.xl, l.xq, l.xqs, l.out);
-    return;
-  }
-  if (kind == kKindBF16)
-    gemv_rows64<kKindBF16, NMAX>(w, s, K, rows_total, row_begin, l.xl, n, l.xq, l.xqs, l.out,
-                                 nullptr);
-  else if (kind == kKindInt8)
-    gemv_rows64<kKindInt8, NMAX>(w, s, K, rows_total, row_begin, l.xl, n, l.xq, l.xqs, l.out,
-                                 nullptr);
-  else
-    gemv_rows64<kKindW8A8, 1>(w, s, K, rows_total, row_begin, l.xl, 1, l.xq, l.xqs, l.out,
-                              nullptr);
-}
-
-// Gate/up: blockIdx.y = row tile, blockIdx.x = a block of 64 rows of the
-// interleaved gate/up matrix (32 hidden columns). Epilogue: h = silu(g) * u
-// (Decoder::feed_forward, src/decoder/mod.rs:114-122).
-template <int NMAX>
-__global__ __launch_bounds__(256) void gemv_gateup_kernel(DeviceLayer L, Scratch S, int T,
-                                                          int mchunk) {
-  extern __shared__ __align__(16) char smem[];
-  const int tile = blockIdx.y;
-  if (tile >= S.counters[0]) return;
-  const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
-  const int W = L.width(g);
-  const int rb = blockIdx.x;
-  if (rb * 32 >= W) return;
-  const bool routed = g < L.E;
-  const int group_rows = routed ? S.offsets[g + 1] - S.offsets[g] : T;
-  const int n = min(mchunk, group_rows - r0);
-  const int kind = L.quant_mode == 0 ? kKindBF16
-                   : (L.quant_mode == 2 && group_rows == 1) ? kKindW8A8
-                                                            : kKindInt8;
-  GemvLds l = carve_lds<NMAX>(smem, max(L.H, L.S));
-  stage_rows(S.xn, routed ? S.perm_rows : nullptr, routed ? S.offsets[g] + r0 : r0, n, L.H, l.xl);
-  __syncthreads();
-  if (kind == kKindW8A8) {
-    quantize_row_lds(l.xl, L.H, l.xq, l.xqs, S.err);
-    __syncthreads();
-  }
-  const void* w;
-  const float* sc = nullptr;
-  if (kind == kKindBF16) {
-    w = L.w13 + L.w13_offset(g);
-  } else {
-    w = L.q13 + L.w13_offset(g);
-    sc = L.s13 + L.s13_offset(g);
-  }
-  gemv_dispatch_kind<NMAX>(kind, w, sc, L.H, 2 * W, rb * 64, l, n);
-  __syncthreads();
-  const int nm = kind == kKindW8A8 ? 1 : NMAX;
-  for (int i = threadIdx.x; i < 32 * n; i += blockDim.x) {
-    const int col = i & 31, m = i >> 5;
-    const float gv = l.out[col * nm + m];
-    const float uv = l.out[(32 + col) * nm + m];
-    const float h = silu(gv) * uv;
-    if (routed)
-      S.h[(size_t)(S.offsets[g] + r0 + m) * L.I + rb * 32 + col] = h;
-    else
-      S.hs[(size_t)(r0 + m) * L.S + rb * 32 + col] = h;
-  }
-}
-
-// Down: blockIdx.x = a block of 64 output features. With `out` set (small
-// batches), the workgroups of one feature block elect the last to finish
-// (device-scope ticket); it adds the block's contributions in order —
-// shared expert first, then each token's experts in ascending id, one
-// rounded multiply and one rounded add per term (src/decoder/mod.rs:185-194)
-// — adds the residual if any, and resets the ticket.
-template <int NMAX>
-__global__ __launch_bounds__(256) void gemv_down_kernel(DeviceLayer L, Scratch S, int T,
-                                                        int mchunk, const float* residual,
-                                                        float* out) {
-  extern __shared__ __align__(16) char smem[];
-  __shared__ int ticket;
-  __shared__ int spos[kGemvChunk][8];
-  __shared__ float sp[kGemvChunk][8];
-  const int tile = blockIdx.y;
-  const int ntiles = S.counters[0];
-  if (tile >= ntiles) return;
-  const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
-  const int W = L.width(g);
-  const int rb = blockIdx.x;
-  const bool routed = g < L.E;
-  const int group_rows = routed ? S.offsets[g + 1] - S.offsets[g] : T;
-  const int n = min(mchunk, group_rows - r0);
-  const int kind = L.quant_mode == 0 ? kKindBF16
-                   : (L.quant_mode == 2 && group_rows == 1) ? kKindW8A8
-                                                            : kKindInt8;
-  GemvLds l = carve_lds<NMAX>(smem, max(L.H, L.S));
-  if (routed)
-    stage_rows(S.h, nullptr, S.offsets[g] + r0, n, W, l.xl);
-  else
-    stage_rows(S.hs, nullptr, r0, n, W, l.xl);
-  __syncthreads();
-  if (kind == kKindW8A8) {
-    quantize_row_lds(l.xl, W, l.xq, l.xqs, S.err);
-    __syncthreads();
-  }
-  const void* w;
-  const float* sc = nullptr;
-  if (kind == kKindBF16) {
-    w = L.w2 + L.w2_offset(g);
-  } else {
-    w = L.q2 + L.w2_offset(g);
-    sc = L.s2 + L.s2_offset(g);
-  }
-  gemv_dispatch_kind<NMAX>(kind, w, sc, W, L.H, rb * 64, l, n);
-  __syncthreads();
-  const int nm = (NMAX == 1 || kind == kKindW8A8) ? 1 : NMAX;
-  for (int i = threadIdx.x; i < 64 * n; i += blockDim.x) {
-    const int r = i & 63, m = i >> 6;
-    const int feature = rb * 64 + r;
-    if (feature >= L.H) continue;
-    const float v = l.out[r * nm + m];
-    if (routed)
-      S.y[(size_t)(S.offsets[g] + r0 + m) * L.H + feature] = v;
-    else
-      S.ys[(size_t)(r0 + m) * L.H + feature] = v;
-  }
-  if (!out) return;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(&S.sync[kSyncDown + rb], 1);
-  __syncthreads();
-  if (ticket != ntiles - 1) return;
-  __threadfence();
-  if (threadIdx.x == 0) atomicExch(&S.sync[kSyncDown + rb], 0);
-  const int K = L.K;
-  if (threadIdx.x < T) {
-    // This token's experts in ascending id (insertion sort of <= 8).
-    const int t = threadIdx.x;
-    int e[8], pos[8];
-    float p[8];
-    for (int jj = 0; jj < K; jj++) {
-      e[jj] = S.topk_ids[(size_t)t * K + jj];
-      pos[jj] = S.inv_pos[(size_t)t * K + jj];
-      p[jj] = S.topk_w[(size_t)t * K + jj];
-      for (int b = jj; b > 0 && e[b] < e[b - 1]; b--) {
-        int te = e[b]; e[b] = e[b - 1]; e[b - 1] = te;
-        int tp = pos[b]; pos[b] = pos[b - 1]; pos[b - 1] = tp;
-        float tw = p[b]; p[b] = p[b - 1]; p[b - 1] = tw;
-      }
-    }
-    for (int jj = 0; jj < K; jj++) {
-      spos[t][jj] = pos[jj];
-      sp[t][jj] = p[jj];
-    }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < T * 64; i += blockDim.x) {
-    const int t = i >> 6, feature = rb * 64 + (i & 63);
-    if (feature >= L.H) continue;
-    float acc = S.ys[(size_t)t * L.H + feature];
-    for (int jj = 0; jj < K; jj++) acc = acc + sp[t][jj] * S.y[(size_t)spos[t][jj] * L.H + feature];
-    if (residual) acc = residual[(size_t)t * L.H + feature] + acc;
-    out[(size_t)t * L.H + feature] = acc;
-  }
-}
-
-void launch_gemv_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        int mchunk, hipStream_t s) {
-  const int kmax = L.H > L.S ? L.H : L.S;
-  dim3 grid(L.S / 32, tiles_bound);
-  if (mchunk == 1)
-    hipLaunchKernelGGL(gemv_gateup_kernel<1>, grid, dim3(256), gemv_lds_bytes(1, kmax), s, L, S, T,
-                       1);
-  else
-    hipLaunchKernelGGL(gemv_gateup_kernel<kGemvChunk>, grid, dim3(256),
-                       gemv_lds_bytes(kGemvChunk, kmax), s, L, S, T, mchunk);
-}
-
-void launch_gemv_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                      const float* residual, float* out, hipStream_t s) {
-  const int kmax = L.H > L.S ? L.H : L.S;
-  dim3 grid((L.H + 63) / 64, tiles_bound);
-  if (mchunk == 1)
-    hipLaunchKernelGGL(gemv_down_kernel<1>, grid, dim3(256), gemv_lds_bytes(1, kmax), s, L, S, T,
-                       1, residual, out);
-  else
-    hipLaunchKernelGGL(gemv_down_kernel<kGemvChunk>, grid, dim3(256),
-                       gemv_lds_bytes(kGemvChunk, kmax), s, L, S, T, mchunk, residual, out);
 }
 
 // ------------------------------------------------------------- operators
@@ -630,14 +334,6 @@ void gemv_init_attributes() {
   // Largest dynamic LDS any launch here asks for is gemv_lds_bytes(16, 1792)
   // = 118 KiB; static LDS plus this must stay within the 160 KiB per CU.
   const int big = 128 * 1024;
-  (void)hipFuncSetAttribute((const void*)gemv_gateup_kernel<1>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, big);
-  (void)hipFuncSetAttribute((const void*)gemv_gateup_kernel<kGemvChunk>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, big);
-  (void)hipFuncSetAttribute((const void*)gemv_down_kernel<1>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, big);
-  (void)hipFuncSetAttribute((const void*)gemv_down_kernel<kGemvChunk>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, big);
   (void)hipFuncSetAttribute((const void*)op_gemv_kernel<kKindBF16>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, big);
   (void)hipFuncSetAttribute((const void*)op_gemv_kernel<kKindInt8>,

@@ -56,14 +56,7 @@ struct Scratch {
   uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
   float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
   int* err;         // device error flag
-  // Persistent per-context counters for "last workgroup" elections: [0] the
-  // small-batch router, [64 + b] feature block b of the fused down/combine.
-  // Each election resets its counter, so they are zero between forwards.
-  int* sync;
 };
-constexpr int kSyncRouter = 0;
-constexpr int kSyncDown = 64;
-constexpr int kSyncSize = 64 + 1024;
 
 int max_tiles(int T, int K, int E, int bm);
 
@@ -73,10 +66,6 @@ void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E
 void launch_topk(const float* logits, int T, int E, int K, int normalize, float scale, int* ids,
                  float* weights, int* err, hipStream_t s);
 
-// Few tokens (T <= 16): router logits, softmax top-k and the dispatch in one
-// launch (bm = 1 for one token, else 16: one row tile per group).
-void launch_route_small(const float* x, const DeviceLayer& L, const Scratch& S, int T, int bm,
-                        hipStream_t s);
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, int* err, hipStream_t s);
@@ -90,11 +79,18 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
                      int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
                      hipStream_t s);
 
-// gemv.hip: row-chunk engine (FP32 math, INT8 weight-only and W8A8).
-void launch_gemv_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        int mchunk, hipStream_t s);
-void launch_gemv_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                      const float* residual, float* out, hipStream_t s);
+// batch.hip: small-batch expert engine over row tiles of <= 16 tokens (FP32
+// math, INT8 weight-only and W8A8), and the small-batch router (T <= 16):
+// logits, then one workgroup that routes and builds the dispatch.
+bool batch_supported(const DeviceLayer& L);
+void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
+                         int mchunk, hipStream_t s);
+void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
+                       hipStream_t s);
+void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
+                        hipStream_t s);
+
+// gemv.hip: single-matrix operator kernels.
 // Operator entry points (single matrix).
 void launch_linear_bf16(const float* x, int m, int k, const uint16_t* w, int n, float* y,
                         hipStream_t s);

@@ -143,131 +143,6 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
   route_token(v, n, K, normalize, scale, ids + (size_t)t * K, weights + (size_t)t * K, err);
 }
 
-// Few tokens (T <= 16), one launch. Wave w of workgroup b computes expert
-// 4b + w's logits for every token (one coalesced pass over its router row).
-// The workgroups then elect the last one to finish through a device-scope
-// ticket (release fence, atomic add, acquire fence); it routes every token
-// and builds the dispatch: per-expert counts, offsets, the stable
-// (expert, token) permutation and one row tile per group. The ticket is
-// reset by the elected workgroup, so it is zero again for the next forward.
-constexpr int kSmallT = 16;
-
-__global__ __launch_bounds__(256) void route_small_kernel(const float* __restrict__ x,
-                                                          DeviceLayer L, Scratch S, int T,
-                                                          int bm) {
-  __shared__ int ticket;
-  __shared__ int idl[kSmallT * 8];
-  __shared__ float wl[kSmallT * 8];
-  __shared__ int offl[64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int H = L.H, E = L.E, K = L.K;
-  const int e = blockIdx.x * 4 + wave;
-  if (e < E) {
-    // The router row (H <= 2048: <= 16 bf16 pairs per lane) is loaded once,
-    // all at once; each token's activations likewise.
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(L.router + (size_t)e * H);
-    const int np = H / 2;
-    uint32_t wr[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int p = lane + 64 * i;
-      if (p < np) wr[i] = row[p];
-    }
-    for (int t = 0; t < T; t++) {
-      const float2* xr = reinterpret_cast<const float2*>(x + (size_t)t * H);
-      float2 xv[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int p = lane + 64 * i;
-        if (p < np) xv[i] = xr[p];
-      }
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int p = lane + 64 * i;
-        if (p < np) {
-          acc = fmaf(bf16_lo(wr[i]), xv[i].x, acc);
-          acc = fmaf(bf16_hi(wr[i]), xv[i].y, acc);
-        }
-      }
-      acc = wave_sum(acc);
-      if (lane == 0) S.logits[(size_t)t * E + e] = acc;
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(&S.sync[kSyncRouter], 1);
-  __syncthreads();
-  if (ticket != (int)gridDim.x - 1) return;
-  __threadfence();
-  if (threadIdx.x == 0) atomicExch(&S.sync[kSyncRouter], 0);
-  for (int t = wave; t < T; t += 4) {
-    const float v = lane < E ? S.logits[(size_t)t * E + lane] : -INFINITY;
-    route_token(v, E, K, L.normalize, L.scale, S.topk_ids + (size_t)t * K,
-                S.topk_w + (size_t)t * K, S.err);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < T * K; i += blockDim.x) {
-    idl[i] = S.topk_ids[i];
-    wl[i] = S.topk_w[i];
-  }
-  __syncthreads();
-  if (wave == 0) {
-    int c = 0;
-    for (int i = 0; i < T * K; i++) c += idl[i] == lane;
-    int incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
-    }
-    const int off = incl - c;
-    offl[lane] = off;
-    if (lane < E) S.offsets[lane] = off;
-    if (lane == 0) S.offsets[E] = T * K;
-    const int nt = lane < E ? (c + bm - 1) / bm : 0;
-    int tincl = nt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(tincl, o);
-      if (lane >= o) tincl += v;
-    }
-    for (int i = 0; i < nt; i++) {
-      S.tiles[2 * (tincl - nt + i)] = lane;
-      S.tiles[2 * (tincl - nt + i) + 1] = i * bm;
-    }
-    const int routed_tiles = __shfl(tincl, 63);
-    const int shared_tiles = (T + bm - 1) / bm;
-    for (int i = lane; i < shared_tiles; i += 64) {
-      S.tiles[2 * (routed_tiles + i)] = E;
-      S.tiles[2 * (routed_tiles + i) + 1] = i * bm;
-    }
-    if (lane == 0) {
-      S.counters[0] = routed_tiles + shared_tiles;
-      S.counters[1] = routed_tiles;
-    }
-  }
-  __syncthreads();
-  // Stable positions: a token's rank within its expert is the number of
-  // earlier tokens routed to the same expert (ids of one token are distinct).
-  for (int i = threadIdx.x; i < T * K; i += blockDim.x) {
-    const int t = i / K, ex = idl[i];
-    int r = 0;
-    for (int u = 0; u < t * K; u++) r += idl[u] == ex;
-    const int pos = offl[ex] + r;
-    S.perm_rows[pos] = t;
-    S.perm_w[pos] = wl[i];
-    S.inv_pos[i] = pos;
-  }
-}
-
-void launch_route_small(const float* x, const DeviceLayer& L, const Scratch& S, int T, int bm,
-                        hipStream_t s) {
-  if (T <= 0) return;
-  hipLaunchKernelGGL(route_small_kernel, dim3((L.E + 3) / 4), dim3(256), 0, s, x, L, S, T, bm);
-}
-
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 

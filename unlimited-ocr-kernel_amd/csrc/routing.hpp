@@ -79,7 +79,8 @@ struct LdsRoute {
 // a workgroup of exactly one wave: the maximum and the softmax sum are read
 // back sequentially (expert 0 first, the order of ops::softmax), and each
 // lane's rank is the number of larger (probability, -id) keys. v holds the
-// lane's logit (lanes >= n unused).
+// lane's logit (lanes >= n unused). Every wave of the workgroup must call it
+// (it synchronises the workgroup); each wave passes its own RouteSmem.
 __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
   const int lane = threadIdx.x & 63;
   // Every pass reads all 64 entries with the loop fully unrolled (reads in
@@ -98,17 +99,12 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
     m = fmaxf(fmaxf(m, u.x), u.y);
     m = fmaxf(fmaxf(m, u.z), u.w);
   }
-  LdsRoute r;
-  if (bad || !isfinite(m)) {
-    r.ok = false;
-    r.rank = lane;
-    r.p = 0.0f;
-    r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
-    return r;
-  }
-  const float ex = lane < n ? expf(v - m) : 0.0f;
+  // Every wave passes every barrier below whatever its logits: a wave with
+  // non-finite logits computes on neutral values and reports !ok.
+  const bool ok = !bad && isfinite(m);
+  const float ex = ok && lane < n ? expf(v - m) : 0.0f;
   __syncthreads();
-  sm.v[lane] = ex;
+  sm.v[lane] = ok ? ex : 1.0f;
   __syncthreads();
   float sum = -0.0f;
 #pragma unroll
@@ -131,6 +127,15 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
     const ulonglong2 u = *reinterpret_cast<const ulonglong2*>(&sm.key[e]);
     rank += (u.x > key ? 1 : 0) + (u.y > key ? 1 : 0);
   }
+  LdsRoute r;
+  if (!ok) {
+    // Distinct ids 0..K-1 with weight 0 keep any dispatch a permutation.
+    r.ok = false;
+    r.rank = lane;
+    r.p = 0.0f;
+    r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
+    return r;
+  }
   r.ok = true;
   r.rank = rank;
   r.p = p;
@@ -143,9 +148,9 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
 // (src/decoder/moe.rs:21-25), then scales (:26-28).
 __device__ inline float route_lds_weight(const LdsRoute& r, int K, int normalize, float scale,
                                          RouteSmem& sm) {
-  if (!r.ok) return 0.0f;
-  if (r.rank < K) sm.selp[r.rank] = r.p;
+  if (r.ok && r.rank < K) sm.selp[r.rank] = r.p;
   __syncthreads();
+  if (!r.ok) return 0.0f;
   float den = -0.0f;
   for (int j = 0; j < K; j++) den += sm.selp[j];
   den = normalize ? den + 1e-20f : 1.0f;

@@ -1,0 +1,296 @@
+// Row-dot building blocks shared by the small-batch expert engines: two
+// weight rows per lane (16 lanes per row, 8 rows per wave), every 16-byte
+// chunk loaded with a range-checked buffer load before any is used.
+//
+// Arithmetic is that of Decoder::projection (src/decoder/mod.rs:99-112):
+// BF16 weights widened exactly; INT8 weight-only as the rounded product
+// w * scale dotted in FP32 (src/cpu/quantized.rs:119-131); W8A8 with the
+// activation row quantised per 32-block and exact i32 block sums
+// (src/cpu/quantized.rs:155-236). Only the FP32 summation order differs.
+#pragma once
+
+#include "common.hpp"
+
+namespace uocr {
+
+enum { kBF16 = 0, kInt8 = 1, kW8A8 = 2 };
+constexpr int kLpr = 16;  // lanes per weight row
+// Offset marker past every buffer (buffers are < 1 GiB, so a sum of two
+// markers stays out of range too).
+constexpr uint32_t kOut = 0x40000000u;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // Raw buffer: stride 0, range-checked against `bytes` (gfx9 word 3).
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Quantise an FP32 row held in LDS per 32-block (Int8Matrix::quantize,
+// src/cpu/quantized.rs:43-74) with the 64 lanes of one wave; non-finite
+// input or an underflowing scale raises Numerical.
+__device__ inline void quantize_lds(const float* xl, int K, int8_t* xq, float* xs, int lane, int* err) {
+  for (int b = lane; b < K / kQBlock; b += 64) {
+    const float* v = xl + b * kQBlock;
+    float maximum = 0.0f;
+    bool bad = false;
+    for (int i = 0; i < kQBlock; i++) {
+      bad |= !isfinite(v[i]);
+      maximum = fmaxf(maximum, fabsf(v[i]));
+    }
+    const float scale = maximum / 127.0f;
+    if (bad || (maximum > 0.0f && scale == 0.0f)) raise_error(err, kErrNumerical);
+    xs[b] = scale;
+    for (int i = 0; i < kQBlock; i++) {
+      int q = 0;
+      if (scale != 0.0f) q = (int)fminf(fmaxf(rintf(v[i] / scale), -127.0f), 127.0f);
+      xq[b * kQBlock + i] = (int8_t)q;
+    }
+  }
+}
+
+// 16-byte weight chunks of two rows, ra and rb, of a row-major [rows, K]
+// matrix with K <= KMAX: the lane takes chunks j, j + 16, ... of both rows
+// (j = lane % 16), so the four 16-lane groups of a wave cover 8 rows.
+template <int KIND, int KMAX>
+struct RowPair {
+  static constexpr int kElems = KIND == kBF16 ? 8 : 16;   // elements per chunk
+  static constexpr int kC = KMAX / kElems / kLpr;          // chunks per lane per row
+  u32x4 wa[kC], wb[kC];
+  float sa[kC], sb[kC];
+};
+
+// Issues every load of a RowPair. Rows outside [0, rows) and chunks past K
+// read as zero; `w` / `s` are the matrix and (INT8) its [rows, K/32] scales.
+template <int KIND, int KMAX>
+__device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w, const float* s,
+                                           int rows, int K, int ra, int rb) {
+  using RP = RowPair<KIND, KMAX>;
+  constexpr int kBytes = KIND == kBF16 ? 2 : 1;
+  const int j = threadIdx.x & (kLpr - 1);
+  const int nchunks = K / RP::kElems;
+  const uint32_t row_bytes = (uint32_t)K * kBytes;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)rows * row_bytes);
+  const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes : kOut;
+  const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes : kOut;
+  if constexpr (KIND == kBF16) {
+#pragma unroll
+    for (int m = 0; m < RP::kC; m++) {
+      const int c = j + kLpr * m;
+      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
+    }
+  } else {
+    // Each chunk's scales are issued with its weights, so chunk m can be
+    // used as soon as its four loads are back.
+    const int nblk = K / kQBlock;
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)rows * nblk * 4u);
+    const uint32_t sa = ra >= 0 && ra < rows ? (uint32_t)ra * nblk * 4u : kOut;
+    const uint32_t sb = rb >= 0 && rb < rows ? (uint32_t)rb * nblk * 4u : kOut;
+#pragma unroll
+    for (int m = 0; m < RP::kC; m++) {
+      const int c = j + kLpr * m;
+      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
+      const uint32_t bo = c < nchunks ? (uint32_t)(c >> 1) * 4u : kOut;
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
+      P.sa[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sa + bo, 0, 0));
+      P.sb[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sb + bo, 0, 0));
+    }
+  }
+}
+
+// Dots both rows with the LDS activation row (xl, or xq/xs for a W8A8
+// dot); every lane of a 16-lane group returns that group's two row sums.
+// DOT picks the arithmetic: INT8 chunks serve both the weight-only and the
+// W8A8 dot.
+template <int DOT, int KIND, int KMAX>
+__device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K, const float* xl,
+                                            const int8_t* xq, const float* xs, float& r0,
+                                            float& r1) {
+  using RP = RowPair<KIND, KMAX>;
+  static_assert((DOT == kBF16) == (KIND == kBF16), "BF16 dots need BF16 chunks");
+  const int j = threadIdx.x & (kLpr - 1);
+  const int nchunks = K / RP::kElems;
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int m = 0; m < RP::kC; m++) {
+    const int c = j + kLpr * m;
+    if (c >= nchunks) break;
+    const u32x4 va = P.wa[m], vb = P.wb[m];
+    if constexpr (DOT == kBF16) {
+      const float4* xp = reinterpret_cast<const float4*>(xl + c * 8);
+      const float4 x0 = xp[0], x1 = xp[1];
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        a0 = fmaf(bf16_lo(va[i]), xv[2 * i], a0);
+        a0 = fmaf(bf16_hi(va[i]), xv[2 * i + 1], a0);
+        a1 = fmaf(bf16_lo(vb[i]), xv[2 * i], a1);
+        a1 = fmaf(bf16_hi(vb[i]), xv[2 * i + 1], a1);
+      }
+    } else if constexpr (DOT == kInt8) {
+      const float4* xp = reinterpret_cast<const float4*>(xl + c * 16);
+#pragma unroll
+      for (int v4 = 0; v4 < 4; v4++) {
+        const float4 xv = xp[v4];
+        const float x4[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          // The reference multiplies the dequantised (rounded) weight by x.
+          const float da = (float)(int8_t)((va[v4] >> (8 * b)) & 0xff) * P.sa[m];
+          const float db = (float)(int8_t)((vb[v4] >> (8 * b)) & 0xff) * P.sb[m];
+          a0 = fmaf(da, x4[b], a0);
+          a1 = fmaf(db, x4[b], a1);
+        }
+      }
+    } else {
+      const int4 xv = *reinterpret_cast<const int4*>(xq + c * 16);
+      int pa = __builtin_amdgcn_sdot4((int)va.x, xv.x, 0, false);
+      pa = __builtin_amdgcn_sdot4((int)va.y, xv.y, pa, false);
+      pa = __builtin_amdgcn_sdot4((int)va.z, xv.z, pa, false);
+      pa = __builtin_amdgcn_sdot4((int)va.w, xv.w, pa, false);
+      int pb = __builtin_amdgcn_sdot4((int)vb.x, xv.x, 0, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.y, xv.y, pb, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.z, xv.z, pb, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.w, xv.w, pb, false);
+      // Chunks 2b and 2b+1 (lanes j, j^1) form block b: exact i32 sum.
+      const int ia = pa + __shfl_xor(pa, 1);
+      const int ib = pb + __shfl_xor(pb, 1);
+      if ((j & 1) == 0) {
+        const int b = c >> 1;
+        a0 += (float)ia * P.sa[m] * xs[b];
+        a1 += (float)ib * P.sb[m] * xs[b];
+      }
+    }
+  }
+  r0 = row16_sum(a0);
+  r1 = row16_sum(a1);
+}
+
+template <int KIND, int KMAX>
+__device__ __forceinline__ void dot_rows(const RowPair<KIND, KMAX>& P, int K, const float* xl,
+                                         const int8_t* xq, const float* xs, float& r0,
+                                         float& r1) {
+  dot_rows_as<KIND>(P, K, xl, xq, xs, r0, r1);
+}
+
+// An FP32 row of n <= N values (n % 4 == 0) held in registers of one wave
+// (float4 at lane, lane + 64, ...): load_row issues every load, store_row
+// writes the row into LDS.
+template <int N>
+struct RowStage {
+  static constexpr int kV = N / 4 / 64;
+  u32x4 v[kV];
+};
+template <int N>
+__device__ __forceinline__ void load_row(RowStage<N>& R, const float* src, int n, int lane) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)n * 4u);
+#pragma unroll
+  for (int i = 0; i < RowStage<N>::kV; i++) {
+    const int at = lane + 64 * i;
+    R.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, at * 4 < n ? (uint32_t)at * 16u : kOut, 0, 0);
+  }
+}
+template <int N>
+__device__ __forceinline__ void store_row(const RowStage<N>& R, float* dst, int n, int lane) {
+#pragma unroll
+  for (int i = 0; i < RowStage<N>::kV; i++) {
+    const int at = lane + 64 * i;
+    if (at * 4 < n) reinterpret_cast<u32x4*>(dst)[at] = R.v[i];
+  }
+}
+
+// Dots both rows with n <= NT activation rows held in LDS (row t at
+// xl + t * ld), FP32 (BF16 or INT8 weight-only kinds). a0[t] / a1[t] hold
+// this lane's partial sums; row16_sum() completes them.
+template <int KIND, int KMAX, int NT>
+__device__ __forceinline__ void dot_rows_multi(const RowPair<KIND, KMAX>& P, int K, const float* xl,
+                                               int ld, int n, float (&a0)[NT], float (&a1)[NT]) {
+  static_assert(KIND != kW8A8, "W8A8 groups are single-row: dot_rows");
+  using RP = RowPair<KIND, KMAX>;
+  const int j = threadIdx.x & (kLpr - 1);
+  const int nchunks = K / RP::kElems;
+#pragma unroll
+  for (int m = 0; m < RP::kC; m++) {
+    const int c = j + kLpr * m;
+    if (c >= nchunks) break;
+    const u32x4 va = P.wa[m], vb = P.wb[m];
+    if constexpr (KIND == kBF16) {
+      float wa[8], wb[8];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        wa[2 * i] = bf16_lo(va[i]);
+        wa[2 * i + 1] = bf16_hi(va[i]);
+        wb[2 * i] = bf16_lo(vb[i]);
+        wb[2 * i + 1] = bf16_hi(vb[i]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t < n) {
+          const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * 8);
+          const float4 x0 = xp[0], x1 = xp[1];
+          const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            a0[t] = fmaf(wa[i], xv[i], a0[t]);
+            a1[t] = fmaf(wb[i], xv[i], a1[t]);
+          }
+        }
+      }
+    } else {
+      float wa[16], wb[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        // The dequantised weight, rounded once, as the reference stores it.
+        wa[i] = (float)(int8_t)((va[i >> 2] >> (8 * (i & 3))) & 0xff) * P.sa[m];
+        wb[i] = (float)(int8_t)((vb[i >> 2] >> (8 * (i & 3))) & 0xff) * P.sb[m];
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t < n) {
+          const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * 16);
+#pragma unroll
+          for (int v4 = 0; v4 < 4; v4++) {
+            const float4 xv = xp[v4];
+            const float x4[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+              a0[t] = fmaf(wa[4 * v4 + b], x4[b], a0[t]);
+              a1[t] = fmaf(wb[4 * v4 + b], x4[b], a1[t]);
+            }
+          }
+        }
+      }
+    }
+    // One chunk's dequantised weights live at a time.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Loads rows [0, n) of an FP32 [*, K] matrix, row t taken from src_rows[t]
+// (K % 4 == 0), into LDS at dst + t * K with every thread of the workgroup;
+// all loads of a thread are issued before its stores.
+template <int PER_THREAD>
+__device__ __forceinline__ void stage_rows_lds(const float* const* src_rows, int n, int K,
+                                               float* dst) {
+  const int vec = K / 4;
+  const int total = n * vec;
+  u32x4 v[PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < PER_THREAD; i++) {
+    const int at = threadIdx.x + i * blockDim.x;
+    if (at < total) {
+      const int t = at / vec, c = at - t * vec;
+      v[i] = reinterpret_cast<const u32x4*>(src_rows[t])[c];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER_THREAD; i++) {
+    const int at = threadIdx.x + i * blockDim.x;
+    if (at < total) reinterpret_cast<u32x4*>(dst)[at] = v[i];
+  }
+}
+
+}  // namespace uocr
