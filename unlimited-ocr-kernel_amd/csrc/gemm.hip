@@ -59,39 +59,41 @@ __global__ void split_planes_kernel(const float* __restrict__ x, size_t n,
         make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
 }
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte load from global memory (explicit address space: the compiler
-// then issues global loads whose completion it can wait for lazily).
-__device__ __forceinline__ u32x4 gload16(const uint16_t* p) { return *(global_u32x4*)(p); }
-
-// Rows past the tile's valid range load row 0 of the same matrix instead
-// (always in bounds): an MFMA output row depends only on its own A row and
-// an output column only on its own B row, and those rows and columns are
-// never written back, so no select is needed and the loads stay in flight.
-template <int KV>
-__device__ __forceinline__ void load_stage(u32x4 (&dst)[KV], const uint16_t* p) {
-#pragma unroll
-  for (int i = 0; i < KV; i++) dst[i] = gload16(p + 8 * i);
+// Global -> LDS load that bypasses registers (buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes land at LDS address M0 + 16 l, M0 being the wave-uniform
+// `lds_addr`. Range-checked like any raw buffer load: offsets at or past the
+// resource size write zeros. Written as inline assembly so the compiler does
+// not treat it as an LDS store to wait for before every LDS read; the
+// kernel waits on vmcnt itself before the barrier that publishes a stage.
+__device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
 }
 
-template <int KV>
-__device__ __forceinline__ void store_stage(uint16_t* dst, const u32x4 (&src)[KV]) {
-#pragma unroll
-  for (int i = 0; i < KV; i++) *reinterpret_cast<u32x4*>(dst + 8 * i) = src[i];
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  i32x4 r;
+  r.x = (int)(uint32_t)a;
+  r.y = (int)((a >> 32) & 0xffffu);  // stride 0
+  r.z = (int)bytes;
+  r.w = 0x00020000;  // gfx9 raw buffer word 3
+  return r;
 }
 
-template <int BK, bool SPLIT, bool GATEUP>
+constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
+// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at maximum).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int BK, int NBUF, bool SPLIT, bool GATEUP>
 __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
                                                                  MfmaPlanes P, int T) {
-  constexpr int kStride = BK + 8;              // bf16 per LDS row
-  constexpr int kPlane = kTileM * kStride;     // bf16 per plane per stage
-  constexpr int kVec = BK / 16;
-  extern __shared__ __align__(16) uint16_t lds[];
-  // Layout: [stage][A hi | B | A lo] planes.
-  uint16_t* const stage0 = lds;
-  uint16_t* const stage1 = lds + (SPLIT ? 3 : 2) * kPlane;
+  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo]
   __shared__ int arow[kTileM];
 
   // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8); XCD
@@ -146,28 +148,62 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   }
   __syncthreads();
 
+  // ---- LDS tiles. A stage holds the A plane(s) and B, each [256 rows][BK]
+  // bf16 with no padding: chunk c (8 bf16) of row r sits at position
+  // c ^ swz(r), which spreads the 16-byte fragment reads of 16 consecutive
+  // rows over all LDS banks. Loads arrive as 1 KB wave segments of
+  // kSegRows rows (lane l -> row l / kCpr, position l % kCpr).
+  constexpr int kCpr = BK / 8;                 // 16-byte chunks per row
+  constexpr int kSegRows = 64 / kCpr;          // rows per 1 KB segment
+  constexpr int kSegs = kTileM / kSegRows;     // segments per plane
+  constexpr int kSegPerWave = kSegs / 8;       // per wave, per plane
+  constexpr int kRowDiv = 16 / kCpr;
+  auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
+  const uint32_t plane_bytes = (uint32_t)kTileM * BK * 2;
+  const uint32_t stage_bytes = (SPLIT ? 3 : 2) * plane_bytes;
+
+  // Per-lane source offsets of this wave's segments (k = 0).
+  const uint32_t row_bytes = (uint32_t)K * 2;
+  uint32_t a_off[kSegPerWave], b_off[kSegPerWave];
+#pragma unroll
+  for (int i = 0; i < kSegPerWave; i++) {
+    const int r = (wave * kSegPerWave + i) * kSegRows + lane / kCpr;
+    const int c = (lane % kCpr) ^ swz(r);
+    const int src_row = arow[r];
+    a_off[i] = src_row >= 0 ? (uint32_t)src_row * row_bytes + 16u * c : kDmaOut;
+    b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes + 16u * c : kDmaOut;
+  }
   const uint16_t* a_hi_src;
   const uint16_t* a_lo_src;
+  uint32_t a_rows;
   if (GATEUP) {
     a_hi_src = P.x_hi;
     a_lo_src = P.x_lo;
+    a_rows = (uint32_t)T;
   } else {
     a_hi_src = routed ? P.h_hi : P.hs_hi;
     a_lo_src = routed ? P.h_lo : P.hs_lo;
+    a_rows = routed ? (uint32_t)T * L.K : (uint32_t)T;
   }
   const uint16_t* wmat = GATEUP ? L.w13 + L.w13_offset(g) : L.w2 + L.w2_offset(g);
+  const i32x4 rs_a = buffer_rsrc(a_hi_src, a_rows * row_bytes);
+  const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
+  const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes);
+  // LDS byte address of this wave's first segment of stage buffer 0.
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds) +
+      (uint32_t)wave * kSegPerWave * 1024u);
+  auto issue = [&](int buf, int k0) {
+    const uint32_t st = lds0 + (uint32_t)buf * stage_bytes;
+    const uint32_t kb = (uint32_t)k0 * 2u;
+#pragma unroll
+    for (int i = 0; i < kSegPerWave; i++) {
+      buffer_load_lds16(rs_a, st + i * 1024u, a_off[i] + kb);
+      buffer_load_lds16(rs_b, st + plane_bytes + i * 1024u, b_off[i] + kb);
+      if constexpr (SPLIT) buffer_load_lds16(rs_l, st + 2 * plane_bytes + i * 1024u, a_off[i] + kb);
+    }
+  };
 
-  // Thread -> (row, k part) for global loads: two threads per row.
-  const int lrow = tid >> 1;
-  const int lk = (tid & 1) * (BK / 2);
-  const int src_row = arow[lrow];
-  const bool a_ok = src_row >= 0;
-  const bool b_ok = n0 + lrow < N;
-  const uint16_t* a_hi_ptr = a_hi_src + (size_t)(a_ok ? src_row : 0) * K + lk;
-  const uint16_t* a_lo_ptr = a_lo_src + (size_t)(a_ok ? src_row : 0) * K + lk;
-  const uint16_t* b_ptr = wmat + (size_t)(b_ok ? n0 + lrow : 0) * K + lk;
-
-  u32x4 ra[kVec], rl[SPLIT ? kVec : 1], rb[kVec];
   floatx16 acc[4][2];
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
@@ -176,57 +212,66 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.0f;
 
-  const int fr = lane & 31;        // fragment row / column
-  const int fk = (lane >> 5) * 8;  // fragment k offset inside a 16-wide step
+  const int fr = lane & 31;   // fragment row / column
+  const int fc = lane >> 5;   // fragment chunk inside a 16-wide k step
   const int nk = K / BK;
 
-  const int a_off = lrow * kStride + lk;
-  auto issue = [&](int k0) {
-    load_stage<kVec>(ra, a_hi_ptr + k0);
-    load_stage<kVec>(rb, b_ptr + k0);
-    if constexpr (SPLIT) load_stage<kVec>(rl, a_lo_ptr + k0);
-  };
-  auto commit = [&](uint16_t* st) {
-    store_stage<kVec>(st + a_off, ra);
-    store_stage<kVec>(st + kPlane + a_off, rb);
-    if constexpr (SPLIT) store_stage<kVec>(st + 2 * kPlane + a_off, rl);
-  };
-  issue(0);
-  commit(stage0);
-  if (nk > 1) issue(BK);
+  // NBUF LDS stages: stages ks+1 .. ks+NBUF-1 are in flight while stage ks
+  // multiplies. Each wave issues kLps loads per stage, and vmcnt retires
+  // them in order, so "stage ks+1 landed" is vmcnt <= (NBUF-2) * kLps.
+  constexpr int kLps = kSegPerWave * (SPLIT ? 3 : 2);
+  for (int i = 0; i < NBUF - 1; i++)
+    if (i < nk) issue(i, i * BK);
+  if (nk >= NBUF - 1)
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((NBUF - 2) * kLps));
+  else
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
   for (int ks = 0; ks < nk; ks++) {
-    const uint16_t* cur = (ks & 1) ? stage1 : stage0;
+    // Buffer (ks + NBUF - 1) % NBUF was last read in step ks - 1, which
+    // every wave has left (barrier).
+    const bool steady = ks + NBUF - 1 < nk;
+    if (steady) issue((ks + NBUF - 1) % NBUF, (ks + NBUF - 1) * BK);
+    const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
+    constexpr int kSub = BK / 16;
+    bf16x8 fa[2][4], fl[2][SPLIT ? 4 : 1], fb[2][2];
+    auto frag = [&](const char* plane, int row, int c) {
+      return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
+    };
+    auto load_frag = [&](int sub, bf16x8 (&a)[4], bf16x8 (&al)[SPLIT ? 4 : 1], bf16x8 (&b)[2]) {
+      const int c = 2 * sub + fc;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      bf16x8 a[4], al[4], b[2];
+      for (int ni = 0; ni < 2; ni++) b[ni] = frag(cur + plane_bytes, wn * 64 + ni * 32 + fr, c);
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) {
-        const int row = wm * 128 + mi * 32 + fr;
-        a[mi] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + row * kStride + kk + fk));
-        if constexpr (SPLIT)
-          al[mi] = as_bf16x8(
-              *reinterpret_cast<const uint4*>(cur + 2 * kPlane + row * kStride + kk + fk));
+        a[mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
+        if constexpr (SPLIT) al[mi] = frag(cur + 2 * plane_bytes, wm * 128 + mi * 32 + fr, c);
       }
+    };
+    load_frag(0, fa[0], fl[0], fb[0]);
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) {
-        const int col = wn * 64 + ni * 32 + fr;
-        b[ni] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + kPlane + col * kStride + kk + fk));
-      }
+    for (int sub = 0; sub < kSub; sub++) {
+      const int cb = sub & 1;
+      // The next substep's fragments are read before this substep's MFMAs
+      // are issued, so every read has a substep of MFMA time to land.
+      if (sub + 1 < kSub) load_frag(sub + 1, fa[cb ^ 1], fl[cb ^ 1], fb[cb ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
 #pragma unroll
         for (int ni = 0; ni < 2; ni++) {
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+          acc[mi][ni] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][mi], fb[cb][ni], acc[mi][ni], 0, 0, 0);
           if constexpr (SPLIT)
-            acc[mi][ni] =
-                __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[mi], b[ni], acc[mi][ni], 0, 0, 0);
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[cb][mi], fb[cb][ni],
+                                                                  acc[mi][ni], 0, 0, 0);
         }
     }
-    if (ks + 1 < nk) {
-      commit((ks & 1) ? stage0 : stage1);
-      if (ks + 2 < nk) issue((ks + 2) * BK);
-    }
+    // Stage ks + 1 is in LDS once every wave's loads for it have landed.
+    if (steady)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only((NBUF - 2) * kLps));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
   }
 
@@ -269,10 +314,13 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   }
 }
 
-template <int BK, bool SPLIT>
+template <int BK, int NBUF, bool SPLIT>
 constexpr size_t mfma_lds_bytes() {
-  return (size_t)2 * (SPLIT ? 3 : 2) * kTileM * (BK + 8) * sizeof(uint16_t);
+  return (size_t)NBUF * (SPLIT ? 3 : 2) * kTileM * BK * sizeof(uint16_t);
 }
+// BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class
+// (hi + lo planes): 32-deep stages, three buffers (144 KiB).
+constexpr int kBkBf16 = 32, kBufBf16 = 4, kBkSplit = 32, kBufSplit = 3;
 
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
   if (n == 0) return;
@@ -294,11 +342,11 @@ static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
                         int tiles_bound, bool bf16_only, hipStream_t s) {
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP));
   if (bf16_only)
-    mfma_group_kernel<64, false, GATEUP>
-        <<<grid, dim3(kThreads), mfma_lds_bytes<64, false>(), s>>>(L, S, P, T);
+    mfma_group_kernel<kBkBf16, kBufBf16, false, GATEUP>
+        <<<grid, dim3(kThreads), mfma_lds_bytes<kBkBf16, kBufBf16, false>(), s>>>(L, S, P, T);
   else
-    mfma_group_kernel<32, true, GATEUP>
-        <<<grid, dim3(kThreads), mfma_lds_bytes<32, true>(), s>>>(L, S, P, T);
+    mfma_group_kernel<kBkSplit, kBufSplit, true, GATEUP>
+        <<<grid, dim3(kThreads), mfma_lds_bytes<kBkSplit, kBufSplit, true>(), s>>>(L, S, P, T);
 }
 
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -312,18 +360,18 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
 }
 
 void mfma_init_attributes() {
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<64, false, true>,
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkBf16, kBufBf16, false, true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<64, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<64, false, false>,
+                            (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkBf16, kBufBf16, false, false>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<64, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<32, true, true>,
+                            (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkSplit, kBufSplit, true, true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<32, true>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<32, true, false>,
+                            (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkSplit, kBufSplit, true, false>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<32, true>());
+                            (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
 
