@@ -31,7 +31,7 @@ namespace uocr {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kTileM = 256, kTileN = 256, kThreads = 512, kXcds = 8;
+constexpr int kTileM = 256, kTileN = 256, kXcds = 8;
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) {
   return __builtin_bit_cast(uint16_t, (__bf16)v);
@@ -90,9 +90,14 @@ constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at maximum).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int BK, int NBUF, bool SPLIT, bool GATEUP>
-__global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
-                                                                 MfmaPlanes P, int T) {
+template <int WAVES, int BK, int NBUF, bool SPLIT, bool GATEUP>
+__global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
+                                                                   MfmaPlanes P, int T) {
+  // Waves form a 2 x (WAVES/2) grid over the 256 x 256 tile; each owns 128
+  // rows and kWc columns as 4 x kNi MFMA tiles.
+  constexpr int kWn = WAVES / 2;
+  constexpr int kWc = kTileN / kWn;
+  constexpr int kNi = kWc / 32;
   extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo]
   __shared__ int arow[kTileM];
 
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / kWn, wn = wave % kWn;
 
   if (tid < kTileM) {
     int src = -1;
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   constexpr int kCpr = BK / 8;                 // 16-byte chunks per row
   constexpr int kSegRows = 64 / kCpr;          // rows per 1 KB segment
   constexpr int kSegs = kTileM / kSegRows;     // segments per plane
-  constexpr int kSegPerWave = kSegs / 8;       // per wave, per plane
+  constexpr int kSegPerWave = kSegs / WAVES;   // per wave, per plane
   constexpr int kRowDiv = 16 / kCpr;
   auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
   const uint32_t plane_bytes = (uint32_t)kTileM * BK * 2;
@@ -204,11 +209,11 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
     }
   };
 
-  floatx16 acc[4][2];
+  floatx16 acc[4][kNi];
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 2; ni++)
+    for (int ni = 0; ni < kNi; ni++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.0f;
 
@@ -234,14 +239,14 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
     if (steady) issue((ks + NBUF - 1) % NBUF, (ks + NBUF - 1) * BK);
     const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
     constexpr int kSub = BK / 16;
-    bf16x8 fa[2][4], fl[2][SPLIT ? 4 : 1], fb[2][2];
+    bf16x8 fa[2][4], fl[2][SPLIT ? 4 : 1], fb[2][kNi];
     auto frag = [&](const char* plane, int row, int c) {
       return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
     };
-    auto load_frag = [&](int sub, bf16x8 (&a)[4], bf16x8 (&al)[SPLIT ? 4 : 1], bf16x8 (&b)[2]) {
+    auto load_frag = [&](int sub, bf16x8 (&a)[4], bf16x8 (&al)[SPLIT ? 4 : 1], bf16x8 (&b)[kNi]) {
       const int c = 2 * sub + fc;
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) b[ni] = frag(cur + plane_bytes, wn * 64 + ni * 32 + fr, c);
+      for (int ni = 0; ni < kNi; ni++) b[ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) {
         a[mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
+        for (int ni = 0; ni < kNi; ni++) {
           acc[mi][ni] =
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][mi], fb[cb][ni], acc[mi][ni], 0, 0, 0);
           if constexpr (SPLIT)
@@ -276,33 +281,38 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_group_kernel(DeviceLayer L, 
   }
 
   // Output element (mi, ni, r) of this lane: row 128 wm + 32 mi + 8 (r/4) +
-  // 4 (lane/32) + r%4, column 64 wn + 32 ni + lane%32.
-  const int wcol0 = n0 + wn * 64;
+  // 4 (lane/32) + r%4, column kWc wn + 32 ni + lane%32.
+  const int wcol0 = n0 + wn * kWc;
   if (wcol0 >= N) return;
   if (GATEUP) {
-    const int col = wcol0 / 2 + fr;  // hidden column of this lane
+    // Columns 64b .. 64b+63 of the wave are one (gate, up) block pair.
     uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
     uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int bp = 0; bp < kNi / 2; bp++) {
+      if (wcol0 + 64 * bp >= N) break;
+      const int col = (wcol0 + 64 * bp) / 2 + fr;  // hidden column of this lane
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < mrows) {
-          const float gv = acc[mi][0][r];
-          const float h = __fdividef(gv, 1.0f + __expf(-gv)) * acc[mi][1][r];
-          const size_t at = (size_t)(base + r0 + row) * W + col;
-          const uint16_t hb = bf16_bits(h);
-          h_hi[at] = hb;
-          if constexpr (SPLIT) h_lo[at] = bf16_bits(h - __uint_as_float((uint32_t)hb << 16));
+      for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row < mrows) {
+            const float gv = acc[mi][2 * bp][r];
+            const float h = __fdividef(gv, 1.0f + __expf(-gv)) * acc[mi][2 * bp + 1][r];
+            const size_t at = (size_t)(base + r0 + row) * W + col;
+            const uint16_t hb = bf16_bits(h);
+            h_hi[at] = hb;
+            if constexpr (SPLIT) h_lo[at] = bf16_bits(h - __uint_as_float((uint32_t)hb << 16));
+          }
         }
-      }
+    }
   } else {
     float* out = routed ? S.y : S.ys;
 #pragma unroll
     for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) {
+      for (int ni = 0; ni < kNi; ni++) {
         const int col = wcol0 + ni * 32 + fr;
         if (col >= N) continue;
 #pragma unroll
@@ -321,6 +331,7 @@ constexpr size_t mfma_lds_bytes() {
 // BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class
 // (hi + lo planes): 32-deep stages, three buffers (144 KiB).
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBkSplit = 32, kBufSplit = 3;
+constexpr int kWaves = 8;
 
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
   if (n == 0) return;
@@ -342,11 +353,11 @@ static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
                         int tiles_bound, bool bf16_only, hipStream_t s) {
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP));
   if (bf16_only)
-    mfma_group_kernel<kBkBf16, kBufBf16, false, GATEUP>
-        <<<grid, dim3(kThreads), mfma_lds_bytes<kBkBf16, kBufBf16, false>(), s>>>(L, S, P, T);
+    mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, GATEUP>
+        <<<grid, dim3(kWaves * 64), mfma_lds_bytes<kBkBf16, kBufBf16, false>(), s>>>(L, S, P, T);
   else
-    mfma_group_kernel<kBkSplit, kBufSplit, true, GATEUP>
-        <<<grid, dim3(kThreads), mfma_lds_bytes<kBkSplit, kBufSplit, true>(), s>>>(L, S, P, T);
+    mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, GATEUP>
+        <<<grid, dim3(kWaves * 64), mfma_lds_bytes<kBkSplit, kBufSplit, true>(), s>>>(L, S, P, T);
 }
 
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -360,16 +371,16 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
 }
 
 void mfma_init_attributes() {
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkBf16, kBufBf16, false, true>,
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkBf16, kBufBf16, false, false>,
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, false>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkSplit, kBufSplit, true, true>,
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kBkSplit, kBufSplit, true, false>,
+  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, false>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
