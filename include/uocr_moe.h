@@ -227,6 +227,83 @@ int uocr_int8_linear_dynamic(uocr_gpu_ctx* ctx, const int8_t* q, const float* sc
 int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
                   const float* weight, float eps, float* out);
 
+/* ---------------------------------------------------- checkpoint files */
+/* The model-directory side of Model::load_with_quantization; the C++ form
+ * of each is in uocr.hpp. */
+
+/* Safetensors dtypes (DType, src/checkpoint.rs:14-21). */
+typedef enum uocr_dtype {
+  UOCR_DTYPE_BF16 = 0,
+  UOCR_DTYPE_F16 = 1,
+  UOCR_DTYPE_F32 = 2,
+  UOCR_DTYPE_I64 = 3,
+  UOCR_DTYPE_I8 = 4,
+} uocr_dtype;
+
+typedef struct uocr_checkpoint uocr_checkpoint;
+/* Checkpoint::open (src/checkpoint.rs:114-178): memory-maps a safetensors
+ * file and validates its header: < 8 bytes, a header over 100 MB, a
+ * truncated header, size overflow, bad offsets, gaps, overlaps or trailing
+ * payload -> Format; malformed header JSON -> Json; unreadable file -> Io. */
+int uocr_checkpoint_open(const char* path, uocr_checkpoint** out);
+void uocr_checkpoint_close(uocr_checkpoint* ckpt);
+/* Checkpoint::sha256 (src/checkpoint.rs:183-206): lowercase hex, NUL-ended. */
+int uocr_checkpoint_sha256(const uocr_checkpoint* ckpt, char out[65]);
+/* Checkpoint::names (src/checkpoint.rs:220-222): sorted; NULL past the end. */
+size_t uocr_checkpoint_count(const uocr_checkpoint* ckpt);
+const char* uocr_checkpoint_name(const uocr_checkpoint* ckpt, size_t index);
+/* Checkpoint::metadata (src/checkpoint.rs:180-182): NULL when absent. */
+const char* uocr_checkpoint_metadata(const uocr_checkpoint* ckpt, const char* key);
+/* Checkpoint::tensor (src/checkpoint.rs:208-219): dtype, shape (up to
+ * max_dims entries) and the mapped bytes; a missing tensor -> Format. */
+int uocr_checkpoint_tensor(const uocr_checkpoint* ckpt, const char* name, int* dtype,
+                           size_t* shape, size_t max_dims, size_t* ndim, const void** data,
+                           size_t* bytes);
+/* QuantizedWeights::load (src/cpu/quantized.rs:304-366) without keeping the
+ * matrices: manifest (path with ".json"), metadata and SHA-256 binding to
+ * `source`, the eligible matrix set and every matrix's storage rules. */
+int uocr_overlay_validate(const char* overlay_path, const uocr_checkpoint* source,
+                          size_t* matrices);
+
+/* ModelConfig (src/model/config.rs:30-115), the fields this library uses. */
+typedef struct uocr_model_config {
+  uint32_t hidden_size;
+  uint32_t intermediate_size;
+  uint32_t moe_intermediate_size;
+  uint32_t num_hidden_layers;
+  uint32_t num_attention_heads;
+  uint32_t num_key_value_heads;
+  uint32_t n_routed_experts;
+  uint32_t n_shared_experts;
+  uint32_t num_experts_per_tok;
+  uint32_t first_k_dense_replace;
+  uint32_t vocab_size;
+  uint32_t norm_topk_prob;
+  float routed_scaling_factor;
+  float rms_norm_eps;
+} uocr_model_config;
+/* ModelConfig::load (src/model/config.rs:71-115): unsupported attention or
+ * routing -> Unsupported; inconsistent sizes -> Shape; JSON errors -> Json. */
+int uocr_config_load(const char* path, uocr_model_config* out);
+
+typedef struct uocr_model uocr_model;
+/* Model::load_with_quantization (src/model/mod.rs:82-109) for the MoE
+ * layers: config.json and model-00001-of-000001.safetensors in `directory`,
+ * the Decoder::new shape rules (src/decoder/mod.rs:32-88), then the overlay
+ * (NULL for none). DynamicActivations without an overlay -> Format. Every
+ * MoE decoder layer is uploaded to ctx's device. */
+int uocr_model_load(uocr_gpu_ctx* ctx, const char* directory, const char* overlay,
+                    uocr_quant_mode mode, uocr_model** out);
+/* Model::precision (src/model/mod.rs:65-73). */
+const char* uocr_model_precision(const uocr_model* model);
+/* The layer handle of MoE decoder layer `layer` (NULL for dense layers). */
+const uocr_moe_layer* uocr_model_layer(const uocr_model* model, size_t layer);
+/* Decoder::experts (src/decoder/mod.rs:124-220) of decoder layer `layer`:
+ * y[T,H] from x[T,H], device pointers; synchronous. */
+int uocr_model_experts(uocr_gpu_ctx* ctx, const uocr_model* model, size_t layer, const float* x,
+                       size_t T, float* y, uint32_t flags);
+void uocr_model_destroy(uocr_model* model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,14 @@ std::once_flag g_attr_once;
 
 }  // namespace
 
+namespace uocr::host {
+// Records the message that uocr_last_error returns on this thread.
+int set_last_error(int status, const char* message) {
+  g_last_error = message;
+  return status;
+}
+}  // namespace uocr::host
+
 enum Phase { kRouter, kTopk, kDispatch, kSplit, kGateUp, kDown, kCombine, kNorm, kPhases };
 static const char* const kPhaseNames[kPhases] = {"router", "topk",   "dispatch", "split",
                                                  "gateup", "down",   "combine",  "norm"};

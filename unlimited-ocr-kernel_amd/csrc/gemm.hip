@@ -67,11 +67,13 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // resource size write zeros. Written as inline assembly so the compiler does
 // not treat it as an LDS store to wait for before every LDS read; the
 // kernel waits on vmcnt itself before the barrier that publishes a stage.
+// M0 is reserved to the compiler, which uses it only for such LDS transfers
+// (none of its own here), so the asm sets it without declaring it.
 __device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(lds_addr), "v"(voffset), "s"(rsrc)
-               : "memory", "m0");
+               : "memory");
 }
 
 __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {

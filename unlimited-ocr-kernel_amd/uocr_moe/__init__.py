@@ -41,7 +41,12 @@ EXPORTS = [
     "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
     "uocr_moe_forward", "uocr_moe_block_forward", "uocr_moe_block_forward_async", "uocr_route",
     "uocr_linear_bf16", "uocr_int8_linear", "uocr_int8_linear_dynamic", "uocr_rms_norm",
+    "uocr_checkpoint_open", "uocr_checkpoint_close", "uocr_checkpoint_sha256",
+    "uocr_checkpoint_count", "uocr_checkpoint_name", "uocr_checkpoint_metadata",
+    "uocr_checkpoint_tensor", "uocr_overlay_validate", "uocr_config_load", "uocr_model_load",
+    "uocr_model_precision", "uocr_model_layer", "uocr_model_experts", "uocr_model_destroy",
 ]
+DTYPES = ["BF16", "F16", "F32", "I64", "I8"]
 
 
 class UocrError(RuntimeError):
@@ -80,6 +85,14 @@ class Int8Weights(ctypes.Structure):
 class PhaseTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64),
                 ("total_ms", ctypes.c_double)]
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, _U32) for n in (
+        "hidden_size", "intermediate_size", "moe_intermediate_size", "num_hidden_layers",
+        "num_attention_heads", "num_key_value_heads", "n_routed_experts", "n_shared_experts",
+        "num_experts_per_tok", "first_k_dense_replace", "vocab_size", "norm_topk_prob")] + [
+        ("routed_scaling_factor", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
 
 
 class Trace(ctypes.Structure):
@@ -122,6 +135,23 @@ def _load():
         "uocr_int8_linear": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, _SZ, _P]),
         "uocr_int8_linear_dynamic": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, _P, _P]),
         "uocr_rms_norm": (ctypes.c_int, [_P, _P, _SZ, _SZ, _P, ctypes.c_float, _P]),
+        "uocr_checkpoint_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+        "uocr_checkpoint_close": (None, [_P]),
+        "uocr_checkpoint_sha256": (ctypes.c_int, [_P, ctypes.c_char_p]),
+        "uocr_checkpoint_count": (_SZ, [_P]),
+        "uocr_checkpoint_name": (ctypes.c_char_p, [_P, _SZ]),
+        "uocr_checkpoint_metadata": (ctypes.c_char_p, [_P, ctypes.c_char_p]),
+        "uocr_checkpoint_tensor": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int),
+                                                  ctypes.POINTER(_SZ), _SZ, ctypes.POINTER(_SZ),
+                                                  ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
+        "uocr_overlay_validate": (ctypes.c_int, [ctypes.c_char_p, _P, ctypes.POINTER(_SZ)]),
+        "uocr_config_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ModelConfig)]),
+        "uocr_model_load": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int,
+                                           ctypes.POINTER(_P)]),
+        "uocr_model_precision": (ctypes.c_char_p, [_P]),
+        "uocr_model_layer": (_P, [_P, _SZ]),
+        "uocr_model_experts": (ctypes.c_int, [_P, _P, _SZ, _P, _SZ, _P, _U32]),
+        "uocr_model_destroy": (None, [_P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -303,3 +333,87 @@ def int8_linear_dynamic(ctx: Context, q, scales, x, y, block_sums=None):
 def rms_norm(ctx: Context, x, weight, eps: float, out):
     rows, width = x.shape
     _check(lib.uocr_rms_norm(ctx.handle, _ptr(x), rows, width, _ptr(weight), eps, _ptr(out)))
+
+
+# --------------------------------------------------------------- files
+
+class Checkpoint:
+    """A memory-mapped safetensors file (Checkpoint::open, src/checkpoint.rs)."""
+
+    def __init__(self, path):
+        self.handle = None
+        h = _P()
+        _check(lib.uocr_checkpoint_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib.uocr_checkpoint_close(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def sha256(self) -> str:
+        buf = ctypes.create_string_buffer(65)
+        _check(lib.uocr_checkpoint_sha256(self.handle, buf))
+        return buf.value.decode()
+
+    def names(self):
+        return [lib.uocr_checkpoint_name(self.handle, i).decode()
+                for i in range(lib.uocr_checkpoint_count(self.handle))]
+
+    def metadata(self, key: str):
+        v = lib.uocr_checkpoint_metadata(self.handle, key.encode())
+        return None if v is None else v.decode()
+
+    def tensor(self, name: str):
+        """(dtype name, shape, bytes) of a tensor, copied out of the mapping."""
+        dt, nd, data, nbytes = ctypes.c_int(), _SZ(), _P(), _SZ()
+        shape = (_SZ * 8)()
+        _check(lib.uocr_checkpoint_tensor(self.handle, name.encode(), ctypes.byref(dt), shape, 8,
+                                          ctypes.byref(nd), ctypes.byref(data),
+                                          ctypes.byref(nbytes)))
+        raw = ctypes.string_at(data.value, nbytes.value) if nbytes.value else b""
+        return DTYPES[dt.value], [shape[i] for i in range(nd.value)], raw
+
+
+def overlay_validate(overlay_path, source: Checkpoint) -> int:
+    """QuantizedWeights::load's checks; returns the matrix count."""
+    n = _SZ()
+    _check(lib.uocr_overlay_validate(os.fsencode(overlay_path), source.handle, ctypes.byref(n)))
+    return n.value
+
+
+def config_load(path) -> ModelConfig:
+    c = ModelConfig()
+    _check(lib.uocr_config_load(os.fsencode(path), ctypes.byref(c)))
+    return c
+
+
+class Model:
+    """The MoE decoder layers of a model directory (Model::load_with_quantization)."""
+
+    def __init__(self, ctx, directory, overlay=None, mode: int = QUANT_WEIGHTS_ONLY):
+        self.handle = None
+        h = _P()
+        _check(lib.uocr_model_load(ctx.handle if ctx is not None else None, os.fsencode(directory),
+                                   None if overlay is None else os.fsencode(overlay), mode,
+                                   ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib.uocr_model_destroy(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def precision(self) -> str:
+        return lib.uocr_model_precision(self.handle).decode()
+
+    def is_moe_layer(self, layer: int) -> bool:
+        return bool(lib.uocr_model_layer(self.handle, layer))
+
+    def experts(self, ctx, layer: int, x, y, flags: int = 0):
+        _check(lib.uocr_model_experts(ctx.handle, self.handle, layer, _ptr(x), x.shape[0], _ptr(y),
+                                      flags))
