@@ -318,7 +318,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_begin(ctx, kRouter);
       uocr::launch_small_route(S.xn, L, S, Ti, st);
       phase_end(ctx);
-    } else if (T > (size_t)uocr::kGemvChunk) {
+    } else if (T > (size_t)uocr::kGemvChunk && uocr::router_mfma_supported(L.H)) {
       // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
       phase_begin(ctx, kRouter);
       uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
@@ -330,7 +330,8 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
                                     S.tiles, S.counters, st);
       phase_end(ctx);
     } else {
-      // MFMA engine forced on a small batch.
+      // MFMA engine forced on a small batch, or a hidden width beyond the
+      // fused router's.
       phase_begin(ctx, kRouter);
       uocr::launch_router_logits(S.xn, L.router, Ti, L.H, L.E, S.logits, st);
       phase_end(ctx);

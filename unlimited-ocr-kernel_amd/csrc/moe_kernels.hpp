@@ -66,6 +66,8 @@ void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E
 void launch_topk(const float* logits, int T, int E, int K, int normalize, float scale, int* ids,
                  float* weights, int* err, hipStream_t s);
 
+// The fused router covers hidden widths up to 2048 (64 K steps of 32).
+inline bool router_mfma_supported(int H) { return H % 32 == 0 && H <= 2048; }
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, int* err, hipStream_t s);

@@ -144,6 +144,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Many tokens: logits on MFMA (v_mfma_f32_16x16x32_bf16), then softmax
@@ -156,12 +157,18 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // for the dispatch scan.
 constexpr int kRouteChunk = 16;
 
-__global__ __launch_bounds__(256) void router_mfma_kernel(
+constexpr int kRouteWaves = 8;
+
+// KS = K steps (32 wide) per wave: wave w takes steps w, w + 8, ...; steps
+// past H / 32 read as zero. All loads of a wave are issued before its MFMAs.
+template <int KS>
+__global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ w, int T, int H, int E, int K,
     int normalize, float scale, float* __restrict__ logits, int* __restrict__ ids,
     float* __restrict__ weights, int* __restrict__ chunk_counts, int* err) {
-  __shared__ float part[4][kRouteChunk][65];
+  __shared__ float part[kRouteWaves][kRouteChunk][65];
   __shared__ int cnt[64];
+  __shared__ RouteSmem rs[kRouteWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -169,43 +176,57 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
   if (tid < 64) cnt[tid] = 0;
   const int ar = lane & 15;        // fragment row (token) / column (expert)
   const int aq = (lane >> 4) * 8;  // fragment k offset within a 32-wide step
-  const int token = t0 + ar;
-  const bool tok_ok = token < T;
-  const float* xrow = x + (size_t)(tok_ok ? token : 0) * H + aq;
+  const int steps = H / 32;
+  // Range-checked buffer loads: tokens >= T and experts >= E read as zero.
+  // The x range starts at this workgroup's first token so offsets stay small.
+  const int nt = min(kRouteChunk, T - t0);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x + (size_t)t0 * H), 0, (int)((uint32_t)nt * H * 4u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(w), 0, (int)((uint32_t)E * H * 2u), 0x00020000);
+  constexpr uint32_t kFar = 0x80000000u;
+  const uint32_t xoff = (uint32_t)ar * H * 4u + aq * 4u;
+  u32x4 xa[KS], xb[KS], wv[KS][4];
+#pragma unroll
+  for (int i = 0; i < KS; i++) {
+    const int st = wave + kRouteWaves * i;
+    const bool ok = st < steps;
+    const uint32_t k0 = (uint32_t)st * 32u;
+    xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + k0 * 4u : kFar, 0, 0);
+    xb[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + k0 * 4u + 16u : kFar, 0, 0);
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) {
+      const uint32_t e = (uint32_t)(ni * 16 + ar);
+      wv[i][ni] = __builtin_amdgcn_raw_buffer_load_b128(
+          wr, ok ? (e * H + k0 + aq) * 2u : kFar, 0, 0);
+    }
+  }
   floatx4 acc[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ni++) acc[ni] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int steps = H / 32;
-#pragma unroll 2
-  for (int st = wave; st < steps; st += 4) {
-    const int k0 = st * 32;
-    const float4 v0 = *reinterpret_cast<const float4*>(xrow + k0);
-    const float4 v1 = *reinterpret_cast<const float4*>(xrow + k0 + 4);
-    uint4 bv[4];
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-      const int e = ni * 16 + ar;
-      bv[ni] = e < E ? *reinterpret_cast<const uint4*>(w + (size_t)e * H + k0 + aq)
-                     : make_uint4(0, 0, 0, 0);
-    }
-    const float xv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  for (int i = 0; i < KS; i++) {
+    const float xv[8] = {__uint_as_float(xa[i].x), __uint_as_float(xa[i].y),
+                         __uint_as_float(xa[i].z), __uint_as_float(xa[i].w),
+                         __uint_as_float(xb[i].x), __uint_as_float(xb[i].y),
+                         __uint_as_float(xb[i].z), __uint_as_float(xb[i].w)};
     bf16x8 hi, mid, lo;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float f = tok_ok ? xv[i] : 0.0f;
+    for (int j = 0; j < 8; j++) {
+      const float f = xv[j];
       const __bf16 h = (__bf16)f;
       const float r1 = f - (float)h;
       const __bf16 m = (__bf16)r1;
-      hi[i] = h;
-      mid[i] = m;
-      lo[i] = (__bf16)(r1 - (float)m);
+      hi[j] = h;
+      mid[j] = m;
+      lo[j] = (__bf16)(r1 - (float)m);
     }
 #pragma unroll
     for (int ni = 0; ni < 4; ni++) {
-      const bf16x8 b = __builtin_bit_cast(bf16x8, bv[ni]);
-      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[ni], 0, 0, 0);
-      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[ni], 0, 0, 0);
-      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[ni], 0, 0, 0);
+      const bf16x8 bb = __builtin_bit_cast(bf16x8, wv[i][ni]);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bb, acc[ni], 0, 0, 0);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, bb, acc[ni], 0, 0, 0);
+      acc[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, bb, acc[ni], 0, 0, 0);
     }
   }
   // acc[ni][r]: token 4 (lane / 16) + r, expert 16 ni + lane % 16.
@@ -214,16 +235,26 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < 4; r++) part[wave][4 * (lane >> 4) + r][ni * 16 + ar] = acc[ni][r];
   __syncthreads();
-  for (int j = 0; j < kRouteChunk / 4; j++) {
-    const int tl = wave * (kRouteChunk / 4) + j;
+  // Wave partial sums in wave order (deterministic); each wave then routes
+  // two tokens with the LDS top-k (every wave makes the same calls: they
+  // synchronise the workgroup).
+  for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
+    const int tl = wave * (kRouteChunk / kRouteWaves) + j;
     const int t = t0 + tl;
-    if (t >= T) break;
-    const float v = ((part[0][tl][lane] + part[1][tl][lane]) + part[2][tl][lane]) +
-                    part[3][tl][lane];
-    if (lane < E) logits[(size_t)t * E + lane] = v;
-    const int id = route_token(v, E, K, normalize, scale, ids + (size_t)t * K,
-                               weights + (size_t)t * K, err);
-    if (lane < K) atomicAdd(&cnt[id], 1);
+    const bool live = t < T;
+    float v = part[0][tl][lane];
+#pragma unroll
+    for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][lane];
+    if (live && lane < E) logits[(size_t)t * E + lane] = v;
+    const LdsRoute r = route_lds(live ? v : 0.0f, E, K, rs[wave]);
+    const float wgt = route_lds_weight(r, K, normalize, scale, rs[wave]);
+    if (!live) continue;
+    if (!r.ok && lane == 0) raise_error(err, kErrNumerical);
+    if ((r.mask >> lane) & 1ull) {
+      ids[(size_t)t * K + r.rank] = lane;
+      weights[(size_t)t * K + r.rank] = wgt;
+      atomicAdd(&cnt[lane], 1);
+    }
   }
   __syncthreads();
   if (tid < 64) chunk_counts[(size_t)blockIdx.x * 64 + tid] = cnt[tid];
@@ -232,10 +263,15 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, int* err, hipStream_t s) {
-  if (T <= 0) return;
-  hipLaunchKernelGGL(router_mfma_kernel, dim3((T + kRouteChunk - 1) / kRouteChunk), dim3(256), 0,
-                     s, x, w, T, H, E, K, normalize, scale, logits, ids, weights, chunk_counts,
-                     err);
+  if (T <= 0 || !router_mfma_supported(H)) return;
+  const dim3 grid((T + kRouteChunk - 1) / kRouteChunk), block(64 * kRouteWaves);
+  const int ks = (H / 32 + kRouteWaves - 1) / kRouteWaves;
+  if (ks <= 5)
+    router_mfma_kernel<5><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
+                                                 weights, chunk_counts, err);
+  else
+    router_mfma_kernel<8><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
+                                                 weights, chunk_counts, err);
 }
 
 void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
