@@ -6,13 +6,14 @@
 //
 // A workgroup of 8 waves computes a 256x256 output tile of one expert group
 // with v_mfma_f32_32x32x16_bf16; wave (wm, wn) owns rows [128 wm, +128) and
-// columns [64 wn, +64) as 4x2 MFMA tiles whose accumulators live in AGPRs.
-// K is walked in stages staged through double-buffered LDS (rows padded by
-// 16 bytes, which keeps 128-bit LDS reads and writes free of bank
-// conflicts); the global loads of stage k+2 are in flight while stage k is
-// multiplied. Weights are exact in bf16. FP32 activations enter as bf16
-// planes: FP32-class precision splits each value x = hi + lo (relative
-// residual <= 2^-18) and multiplies both planes; BF16 activations use hi.
+// columns [64 wn, +64) as 4x2 MFMA tiles. K is walked in 32-deep stages that
+// global->LDS loads (no register staging) bring into a ring of LDS buffers,
+// several stages ahead of the one being multiplied; the two waves of each
+// SIMD alternate between multiplying and memory work (ping-pong), one
+// barrier-separated phase apart. Weights are exact in bf16. FP32
+// activations enter as bf16 planes: FP32-class precision splits each value
+// x = hi + lo (relative residual <= 2^-18) and multiplies both planes; BF16
+// activations use hi.
 //
 // Gate/up rows are interleaved in blocks of 32 (gate j.., up j..), so the
 // wave whose 64 columns are one (gate, up) block pair holds g and u for the
@@ -21,8 +22,8 @@
 //
 // Work items are (row tile, column tile) pairs enumerated on the device.
 // Workgroup ids reach the 8 XCDs round-robin; they are remapped so each XCD
-// takes a contiguous range of the existing items, keeping an expert's
-// weights in that XCD's L2.
+// takes a contiguous, cost-balanced range of the existing items, keeping an
+// expert's weights in that XCD's L2.
 #include "common.hpp"
 #include "moe_kernels.hpp"
 
@@ -103,30 +104,39 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo]
   __shared__ int arow[kTileM];
 
-  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8); XCD
-  // x takes the contiguous item range [x * chunk, (x + 1) * chunk) of the
-  // items that exist, so all 8 XCDs share the work and neighbouring items
-  // (same expert) meet in one L2.
+  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
+  // items are listed shared-expert first, then routed (each in row-tile,
+  // column-tile order), and cut into 8 contiguous ranges of equal cost, one
+  // per XCD: an item costs its K depth, so the deeper shared items of the
+  // down GEMM do not pile up on one XCD, neighbouring items (same expert,
+  // same rows) meet in one L2, and an XCD's deeper items start first.
   const int routed_tiles = S.counters[1];
   const int all_tiles = S.counters[0];
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
   const int nt_routed = (n_routed + kTileN - 1) / kTileN;
   const int nt_shared = (n_shared + kTileN - 1) / kTileN;
-  const int routed_items = routed_tiles * nt_routed;
-  const int n_items = routed_items + (all_tiles - routed_tiles) * nt_shared;
-  const int chunk = (n_items + kXcds - 1) / kXcds;
-  const int slot = blockIdx.x / kXcds;
-  const int item = (blockIdx.x % kXcds) * chunk + slot;
-  if (slot >= chunk || item >= n_items) return;
+  const long long routed_items = (long long)routed_tiles * nt_routed;
+  const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
+  const long long c_shared = GATEUP ? L.H : L.S, c_routed = GATEUP ? L.H : L.I;
+  const long long shared_cost = shared_items * c_shared;
+  const long long total_cost = shared_cost + routed_items * c_routed;
+  // First item of XCD x: the first whose cost prefix reaches x / 8 of the total.
+  auto first_item = [&](int x) -> long long {
+    const long long b = total_cost * x / kXcds;
+    if (b <= shared_cost) return (b + c_shared - 1) / c_shared;
+    return shared_items + (b - shared_cost + c_routed - 1) / c_routed;
+  };
+  const int xcd = blockIdx.x % kXcds;
+  const long long item = first_item(xcd) + blockIdx.x / kXcds;
+  if (item >= first_item(xcd + 1)) return;
   int tile, ntile;
-  if (item < routed_items) {
-    tile = item / nt_routed;
-    ntile = item % nt_routed;
+  if (item < shared_items) {
+    tile = routed_tiles + (int)(item / nt_shared);
+    ntile = (int)(item % nt_shared);
   } else {
-    const int rest = item - routed_items;
-    tile = routed_tiles + rest / nt_shared;
-    ntile = rest % nt_shared;
+    tile = (int)((item - shared_items) / nt_routed);
+    ntile = (int)((item - shared_items) % nt_routed);
   }
   const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
   const bool routed = g < L.E;
@@ -223,64 +233,79 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   const int fc = lane >> 5;   // fragment chunk inside a 16-wide k step
   const int nk = K / BK;
 
-  // NBUF LDS stages: stages ks+1 .. ks+NBUF-1 are in flight while stage ks
-  // multiplies. Each wave issues kLps loads per stage, and vmcnt retires
-  // them in order, so "stage ks+1 landed" is vmcnt <= (NBUF-2) * kLps.
+  // Ping-pong schedule. The two waves sharing a SIMD (w and w + 4) are in
+  // opposite groups, one phase apart: while one group multiplies stage ks
+  // from registers, the other reads its stage-ks fragments from LDS and
+  // issues the global loads of stage ks + kDepth, so each SIMD's MFMA pipe
+  // is fed by one wave while its partner does memory work. Every phase ends
+  // at a workgroup barrier (group 1 passes one extra at the start, group 0
+  // one at the end, so both pass 2 nk + 1).
+  //
+  // Buffers: stage s lives in buffer s % NBUF, NBUF = kDepth + 1. The loads
+  // of stage ks + kDepth overwrite stage ks - 1, whose last reader (group 1,
+  // the phase before) finished its reads before that phase's barrier. Each
+  // wave issues kLps loads per stage, and vmcnt retires them in order, so at
+  // the end of a memory phase "own loads of stage ks + 1 landed" is
+  // vmcnt <= (kDepth - 1) * kLps; the barrier then publishes them to both
+  // groups before either reads stage ks + 1.
+  static_assert(WAVES == 8, "the ping-pong schedule pairs two waves per SIMD");
+  constexpr int kDepth = NBUF - 1;
   constexpr int kLps = kSegPerWave * (SPLIT ? 3 : 2);
-  for (int i = 0; i < NBUF - 1; i++)
+  constexpr int kSub = BK / 16;
+  const int grp = wave >> 2;
+  for (int i = 0; i < kDepth; i++)
     if (i < nk) issue(i, i * BK);
-  if (nk >= NBUF - 1)
-    __builtin_amdgcn_s_waitcnt(vmcnt_only((NBUF - 2) * kLps));
+  if (nk >= kDepth)
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((kDepth - 1) * kLps));
   else
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
+  if (grp) __syncthreads();
   for (int ks = 0; ks < nk; ks++) {
-    // Buffer (ks + NBUF - 1) % NBUF was last read in step ks - 1, which
-    // every wave has left (barrier).
-    const bool steady = ks + NBUF - 1 < nk;
-    if (steady) issue((ks + NBUF - 1) % NBUF, (ks + NBUF - 1) * BK);
+    // ---- memory phase
+    const bool steady = ks + kDepth < nk;
+    if (steady) issue((ks + kDepth) % NBUF, (ks + kDepth) * BK);
     const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
-    constexpr int kSub = BK / 16;
-    bf16x8 fa[2][4], fl[2][SPLIT ? 4 : 1], fb[2][kNi];
+    bf16x8 fa[kSub][4], fl[kSub][SPLIT ? 4 : 1], fb[kSub][kNi];
     auto frag = [&](const char* plane, int row, int c) {
       return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
     };
-    auto load_frag = [&](int sub, bf16x8 (&a)[4], bf16x8 (&al)[SPLIT ? 4 : 1], bf16x8 (&b)[kNi]) {
-      const int c = 2 * sub + fc;
-#pragma unroll
-      for (int ni = 0; ni < kNi; ni++) b[ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++) {
-        a[mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
-        if constexpr (SPLIT) al[mi] = frag(cur + 2 * plane_bytes, wm * 128 + mi * 32 + fr, c);
-      }
-    };
-    load_frag(0, fa[0], fl[0], fb[0]);
 #pragma unroll
     for (int sub = 0; sub < kSub; sub++) {
-      const int cb = sub & 1;
-      // The next substep's fragments are read before this substep's MFMAs
-      // are issued, so every read has a substep of MFMA time to land.
-      if (sub + 1 < kSub) load_frag(sub + 1, fa[cb ^ 1], fl[cb ^ 1], fb[cb ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);
+      const int c = 2 * sub + fc;
+#pragma unroll
+      for (int ni = 0; ni < kNi; ni++) fb[sub][ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++) {
+        fa[sub][mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
+        if constexpr (SPLIT) fl[sub][mi] = frag(cur + 2 * plane_bytes, wm * 128 + mi * 32 + fr, c);
+      }
+    }
+    if (steady)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only((kDepth - 1) * kLps));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- compute phase
+#pragma unroll
+    for (int sub = 0; sub < kSub; sub++)
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
 #pragma unroll
         for (int ni = 0; ni < kNi; ni++) {
           acc[mi][ni] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][mi], fb[cb][ni], acc[mi][ni], 0, 0, 0);
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[sub][mi], fb[sub][ni], acc[mi][ni], 0, 0, 0);
           if constexpr (SPLIT)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[cb][mi], fb[cb][ni],
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[sub][mi], fb[sub][ni],
                                                                   acc[mi][ni], 0, 0, 0);
         }
-    }
-    // Stage ks + 1 is in LDS once every wave's loads for it have landed.
-    if (steady)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only((NBUF - 2) * kLps));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (!grp) __syncthreads();
 
   // Output element (mi, ni, r) of this lane: row 128 wm + 32 mi + 8 (r/4) +
   // 4 (lane/32) + r%4, column kWc wn + 32 ni + lane%32.
@@ -342,12 +367,16 @@ void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, h
                      s, x, n, hi, lo);
 }
 
-// Upper bound of work items: every row tile times the widest column count,
-// rounded up to a multiple of the XCD count.
+// Workgroups: 8 XCDs times the most items one XCD can take. Items are
+// bounded by every row tile times the widest column count; an XCD's range
+// holds an eighth of the cost, so at most (bound / 8) * (deepest / shallowest
+// item) + 2 items.
 static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
-  const int n = gateup ? 2 * L.S : L.H;
+  const int n = gateup ? std::max(2 * L.S, 2 * L.I) : L.H;
   const long long items = (long long)tiles_bound * ((n + kTileN - 1) / kTileN);
-  return (unsigned)((items + kXcds - 1) / kXcds * kXcds);
+  const long long deep = gateup ? 1 : std::max(L.S, L.I), shallow = gateup ? 1 : std::min(L.S, L.I);
+  const long long per_xcd = (items * deep + kXcds * shallow - 1) / (kXcds * shallow) + 2;
+  return (unsigned)(per_xcd * kXcds);
 }
 
 template <bool GATEUP>
