@@ -361,3 +361,34 @@ def test_int8_forced_mfma_is_unsupported(ctx, full_int8):
     with pytest.raises(um.UocrError) as e:
         um.forward(ctx, full_int8.layer, x, torch.empty_like(x), flags=um.FLAG_FORCE_MFMA)
     assert e.value.status == um.UNSUPPORTED
+
+
+@pytest.fixture(scope="module")
+def hot_bf16(ctx):
+    hot = syn.route_profile(syn.hot_share(FULL["experts"], 6, 8, 0.8), 6)
+    return Case(ctx, FULL, 6, seed=41, router_scale=hot)
+
+
+def test_mfma_hot_experts(ctx, hot_bf16):
+    """Skewed routing (80% of assignments on 8 experts): hot experts span
+    several 256-row tiles whose last tile is partial, cold experts fill one
+    small tile. Rows are independent, so a sample of rows is checked against
+    the oracle."""
+    T = 1536
+    x = syn.activations(T, 1280, seed=77)
+    rows = np.sort(np.random.default_rng(5).choice(T, 40, replace=False))
+    ref, rtr = orc.moe_experts(hot_bf16.orc, x[rows], trace=True)
+    for flags, tol in ((0, FP32_TOL), (um.FLAG_BF16_ACTIVATIONS, BF16_TOL)):
+        say(f"hot-expert MFMA T={T} flags={flags}")
+        y, tr = hot_bf16.run(ctx, x, flags)
+        counts = np.diff(tr["expert_offsets"])
+        tail = counts % 256
+        assert (counts > 256).any()
+        assert ((tail > 128) & (counts > 256)).any() and ((tail > 0) & (tail <= 128)).any()
+        assert np.all(np.isfinite(y))
+        keep = [i for i, t in enumerate(rows)
+                if set(tr["topk_ids"][t].tolist()) == set(rtr.topk_ids[i].tolist())]
+        assert len(keep) >= len(rows) - 2
+        err = normwise(y[rows[keep]], ref[keep])
+        say(f"  normwise={err:.3e}")
+        assert err <= tol, err
