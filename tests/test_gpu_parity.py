@@ -392,3 +392,60 @@ def test_mfma_hot_experts(ctx, hot_bf16):
         err = normwise(y[rows[keep]], ref[keep])
         say(f"  normwise={err:.3e}")
         assert err <= tol, err
+
+
+# ------------------------------------------------------------ block stack
+
+def _stack(ctx, n, quant=orc.QUANT_NONE):
+    """n SMALL layers with distinct weights and non-trivial norm weights."""
+    cases, norms = [], []
+    for l in range(n):
+        c = Case(ctx, SMALL, 4, seed=900 + 7 * l, quant=quant, normalize=True)
+        nw = (0.75 + 0.5 * np.sin(np.arange(SMALL["hidden"]) * (0.3 + 0.1 * l))).astype(np.float32)
+        nw = orc.bf16_to_f32(orc.f32_to_bf16(nw))
+        c.w["norm_weight"] = orc.f32_to_bf16(nw).view(np.uint16)
+        cfg = um.config(SMALL["hidden"], SMALL["inter"], SMALL["experts"], SMALL["shared"], 4,
+                        normalize=True)
+        c.layer = um.MoeLayer(ctx, cfg, c.w, um.MEMORY_HOST)
+        if quant != orc.QUANT_NONE:
+            c.layer.attach_int8(ctx, c.orc.q, um.MEMORY_HOST, quant)
+        cases.append(c)
+        norms.append(nw)
+    return cases, norms
+
+
+def _stack_ref(cases, norms, x, eps=1e-6):
+    """Oracle stack, and the tokens whose routing has a near-tie at some layer."""
+    near = np.zeros(x.shape[0], bool)
+    for c, nw in zip(cases, norms):
+        n = orc.rms_norm(x, nw, eps)
+        out, tr = orc.moe_experts(c.orc, n, trace=True)
+        srt = np.sort(tr.logits, axis=1)[:, ::-1]
+        near |= (srt[:, c.top_k - 1] - srt[:, c.top_k]) < 1e-5
+        x = x + out
+    return x, near
+
+
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY])
+@pytest.mark.parametrize("T", [1, 8, 40, 300])
+def test_block_stack(ctx, T, quant):
+    """uocr_moe_block_forward over 3 layers (RMSNorm of each layer fused into
+    the previous layer's combine, with the MFMA engine's bf16 planes) against
+    the oracle's moe_block chain."""
+    cases, norms = _stack(ctx, 3, quant)
+    x = syn.activations(T, SMALL["hidden"], seed=1000 + T)
+    ref, near = _stack_ref(cases, norms, x)
+    keep = ~near
+    flag_sets = [(0, FP32_TOL)]
+    if quant == orc.QUANT_NONE and T > 16:
+        flag_sets.append((um.FLAG_BF16_ACTIVATIONS, BF16_TOL))
+    for flags, tol in flag_sets:
+        say(f"block stack T={T} quant={quant} flags={flags}")
+        xd = dev(x)
+        yd = torch.full_like(xd, float("nan"))
+        um.block_forward(ctx, [c.layer for c in cases], xd, yd, flags=flags)
+        y = yd.cpu().numpy()
+        assert np.all(np.isfinite(y))
+        err = normwise(y[keep], ref[keep])
+        say(f"  normwise={err:.3e} (near-ties {int(near.sum())})")
+        assert err <= tol, err

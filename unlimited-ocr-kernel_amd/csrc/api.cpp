@@ -9,7 +9,6 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
-#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -146,7 +145,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
-      chunk_base, h, hs, y, ys, xn, xb, gu, total;
+      h, hs, y, ys, xn, xb, gu, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -170,7 +169,6 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   p.tiles = take((size_t)uocr::max_tiles((int)T, (int)K, (int)E, 1) * 2 * 4);
   p.counters = take(16);
   p.chunk_counts = take((T + 15) / 16 * 64 * 4);
-  p.chunk_base = take((T + 15) / 16 * 64 * 4);
   p.h = take(T * K * I * 4);
   p.hs = take(T * S * 4);
   p.y = take(T * K * H * 4);
@@ -195,7 +193,6 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.tiles = reinterpret_cast<int*>(b + p.tiles);
   s.counters = reinterpret_cast<int*>(b + p.counters);
   s.chunk_counts = reinterpret_cast<int*>(b + p.chunk_counts);
-  s.chunk_base = reinterpret_cast<int*>(b + p.chunk_base);
   s.h = reinterpret_cast<float*>(b + p.h);
   s.hs = reinterpret_cast<float*>(b + p.hs);
   s.y = reinterpret_cast<float*>(b + p.y);
@@ -269,9 +266,36 @@ int read_and_clear_error(uocr_gpu_ctx* ctx) {
   return UOCR_OK;
 }
 
+// Engine of a forward: the one-token decode engine, the small-batch engine
+// (row tiles of <= 16 tokens, bandwidth-bound) for T <= 16 and for INT8
+// weights, the MFMA grouped GEMM for larger BF16 batches.
+enum class Engine { Decode, Batch, Mfma };
+
+Engine choose_engine(const uocr_moe_layer* layer, size_t T, uint32_t flags) {
+  const DeviceLayer& L = layer->dev;
+  bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
+              (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
+  if (L.quant_mode != UOCR_QUANT_NONE) mfma = false;
+  if (mfma) return Engine::Mfma;
+  if (T == 1 && uocr::decode_supported(L)) return Engine::Decode;
+  return Engine::Batch;
+}
+
+// bf16 planes of the layer input in scratch (the MFMA engine's A operand).
+void input_planes(const Scratch& S, const DeviceLayer& L, size_t T, uint32_t flags, uint16_t** hi,
+                  uint16_t** lo) {
+  *hi = S.xb;
+  *lo = (flags & UOCR_FLAG_BF16_ACTIVATIONS) ? nullptr : S.xb + T * L.H;
+}
+
+// planes_ready: the MFMA engine's input planes are already in scratch.
+// next: the following layer's RMSNorm, fused into this layer's combine (not
+// taken by the decode engine; *fused says whether it ran).
 int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
                     const float* residual, float* y, uint32_t flags,
-                    const uocr_moe_trace* trace, bool x_in_scratch) {
+                    const uocr_moe_trace* trace, bool x_in_scratch, bool planes_ready = false,
+                    const uocr::RowNorm* next = nullptr, bool* fused = nullptr) {
+  if (fused) *fused = false;
   const uocr_moe_config& c = layer->cfg;
   const ScratchPlan plan = plan_scratch(c, T);
   if (plan.total > ctx->scratch_limit)
@@ -282,16 +306,10 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
   hipStream_t st = ctx->stream;
-  // Engines: the one-token decode engine; the small-batch engine (row tiles
-  // of <= 16 tokens, bandwidth-bound) for T <= 16 and for INT8 weights; the
-  // MFMA grouped GEMM for larger BF16 batches.
-  bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
-              (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
-  if (L.quant_mode != UOCR_QUANT_NONE) {
-    if (flags & UOCR_FLAG_FORCE_MFMA)
-      return fail(UOCR_ERR_UNSUPPORTED, "the MFMA engine takes BF16 weights only");
-    mfma = false;
-  }
+  if (L.quant_mode != UOCR_QUANT_NONE && (flags & UOCR_FLAG_FORCE_MFMA))
+    return fail(UOCR_ERR_UNSUPPORTED, "the MFMA engine takes BF16 weights only");
+  const Engine engine = choose_engine(layer, T, flags);
+  const bool mfma = engine == Engine::Mfma;
   if (!mfma && !uocr::batch_supported(L))
     return fail(UOCR_ERR_UNSUPPORTED, "small-batch engine needs hidden and shared widths <= 2048");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
@@ -299,7 +317,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
-  if (!mfma && T == 1 && uocr::decode_supported(L)) {
+  if (engine == Engine::Decode) {
     // One token: three launches with no routing launch of their own (the
     // router rides with the shared gate/up, top-k with the routed gate/up).
     phase_begin(ctx, kRouter);
@@ -326,8 +344,8 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
       uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.chunk_counts,
-                                    S.chunk_base, S.offsets, S.perm_rows, S.perm_w, S.inv_pos,
-                                    S.tiles, S.counters, st);
+                                    S.offsets, S.perm_rows, S.perm_w, S.inv_pos, S.tiles,
+                                    S.counters, st);
       phase_end(ctx);
     } else {
       // MFMA engine forced on a small batch, or a hidden width beyond the
@@ -352,9 +370,11 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       P.h_lo = P.h_hi + T * L.K * L.I;
       P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
       P.hs_lo = P.hs_hi + T * L.S;
-      phase_begin(ctx, kSplit);
-      uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
-      phase_end(ctx);
+      if (!planes_ready) {
+        phase_begin(ctx, kSplit);
+        uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+        phase_end(ctx);
+      }
       phase_begin(ctx, kGateUp);
       uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, st);
       phase_end(ctx);
@@ -370,8 +390,9 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_end(ctx);
     }
     phase_begin(ctx, kCombine);
-    uocr::launch_combine(S, residual, Ti, L.H, L.K, y, st);
+    uocr::launch_combine(S, residual, Ti, L.H, L.K, y, next, st);
     phase_end(ctx);
+    if (fused) *fused = next != nullptr;
   }
   HIP_TRY(hipGetLastError(), "kernel launch");
   if (trace) {
@@ -712,21 +733,55 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
   if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
   if (T > (size_t)262144) return fail(UOCR_ERR_RESOURCE, "token count too large");
   HIP_TRY(hipSetDevice(ctx->device), "set device");
+  for (size_t l = 0; l < n_layers; l++) {
+    if (!layers[l]) return fail(UOCR_ERR_SHAPE, "null layer %zu", l);
+    if (!layers[l]->dev.norm_w) return fail(UOCR_ERR_FORMAT, "layer %zu has no norm weight", l);
+    if (plan_scratch(layers[l]->cfg, T).total > ctx->scratch_limit)
+      return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
+  }
+  // Layer l's RMSNorm (and the bf16 planes of its output when layer l uses
+  // the MFMA engine) runs fused into layer l - 1's combine when both layers
+  // have the same scratch layout and the combine is not the decode
+  // engine's; otherwise as a kernel of its own.
+  auto norm_of = [&](size_t l, const Scratch& S) {
+    const uocr_moe_layer* layer = layers[l];
+    uocr::RowNorm nn;
+    nn.w = layer->dev.norm_w;
+    nn.eps = layer->dev.eps;
+    nn.out = S.xn;
+    if (choose_engine(layer, T, flags) == Engine::Mfma && uocr::row_norm_fusable(layer->dev.H))
+      input_planes(S, layer->dev, T, flags, &nn.hi, &nn.lo);
+    return nn;
+  };
   const float* cur = x;
+  bool normed = false;  // layer l's norm already ran (fused)
   for (size_t l = 0; l < n_layers; l++) {
     const uocr_moe_layer* layer = layers[l];
-    if (!layer) return fail(UOCR_ERR_SHAPE, "null layer %zu", l);
-    if (!layer->dev.norm_w) return fail(UOCR_ERR_FORMAT, "layer %zu has no norm weight", l);
     const ScratchPlan plan = plan_scratch(layer->cfg, T);
-    if (plan.total > ctx->scratch_limit)
-      return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
     Scratch S = carve(ctx, plan);
-    phase_begin(ctx, kNorm);
-    uocr::launch_rms_norm(cur, (int)T, layer->dev.H, layer->dev.norm_w, layer->dev.eps, S.xn,
-                          S.err, ctx->stream);
-    phase_end(ctx);
-    int r = enqueue_experts(ctx, layer, S.xn, T, cur, y, flags, nullptr, true);
+    const uocr::RowNorm nn = norm_of(l, S);
+    if (!normed) {
+      phase_begin(ctx, kNorm);
+      uocr::launch_rms_norm(cur, (int)T, layer->dev.H, nn, S.err, ctx->stream);
+      phase_end(ctx);
+    }
+    uocr::RowNorm next;
+    bool want = false;
+    if (l + 1 < n_layers && uocr::row_norm_fusable(layer->dev.H)) {
+      // Same scratch layout: the shapes plan_scratch reads.
+      const uocr_moe_config &a = layer->cfg, &b = layers[l + 1]->cfg;
+      if (a.hidden_size == b.hidden_size && a.moe_intermediate_size == b.moe_intermediate_size &&
+          a.n_routed_experts == b.n_routed_experts && a.n_shared_experts == b.n_shared_experts &&
+          a.num_experts_per_tok == b.num_experts_per_tok) {
+        next = norm_of(l + 1, S);
+        want = true;
+      }
+    }
+    bool fused = false;
+    int r = enqueue_experts(ctx, layer, S.xn, T, cur, y, flags, nullptr, true, nn.hi != nullptr,
+                            want ? &next : nullptr, &fused);
     if (r) return r;
+    normed = fused;
     cur = y;
   }
   return UOCR_OK;
@@ -801,7 +856,11 @@ int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
     return fail(UOCR_ERR_SHAPE, "invalid normalization parameters");
   if (rows == 0) return UOCR_OK;
   HIP_TRY(hipSetDevice(ctx->device), "set device");
-  uocr::launch_rms_norm(x, (int)rows, (int)width, weight, eps, out, ctx->err, ctx->stream);
+  uocr::RowNorm nn;
+  nn.w = weight;
+  nn.eps = eps;
+  nn.out = out;
+  uocr::launch_rms_norm(x, (int)rows, (int)width, nn, ctx->err, ctx->stream);
   HIP_TRY(hipGetLastError(), "kernel launch");
   return read_and_clear_error(ctx);
 }

@@ -1,4 +1,5 @@
-// Ordered combine back to token order, and RMSNorm.
+// Ordered combine back to token order, and RMSNorm (fused into the combine
+// when a following layer's norm is given).
 //
 // Combine: out[t] = shared(x)[t], then for t's experts in ascending id,
 // out[t] += p * expert_out — one rounded multiply and one rounded add per
@@ -10,13 +11,78 @@
 
 namespace uocr {
 
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ ys,
-                                                      const float* __restrict__ y,
-                                                      const int* __restrict__ ids,
-                                                      const float* __restrict__ w,
-                                                      const int* __restrict__ inv_pos,
-                                                      const float* __restrict__ residual, int H,
-                                                      int K, float* __restrict__ out) {
+// One row (token) per workgroup of 256 threads; thread i holds float4
+// chunks i and i + 256 of the row (widths up to 2048).
+constexpr int kRowThreads = 256, kRowChunks = 2;
+
+// RMSNorm of a row held as float4 chunks (src/cpu/ops.rs:362-423, center =
+// false): variance = sum(v^2) / W, scale = 1 / sqrt(variance + eps),
+// out = v * scale * w. Non-finite row or weight -> Numerical (:382-389).
+// The sum runs per thread over its chunks (x, y, z, w in turn), then over
+// the wave and the four waves in order, so the standalone and the fused
+// norms give the same bits. Writes the normalised row and, when hi is set,
+// its bf16 planes (hi = bf16(v), lo = bf16(v - hi) when lo is set).
+__device__ inline void norm_row(const float4 (&v)[kRowChunks], int width, const float* __restrict__ w,
+                                float eps, float* __restrict__ out, uint16_t* __restrict__ hi,
+                                uint16_t* __restrict__ lo, int* err) {
+  __shared__ float partial[kRowThreads / 64];
+  __shared__ int bad_any;
+  const int tid = threadIdx.x;
+  if (tid == 0) bad_any = 0;
+  __syncthreads();
+  float ss = 0.0f;
+  bool bad = false;
+  float4 wv[kRowChunks];
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (tid + kRowThreads * it) * 4;
+    if (i >= width) break;
+    wv[it] = *reinterpret_cast<const float4*>(w + i);
+    const float4 x = v[it];
+    bad |= !isfinite(x.x) || !isfinite(x.y) || !isfinite(x.z) || !isfinite(x.w);
+    bad |= !isfinite(wv[it].x) || !isfinite(wv[it].y) || !isfinite(wv[it].z) || !isfinite(wv[it].w);
+    ss = fmaf(x.x, x.x, ss);
+    ss = fmaf(x.y, x.y, ss);
+    ss = fmaf(x.z, x.z, ss);
+    ss = fmaf(x.w, x.w, ss);
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) partial[tid >> 6] = ss;
+  if (bad) bad_any = 1;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  if (bad_any && tid == 0) raise_error(err, kErrNumerical);
+  const float scale = 1.0f / sqrtf(total / (float)width + eps);
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (tid + kRowThreads * it) * 4;
+    if (i >= width) break;
+    const float4 x = v[it];
+    const float o[4] = {x.x * scale * wv[it].x, x.y * scale * wv[it].y, x.z * scale * wv[it].z,
+                        x.w * scale * wv[it].w};
+    *reinterpret_cast<float4*>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+    if (hi) {
+      uint16_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        h[j] = __builtin_bit_cast(uint16_t, (__bf16)o[j]);
+        l[j] = __builtin_bit_cast(uint16_t, (__bf16)(o[j] - __uint_as_float((uint32_t)h[j] << 16)));
+      }
+      *reinterpret_cast<uint2*>(hi + i) =
+          make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+      if (lo)
+        *reinterpret_cast<uint2*>(lo + i) =
+            make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    }
+  }
+}
+
+// Combine, then (NORM) the next layer's RMSNorm of the result.
+template <bool NORM>
+__global__ __launch_bounds__(kRowThreads) void combine_kernel(
+    const float* __restrict__ ys, const float* __restrict__ y, const int* __restrict__ ids,
+    const float* __restrict__ w, const int* __restrict__ inv_pos, const float* __restrict__ residual,
+    int H, int K, float* __restrict__ out, RowNorm nn, int* err) {
   const int t = blockIdx.x;
   int e[8], pos[8];
   float p[8];
@@ -38,7 +104,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       }
     }
   }
-  for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
+  float4 row[kRowChunks];
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (threadIdx.x + kRowThreads * it) * 4;
+    if (i >= H) break;
     float4 acc = *reinterpret_cast<const float4*>(ys + (size_t)t * H + i);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -58,22 +128,43 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       acc.w = r.w + acc.w;
     }
     *reinterpret_cast<float4*>(out + (size_t)t * H + i) = acc;
+    row[it] = acc;
   }
+  if constexpr (NORM)
+    norm_row(row, H, nn.w, nn.eps, nn.out + (size_t)t * H, nn.hi ? nn.hi + (size_t)t * H : nullptr,
+             nn.lo ? nn.lo + (size_t)t * H : nullptr, err);
 }
 
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
-                    hipStream_t s) {
+                    const RowNorm* next, hipStream_t s) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, s, S.ys, S.y, S.topk_ids, S.topk_w,
-                     S.inv_pos, residual, H, K, out);
+  if (next)
+    combine_kernel<true><<<T, kRowThreads, 0, s>>>(S.ys, S.y, S.topk_ids, S.topk_w, S.inv_pos,
+                                                   residual, H, K, out, *next, S.err);
+  else
+    combine_kernel<false><<<T, kRowThreads, 0, s>>>(S.ys, S.y, S.topk_ids, S.topk_w, S.inv_pos,
+                                                    residual, H, K, out, RowNorm{}, S.err);
 }
 
-// RMSNorm (src/cpu/ops.rs:362-423, center = false): variance = sum(v^2)/W,
-// scale = 1/sqrt(variance + eps), out = v * scale * w. Non-finite input ->
-// Numerical (:382-389). One workgroup per row.
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, int width,
-                                                       const float* __restrict__ w, float eps,
-                                                       float* __restrict__ out, int* err) {
+__global__ __launch_bounds__(kRowThreads) void rms_norm_kernel(const float* __restrict__ x, int width,
+                                                               RowNorm nn, int* err) {
+  const int t = blockIdx.x;
+  float4 row[kRowChunks];
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (threadIdx.x + kRowThreads * it) * 4;
+    if (i >= width) break;
+    row[it] = *reinterpret_cast<const float4*>(x + (size_t)t * width + i);
+  }
+  norm_row(row, width, nn.w, nn.eps, nn.out + (size_t)t * width,
+           nn.hi ? nn.hi + (size_t)t * width : nullptr, nn.lo ? nn.lo + (size_t)t * width : nullptr,
+           err);
+}
+
+// Wider rows: one workgroup per row, scalar passes.
+__global__ __launch_bounds__(256) void rms_norm_wide_kernel(const float* __restrict__ x, int width,
+                                                            const float* __restrict__ w, float eps,
+                                                            float* __restrict__ out, int* err) {
   __shared__ float partial[4];
   __shared__ int bad_any;
   const int row = blockIdx.x;
@@ -100,10 +191,15 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
   for (int i = threadIdx.x; i < width; i += blockDim.x) out[(size_t)row * width + i] = in[i] * scale * w[i];
 }
 
-void launch_rms_norm(const float* x, int rows, int width, const float* w, float eps, float* out,
-                     int* err, hipStream_t s) {
+bool row_norm_fusable(int width) { return width % 4 == 0 && width <= kRowThreads * kRowChunks * 4; }
+
+void launch_rms_norm(const float* x, int rows, int width, const RowNorm& nn, int* err,
+                     hipStream_t s) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, width, w, eps, out, err);
+  if (row_norm_fusable(width))
+    rms_norm_kernel<<<rows, kRowThreads, 0, s>>>(x, width, nn, err);
+  else
+    rms_norm_wide_kernel<<<rows, 256, 0, s>>>(x, width, nn.w, nn.eps, nn.out, err);
 }
 
 }  // namespace uocr

@@ -7,6 +7,7 @@
 // in ascending id (:198-218); the permutation below is that order.
 #include "common.hpp"
 #include "moe_kernels.hpp"
+#include "rowdot.hpp"
 
 namespace uocr {
 
@@ -139,34 +140,61 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 // chunks v, v+16, ... per expert (lane = expert), the 16 wave totals are
 // scanned, and each (chunk, expert) gets its first dispatched slot. Wave 0
 // then lists the row tiles.
-constexpr int kChunk = 16;
-constexpr int kScanMaxChunks = 256;  // 4096 tokens per scan pass
+constexpr int kChunk = 16;          // tokens per router chunk
+constexpr int kFusedThreads = 256;  // 16 chunk rows x 16 expert quads per pass
 
-__global__ __launch_bounds__(1024) void dispatch_scan_kernel(
-    const int* __restrict__ chunk_counts, int nchunks, int T, int E, int K, int bm,
-    int* __restrict__ chunk_base, int* __restrict__ offsets, int* __restrict__ tiles,
-    int* __restrict__ counters) {
-  __shared__ int cc[kScanMaxChunks][64];
-  __shared__ int wave_total[16][64];
-  __shared__ int expert_total[64];
-  __shared__ int carry[64];
+// Dispatch for the chunked router (one workgroup per 16-token chunk, no
+// second launch): every workgroup sums the router's per-chunk expert counts
+// over all chunks (the expert totals, hence the expert offsets) and over
+// the chunks before its own (its chunk's first slot per expert), then
+// places its tokens: a token's rank among earlier tokens of the same expert
+// inside the chunk comes from a ballot. Workgroup 0 also writes the offsets,
+// the row tiles and the tile counters. The slot of (token t, expert e) is
+// offsets[e] + (count of e in earlier chunks) + (rank of t in its chunk):
+// tokens in ascending order within each expert, as the reference's stable
+// dispatch (src/decoder/mod.rs:124-183).
+__global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
+    const int* __restrict__ chunk_counts, const int* __restrict__ ids, const float* __restrict__ w,
+    int nchunks, int T, int E, int K, int bm, int* __restrict__ offsets,
+    int* __restrict__ perm_rows, float* __restrict__ perm_w, int* __restrict__ inv_pos,
+    int* __restrict__ tiles, int* __restrict__ counters) {
+  __shared__ __attribute__((aligned(16))) int part_tot[16][64];
+  __shared__ __attribute__((aligned(16))) int part_bef[16][64];
+  __shared__ int base[64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  if (tid < 64) carry[tid] = 0;
-  // Pass 1: totals per expert over all chunks.
-  int mine = 0;
-  for (int c = wave; c < nchunks; c += 16) mine += chunk_counts[(size_t)c * 64 + lane];
-  wave_total[wave][lane] = mine;
-  __syncthreads();
-  if (tid < 64) {
-    int total = 0;
-    for (int v = 0; v < 16; v++) total += wave_total[v][tid];
-    expert_total[tid] = tid < E ? total : 0;
+  const int c = blockIdx.x;
+  // Thread (row = tid / 16, quad = tid % 16) sums experts 4 quad .. 4 quad + 3
+  // of chunks row, row + 16, ...; 16 loads in flight per pass, chunks past
+  // the end read as zero.
+  const int row = tid >> 4, quad = tid & 15;
+  const __amdgpu_buffer_rsrc_t cr = make_rsrc(chunk_counts, (uint32_t)nchunks * 64u * 4u);
+  u32x4 tot = {0u, 0u, 0u, 0u}, bef = {0u, 0u, 0u, 0u};
+  for (int c0 = 0; c0 < nchunks; c0 += 256) {
+    u32x4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t cc = (uint32_t)(c0 + 16 * i + row);
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(cr, (cc * 64u + 4u * quad) * 4u, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      tot += v[i];
+      if (c0 + 16 * i + row < c) bef += v[i];
+    }
   }
+  *reinterpret_cast<u32x4*>(&part_tot[row][4 * quad]) = tot;
+  *reinterpret_cast<u32x4*>(&part_bef[row][4 * quad]) = bef;
   __syncthreads();
   if (wave == 0) {
-    const int total = expert_total[lane];
+    int total = 0, before = 0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      total += part_tot[r][lane];
+      before += part_bef[r][lane];
+    }
+    if (lane >= E) total = 0;
     int incl = total;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -174,70 +202,37 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
       if (lane >= o) incl += v;
     }
     const int excl = incl - total;
-    if (lane < E) offsets[lane] = excl;
-    if (lane == 0) offsets[E] = T * K;
-    carry[lane] = excl;
-    const int nt = lane < E ? (total + bm - 1) / bm : 0;
-    int tincl = nt;
+    base[lane] = excl + before;
+    if (c == 0) {
+      if (lane < E) offsets[lane] = excl;
+      if (lane == 0) offsets[E] = T * K;
+      const int nt = lane < E ? (total + bm - 1) / bm : 0;
+      int tincl = nt;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(tincl, o);
-      if (lane >= o) tincl += v;
-    }
-    const int tstart = tincl - nt;
-    for (int i = 0; i < nt; i++) {
-      tiles[2 * (tstart + i)] = lane;
-      tiles[2 * (tstart + i) + 1] = i * bm;
-    }
-    const int routed_tiles = __shfl(tincl, 63);
-    const int shared_tiles = (T + bm - 1) / bm;
-    for (int i = lane; i < shared_tiles; i += 64) {
-      tiles[2 * (routed_tiles + i)] = E;
-      tiles[2 * (routed_tiles + i) + 1] = i * bm;
-    }
-    if (lane == 0) {
-      counters[0] = routed_tiles + shared_tiles;
-      counters[1] = routed_tiles;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(tincl, o);
+        if (lane >= o) tincl += v;
+      }
+      const int tstart = tincl - nt;
+      for (int i = 0; i < nt; i++) {
+        tiles[2 * (tstart + i)] = lane;
+        tiles[2 * (tstart + i) + 1] = i * bm;
+      }
+      const int routed_tiles = __shfl(tincl, 63);
+      const int shared_tiles = (T + bm - 1) / bm;
+      for (int i = lane; i < shared_tiles; i += 64) {
+        tiles[2 * (routed_tiles + i)] = E;
+        tiles[2 * (routed_tiles + i) + 1] = i * bm;
+      }
+      if (lane == 0) {
+        counters[0] = routed_tiles + shared_tiles;
+        counters[1] = routed_tiles;
+      }
     }
   }
   __syncthreads();
-  // Pass 2: chunk bases, kScanMaxChunks chunks at a time through LDS.
-  for (int c0 = 0; c0 < nchunks; c0 += kScanMaxChunks) {
-    const int nc = min(kScanMaxChunks, nchunks - c0);
-    for (int i = tid; i < nc * 64; i += 1024) cc[i >> 6][i & 63] = chunk_counts[(size_t)c0 * 64 + i];
-    __syncthreads();
-    // Wave v owns a contiguous run of chunks.
-    const int per = (nc + 15) / 16;
-    const int cb = wave * per, ce = min(nc, cb + per);
-    int run = 0;
-    for (int c = cb; c < ce; c++) run += cc[c][lane];
-    wave_total[wave][lane] = run;
-    __syncthreads();
-    int before = carry[lane];
-    for (int v = 0; v < wave; v++) before += wave_total[v][lane];
-    for (int c = cb; c < ce; c++) {
-      chunk_base[(size_t)(c0 + c) * 64 + lane] = before;
-      before += cc[c][lane];
-    }
-    __syncthreads();
-    if (tid < 64) {
-      int add = 0;
-      for (int v = 0; v < 16; v++) add += wave_total[v][tid];
-      carry[tid] += add;
-    }
-    __syncthreads();
-  }
-}
-
-// Scatter: one wave per chunk (lanes past the chunk idle); a token's rank
-// among earlier tokens of the same expert inside the chunk comes from a
-// ballot.
-__global__ __launch_bounds__(64) void dispatch_scatter_kernel(
-    const int* __restrict__ ids, const float* __restrict__ w, int T, int E, int K,
-    const int* __restrict__ chunk_base, int* __restrict__ perm_rows, float* __restrict__ perm_w,
-    int* __restrict__ inv_pos) {
-  const int lane = threadIdx.x;
-  const int c = blockIdx.x;
+  if (wave != 0) return;
+  // Place the chunk's tokens (lanes past the chunk idle).
   const int t = c * kChunk + lane;
   const bool valid = lane < kChunk && t < T;
   int my_e[8], my_rank[8];
@@ -263,7 +258,7 @@ __global__ __launch_bounds__(64) void dispatch_scatter_kernel(
   for (int j = 0; j < 8; j++) {
     if (j < K) {
       const int e = my_e[j];
-      const int pos = chunk_base[(size_t)c * 64 + e] + my_rank[j];
+      const int pos = base[e] + my_rank[j];
       perm_rows[pos] = t;
       perm_w[pos] = w[(size_t)t * K + j];
       inv_pos[(size_t)t * K + j] = pos;
@@ -272,14 +267,12 @@ __global__ __launch_bounds__(64) void dispatch_scatter_kernel(
 }
 
 void launch_dispatch_chunked(const int* ids, const float* w, int T, int E, int K, int bm,
-                             const int* chunk_counts, int* chunk_base, int* offsets,
-                             int* perm_rows, float* perm_w, int* inv_pos, int* tiles,
-                             int* counters, hipStream_t s) {
+                             const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
+                             int* inv_pos, int* tiles, int* counters, hipStream_t s) {
   const int nchunks = (T + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_counts, nchunks, T,
-                     E, K, bm, chunk_base, offsets, tiles, counters);
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nchunks), dim3(64), 0, s, ids, w, T, E, K,
-                     chunk_base, perm_rows, perm_w, inv_pos);
+  hipLaunchKernelGGL(dispatch_fused_kernel, dim3(nchunks), dim3(kFusedThreads), 0, s, chunk_counts,
+                     ids, w, nchunks, T, E, K, bm, offsets, perm_rows, perm_w, inv_pos, tiles,
+                     counters);
 }
 
 void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,

@@ -47,7 +47,6 @@ struct Scratch {
   int* tiles;       // [max_tiles*2] (group, first row) per row tile
   int* counters;    // [4]: row tiles, routed row tiles
   int* chunk_counts;  // [ceil(T/16), 64] per-chunk expert counts (router)
-  int* chunk_base;    // [ceil(T/16), 64] first dispatched slot per (chunk, expert)
   float* h;         // [T*K, I] routed hidden in dispatched order
   float* hs;        // [T, S] shared hidden
   float* y;         // [T*K, H] routed expert outputs in dispatched order
@@ -74,9 +73,8 @@ void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, in
 
 // dispatch.hip
 void launch_dispatch_chunked(const int* ids, const float* w, int T, int E, int K, int bm,
-                             const int* chunk_counts, int* chunk_base, int* offsets,
-                             int* perm_rows, float* perm_w, int* inv_pos, int* tiles,
-                             int* counters, hipStream_t s);
+                             const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
+                             int* inv_pos, int* tiles, int* counters, hipStream_t s);
 void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,
                      int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
                      hipStream_t s);
@@ -130,9 +128,22 @@ void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, cons
                          float* out, hipStream_t s);
 
 // combine.hip
+// RMSNorm output of a row: the normalised row (out) and optionally its
+// bf16 planes (hi, and lo for FP32-class precision).
+struct RowNorm {
+  const float* w = nullptr;
+  float eps = 0.0f;
+  float* out = nullptr;
+  uint16_t* hi = nullptr;
+  uint16_t* lo = nullptr;
+};
+// Combine; with `next`, also the following layer's RMSNorm of the result.
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
-                    hipStream_t s);
-void launch_rms_norm(const float* x, int rows, int width, const float* w, float eps, float* out,
-                     int* err, hipStream_t s);
+                    const RowNorm* next, hipStream_t s);
+// Rows of width <= 2048 (multiple of 4) take the fused norm (planes too);
+// wider rows a plain one (no planes).
+bool row_norm_fusable(int width);
+void launch_rms_norm(const float* x, int rows, int width, const RowNorm& nn, int* err,
+                     hipStream_t s);
 
 }  // namespace uocr
