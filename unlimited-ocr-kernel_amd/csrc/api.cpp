@@ -390,7 +390,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_end(ctx);
     }
     phase_begin(ctx, kCombine);
-    uocr::launch_combine(S, residual, Ti, L.H, L.K, y, next, st);
+    uocr::launch_combine(S, residual, Ti, L.H, L.K, y, next, mfma && bf16_only, st);
     phase_end(ctx);
     if (fused) *fused = next != nullptr;
   }

@@ -77,8 +77,21 @@ __device__ inline void norm_row(const float4 (&v)[kRowChunks], int width, const 
   }
 }
 
-// Combine, then (NORM) the next layer's RMSNorm of the result.
-template <bool NORM>
+// Four consecutive values of an f32 row, or of a bf16 row (Y16).
+template <bool Y16>
+__device__ __forceinline__ float4 load4(const float* __restrict__ row, int i) {
+  if constexpr (Y16) {
+    const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(row) + i);
+    return make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u),
+                       __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xffff0000u));
+  } else {
+    return *reinterpret_cast<const float4*>(row + i);
+  }
+}
+
+// Combine, then (NORM) the next layer's RMSNorm of the result. Y16: the
+// expert outputs (routed and shared) are bf16 rows (BF16 activations).
+template <bool NORM, bool Y16>
 __global__ __launch_bounds__(kRowThreads) void combine_kernel(
     const float* __restrict__ ys, const float* __restrict__ y, const int* __restrict__ ids,
     const float* __restrict__ w, const int* __restrict__ inv_pos, const float* __restrict__ residual,
@@ -109,11 +122,12 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(
   for (int it = 0; it < kRowChunks; it++) {
     const int i = (threadIdx.x + kRowThreads * it) * 4;
     if (i >= H) break;
-    float4 acc = *reinterpret_cast<const float4*>(ys + (size_t)t * H + i);
+    const size_t rs = Y16 ? (size_t)H / 2 : (size_t)H;  // row stride in floats
+    float4 acc = load4<Y16>(ys + t * rs, i);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       if (j < K) {
-        const float4 v = *reinterpret_cast<const float4*>(y + (size_t)pos[j] * H + i);
+        const float4 v = load4<Y16>(y + pos[j] * rs, i);
         acc.x = acc.x + p[j] * v.x;
         acc.y = acc.y + p[j] * v.y;
         acc.z = acc.z + p[j] * v.z;
@@ -136,14 +150,21 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(
 }
 
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
-                    const RowNorm* next, hipStream_t s) {
+                    const RowNorm* next, bool y16, hipStream_t s) {
   if (T <= 0) return;
-  if (next)
-    combine_kernel<true><<<T, kRowThreads, 0, s>>>(S.ys, S.y, S.topk_ids, S.topk_w, S.inv_pos,
-                                                   residual, H, K, out, *next, S.err);
+  const RowNorm nn = next ? *next : RowNorm{};
+#define UOCR_COMBINE(NORM, Y16)                                                               \
+  combine_kernel<NORM, Y16><<<T, kRowThreads, 0, s>>>(S.ys, S.y, S.topk_ids, S.topk_w,         \
+                                                      S.inv_pos, residual, H, K, out, nn, S.err)
+  if (next && y16)
+    UOCR_COMBINE(true, true);
+  else if (next)
+    UOCR_COMBINE(true, false);
+  else if (y16)
+    UOCR_COMBINE(false, true);
   else
-    combine_kernel<false><<<T, kRowThreads, 0, s>>>(S.ys, S.y, S.topk_ids, S.topk_w, S.inv_pos,
-                                                    residual, H, K, out, RowNorm{}, S.err);
+    UOCR_COMBINE(false, false);
+#undef UOCR_COMBINE
 }
 
 __global__ __launch_bounds__(kRowThreads) void rms_norm_kernel(const float* __restrict__ x, int width,

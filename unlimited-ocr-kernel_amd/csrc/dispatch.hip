@@ -148,7 +148,7 @@ constexpr int kFusedThreads = 256;  // 16 chunk rows x 16 expert quads per pass
 // over all chunks (the expert totals, hence the expert offsets) and over
 // the chunks before its own (its chunk's first slot per expert), then
 // places its tokens: a token's rank among earlier tokens of the same expert
-// inside the chunk comes from a ballot. Workgroup 0 also writes the offsets,
+// inside the chunk comes from a per-expert token mask. Workgroup 0 also writes the offsets,
 // the row tiles and the tile counters. The slot of (token t, expert e) is
 // offsets[e] + (count of e in earlier chunks) + (rank of t in its chunk):
 // tokens in ascending order within each expert, as the reference's stable
@@ -161,6 +161,7 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
   __shared__ __attribute__((aligned(16))) int part_tot[16][64];
   __shared__ __attribute__((aligned(16))) int part_bef[16][64];
   __shared__ int base[64];
+  __shared__ unsigned long long emask[64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -230,35 +231,28 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
       }
     }
   }
+  if (tid < 64) emask[tid] = 0ull;
   __syncthreads();
   if (wave != 0) return;
-  // Place the chunk's tokens (lanes past the chunk idle).
+  // Place the chunk's tokens (lanes past the chunk idle): bit t of emask[e]
+  // is set when token t of the chunk selected expert e, so a token's rank
+  // among the chunk's earlier tokens of that expert is a popcount. One wave
+  // sets and reads the masks; its LDS operations complete in order.
   const int t = c * kChunk + lane;
   const bool valid = lane < kChunk && t < T;
-  int my_e[8], my_rank[8];
+  int my_e[8];
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     my_e[j] = (valid && j < K) ? ids[(size_t)t * K + j] : -1;
-    my_rank[j] = 0;
-  }
-  const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  for (int e = 0; e < E; e++) {
-    bool has = false;
-#pragma unroll
-    for (int j = 0; j < 8; j++) has |= my_e[j] == e;
-    const unsigned long long mask = __ballot(has);
-    if (!mask) continue;
-    const int r = __popcll(mask & lt);
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-      if (my_e[j] == e) my_rank[j] = r;
+    if (my_e[j] >= 0) atomicOr(&emask[my_e[j]], 1ull << lane);
   }
   if (!valid) return;
+  const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     if (j < K) {
       const int e = my_e[j];
-      const int pos = base[e] + my_rank[j];
+      const int pos = base[e] + __popcll(emask[e] & lt);
       perm_rows[pos] = t;
       perm_w[pos] = w[(size_t)t * K + j];
       inv_pos[(size_t)t * K + j] = pos;

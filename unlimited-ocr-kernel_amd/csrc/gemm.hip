@@ -335,7 +335,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
         }
     }
   } else {
+    // FP32-class: y in f32. BF16 activations: y rounded to bf16 (the
+    // combine's operands), in the first half of the same buffer.
     float* out = routed ? S.y : S.ys;
+    uint16_t* out16 = reinterpret_cast<uint16_t*>(out);
 #pragma unroll
     for (int mi = 0; mi < 4; mi++)
 #pragma unroll
@@ -345,7 +348,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row < mrows) out[(size_t)(base + r0 + row) * L.H + col] = acc[mi][ni][r];
+          if (row >= mrows) continue;
+          const size_t at = (size_t)(base + r0 + row) * L.H + col;
+          if constexpr (SPLIT)
+            out[at] = acc[mi][ni][r];
+          else
+            out16[at] = bf16_bits(acc[mi][ni][r]);
         }
       }
   }

@@ -138,8 +138,9 @@ struct RowNorm {
   uint16_t* lo = nullptr;
 };
 // Combine; with `next`, also the following layer's RMSNorm of the result.
+// y16: the expert outputs are bf16 rows (MFMA engine, BF16 activations).
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
-                    const RowNorm* next, hipStream_t s);
+                    const RowNorm* next, bool y16, hipStream_t s);
 // Rows of width <= 2048 (multiple of 4) take the fused norm (planes too);
 // wider rows a plain one (no planes).
 bool row_norm_fusable(int width);
