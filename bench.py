@@ -10,7 +10,9 @@ MoE-layer tokens/s = 4096 * 12 / step time, inputs resident in HBM.
 Secondary workloads (same JSON line, "secondary"): batch-1 decode with the
 INT8 block-32 overlay and with BF16 weights (rotating over 12 distinct layers
 so the 256 MB MALL cannot hold the working set), and the 1024-token prefill
-with Zipf(1.1) expert popularity in both activation precision classes.
+with Zipf(1.1) expert popularity in both activation precision classes, and
+the vocabulary projection (final RMSNorm + 129280 x 1280 lm_head) in BF16,
+INT8 weight-only and W8A8.
 
 The CPU baseline is the C oracle (a restatement of the reference's scalar
 x86 path) on a bounded sample of the headline workload.
@@ -47,7 +49,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--secondary", default="decode_int8,decode_bf16,decode_int8_t16,prefill1024",
+    ap.add_argument("--secondary",
+                    default="decode_int8,decode_bf16,decode_int8_t16,prefill1024,lm_head_bf16,"
+                            "lm_head_int8,lm_head_w8a8",
                     help="comma list of secondary workloads, or 'none'")
     ap.add_argument("--cpu-sample", type=int, default=512,
                     help="tokens of the headline workload timed on the CPU oracle (0: skip)")
@@ -267,6 +271,57 @@ def main():
                                    4)})
             log(f"prefill1024 {cls}: {ms:.3f} ms")
         layer.close()
+
+    # ------------------------------------------------ vocabulary projection
+    def lm_head(kind: str):
+        """Decoder::logits at the model's shape: the final RMSNorm of one
+        hidden row, then the 129280 x 1280 projection (BF16, or INT8 block-32
+        weight-only / W8A8), two matrices alternating so that the 256 MB MALL
+        cannot serve them."""
+        V = 129280
+        log(f"lm_head {kind}: {V} x {H}")
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(7)
+        norm = torch.rand(H, generator=gen, device="cuda") + 0.5
+        heads = []
+        for i in range(2):
+            if kind == "bf16":
+                w = (torch.randn((V, H), generator=gen, device="cuda") * 0.02).to(
+                    torch.bfloat16).view(torch.int16)
+                heads.append(um.LmHead(ctx, norm, 1e-6, weight=w, where=um.MEMORY_DEVICE))
+            else:
+                q = torch.randint(-127, 128, (V, H), generator=gen, device="cuda",
+                                  dtype=torch.int32).to(torch.int8)
+                sc = torch.rand((V, H // 32), generator=gen, device="cuda") * 0.002 + 0.001
+                mode = um.QUANT_WEIGHTS_ONLY if kind == "int8" else um.QUANT_DYNAMIC
+                heads.append(um.LmHead(ctx, norm, 1e-6, q=q, scales=sc, mode=mode,
+                                       where=um.MEMORY_DEVICE))
+            torch.cuda.empty_cache()
+        hidden = torch.randn((4, H), generator=gen, device="cuda")
+        logits = torch.empty(V, device="cuda")
+        for i in range(4):
+            heads[i % 2].logits(ctx, hidden, logits, sync=False)
+        sync()
+        n = max(args.steps, 1) * 20
+        t0 = time.perf_counter()
+        for i in range(n):
+            heads[i % 2].logits(ctx, hidden, logits, sync=False)
+        sync()
+        us = (time.perf_counter() - t0) * 1e6 / n
+        nbytes = V * H * 2 if kind == "bf16" else V * H + V * (H // 32) * 4
+        for h in heads:
+            h.close()
+        torch.cuda.empty_cache()
+        log(f"lm_head {kind}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
+        return {"workload": f"lm-head-{kind}-129280x1280", "value": round(1e6 / us, 1),
+                "unit": "projections/s", "us_per_call": round(us, 2),
+                "algorithmic_bytes": int(nbytes),
+                "hbm_frac_wall": round(nbytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    for key, kind in (("lm_head_bf16", "bf16"), ("lm_head_int8", "int8"),
+                      ("lm_head_w8a8", "w8a8")):
+        if key in wanted:
+            secondary.append(lm_head(key.split("_")[-1]))
 
     # --------------------------------------------------------- CPU baseline
     cpu = None

@@ -9,11 +9,13 @@
 //   Int8Matrix /
 //   QuantizedWeights            src/cpu/quantized.rs:9-42, 239-369 (overlay)
 //   ModelConfig                 src/model/config.rs:30-115
-//   Model                       src/model/mod.rs:60-109 and the MoE seam of
+//   Model                       src/model/mod.rs:60-109, the MoE seam of
 //                               Decoder (src/decoder/mod.rs:32-88, 124-220)
+//                               and Decoder::logits (:367-379)
 // Errors are thrown as OcrError; the C entry points return the same kinds as
 // status codes. Vision, tokenizer, attention and generation are not part of
-// this library: Model holds the MoE layers of the decoder.
+// this library: Model holds the MoE layers of the decoder and its
+// vocabulary projection.
 #pragma once
 
 #include <cstddef>
@@ -197,6 +199,12 @@ class Model {
                uint32_t flags = UOCR_FLAG_FP32_CLASS) const;
   void experts(uocr_gpu_ctx* gpu, size_t layer, const float* x, size_t T, float* y,
                uint32_t flags = UOCR_FLAG_FP32_CLASS) const;
+  // Decoder::logits (src/decoder/mod.rs:367-379): logits[vocab_size] of the
+  // last row of hidden[T, H] (device pointers); synchronous. T == 0 ->
+  // Shape.
+  void logits(CpuContext& cpu, const float* hidden, size_t T, float* logits) const;
+  void logits(uocr_gpu_ctx* gpu, const float* hidden, size_t T, float* logits) const;
+  const uocr_lm_head* lm_head() const { return lm_head_; }
 
  private:
   Model() = default;
@@ -204,6 +212,7 @@ class Model {
   bool quantized_ = false;
   QuantizationMode mode_ = QuantizationMode::WeightsOnly;
   std::vector<uocr_moe_layer*> layers_;  // per decoder layer, null if dense
+  uocr_lm_head* lm_head_ = nullptr;       // final norm + lm_head.weight
 };
 
 }  // namespace uocr

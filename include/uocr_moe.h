@@ -227,6 +227,36 @@ int uocr_int8_linear_dynamic(uocr_gpu_ctx* ctx, const int8_t* q, const float* sc
 int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
                   const float* weight, float eps, float* out);
 
+/* ------------------------------------------------- vocabulary projection */
+/* Decoder::logits (src/decoder/mod.rs:367-379): the last hidden row,
+ * RMSNorm with model.norm.weight, then Decoder::projection (:99-112) with
+ * lm_head.weight — BF16, or the INT8 overlay's lm_head.weight
+ * (src/cpu/quantized.rs:267-269): weight-only, or W8A8 under
+ * DynamicActivations (the projected row is a single row). */
+typedef struct uocr_lm_head uocr_lm_head;
+typedef struct uocr_lm_head_weights {
+  uint32_t vocab_size;   /* V, rows of lm_head.weight */
+  uint32_t hidden_size;  /* H */
+  float rms_norm_eps;
+  const float* norm_weight;  /* model.norm.weight widened to f32, [H] */
+  const uint16_t* weight;    /* lm_head.weight bf16 bits [V, H]; may be NULL with q */
+  const int8_t* q;           /* overlay lm_head.weight [V, H], or NULL */
+  const float* scales;       /* its .q8_scales [V, H/32] */
+  uocr_quant_mode quant_mode; /* UOCR_QUANT_NONE when q is NULL */
+} uocr_lm_head_weights;
+int uocr_lm_head_create(uocr_gpu_ctx* ctx, const uocr_lm_head_weights* w, uocr_memory where,
+                        uocr_lm_head** out);
+/* logits[V] of hidden[T, H] (device pointers): its last row. T == 0 ->
+ * Shape ("missing final hidden state"); non-finite row -> Numerical. */
+int uocr_lm_head_logits(uocr_gpu_ctx* ctx, const uocr_lm_head* head, const float* hidden,
+                        size_t T, float* logits);
+int uocr_lm_head_logits_async(uocr_gpu_ctx* ctx, const uocr_lm_head* head, const float* hidden,
+                              size_t T, float* logits);
+/* "bf16_weights_fp32", "int8_weights_fp32", "int8_weights_dynamic_activations". */
+const char* uocr_lm_head_precision(const uocr_lm_head* head);
+size_t uocr_lm_head_device_bytes(const uocr_lm_head* head);
+void uocr_lm_head_destroy(uocr_lm_head* head);
+
 /* ---------------------------------------------------- checkpoint files */
 /* The model-directory side of Model::load_with_quantization; the C++ form
  * of each is in uocr.hpp. */
@@ -302,6 +332,10 @@ const uocr_moe_layer* uocr_model_layer(const uocr_model* model, size_t layer);
  * y[T,H] from x[T,H], device pointers; synchronous. */
 int uocr_model_experts(uocr_gpu_ctx* ctx, const uocr_model* model, size_t layer, const float* x,
                        size_t T, float* y, uint32_t flags);
+/* Decoder::logits of a loaded model: logits[vocab_size] of the last row of
+ * hidden[T, H] (device pointers); synchronous. */
+int uocr_model_logits(uocr_gpu_ctx* ctx, const uocr_model* model, const float* hidden, size_t T,
+                      float* logits);
 void uocr_model_destroy(uocr_model* model);
 
 #ifdef __cplusplus

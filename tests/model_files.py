@@ -86,7 +86,7 @@ def model_dir(directory, s: dict = MOE_TINY, seed: int = 5, drop=(), reshape=Non
     t, moe = {}, {}
     t["model.embed_tokens.weight"] = bf16(normal((s["vocab"], H)))
     t["lm_head.weight"] = bf16(normal((s["vocab"], H)))
-    t["model.norm.weight"] = bf16(np.ones(H))
+    t["model.norm.weight"] = bf16(0.5 + np.arange(H) / H)
     for layer in range(s["layers"]):
         p = f"model.layers.{layer}"
         t[f"{p}.input_layernorm.weight"] = bf16(np.ones(H))

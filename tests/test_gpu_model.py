@@ -104,3 +104,43 @@ def test_reference_overlay_fixture_product(ctx, tmp_path):
     yd = torch.zeros((1, 1), device="cuda")
     um.int8_linear(ctx, qd, sd, xd, yd)
     assert yd.cpu().numpy().tolist() == [[-5.0]]
+
+
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY, orc.QUANT_DYNAMIC])
+def test_model_logits_match_oracle(ctx, model_files, quant):
+    """Decoder::logits (src/decoder/mod.rs:367-379) of the last hidden row:
+    RMSNorm with model.norm.weight, then lm_head.weight in BF16 or the
+    overlay's INT8 (weight-only, or W8A8 under DynamicActivations)."""
+    d, _, mats = model_files
+    s = mf.MOE_TINY
+    say(f"model logits quant={quant}")
+    overlay = None if quant == orc.QUANT_NONE else d / "overlay.safetensors"
+    mode = um.QUANT_WEIGHTS_ONLY if quant != orc.QUANT_DYNAMIC else um.QUANT_DYNAMIC
+    model = um.Model(ctx, d, overlay, mode)
+    ck = um.Checkpoint(d / "model-00001-of-000001.safetensors")
+    dt, shape, raw = ck.tensor("model.norm.weight")
+    assert dt == "BF16" and shape == [s["hidden"]]
+    norm = orc.bf16_to_f32(np.frombuffer(raw, np.uint16))
+    hidden = np.random.default_rng(7 + quant).standard_normal((3, s["hidden"]), dtype=np.float32)
+    n = orc.rms_norm(hidden[-1:], norm, 1e-6)
+    if quant == orc.QUANT_NONE:
+        dt, shape, raw = ck.tensor("lm_head.weight")
+        w = np.frombuffer(raw, np.uint16).reshape(shape)
+        ref = orc.linear_weight_bf16(n, w)
+    elif quant == orc.QUANT_WEIGHTS_ONLY:
+        q, sc = mats["lm_head.weight"]
+        ref = orc.int8_linear(q, sc, n)
+    else:
+        q, sc = mats["lm_head.weight"]
+        ref = orc.int8_linear_dynamic(q, sc, n)
+    hd = torch.from_numpy(hidden).cuda()
+    out = torch.full((s["vocab"],), float("nan"), device="cuda")
+    model.logits(ctx, hd, out)
+    got = out.cpu().numpy().reshape(1, -1)
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    say(f"  normwise={err:.3e}")
+    assert err <= 1e-5, err
+    with pytest.raises(um.UocrError) as e:
+        model.logits(ctx, hd[:0], out)  # no hidden state
+    assert e.value.status == um.SHAPE
+    model.close()

@@ -449,3 +449,54 @@ def test_block_stack(ctx, T, quant):
         err = normwise(y[keep], ref[keep])
         say(f"  normwise={err:.3e} (near-ties {int(near.sum())})")
         assert err <= tol, err
+
+
+# ------------------------------------------------------ vocabulary projection
+
+@pytest.mark.parametrize("V,H", [(1000, 1280), (4099, 1280), (517, 2048), (300, 192),
+                                 (257, 96)])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "w8a8"])
+def test_lm_head(ctx, V, H, kind):
+    """Decoder::logits: RMSNorm of the last hidden row, then the projection
+    (src/decoder/mod.rs:99-112, 367-379). Widths that are multiples of 64 up
+    to 2048 take the one-launch kernel; 96 takes the operator fallback. FP32
+    accumulation order differs from the oracle's: 1e-5 normwise; W8A8 also
+    quantises the normalised row, where a 1-ulp difference in the norm can
+    move one int8 by one step: 3e-3."""
+    rng = np.random.default_rng(V + H)
+    say(f"lm_head V={V} H={H} {kind}")
+    hidden = rng.standard_normal((3, H), dtype=np.float32)
+    norm = orc.bf16_to_f32(orc.f32_to_bf16(0.5 + rng.random(H, dtype=np.float32)))
+    n = orc.rms_norm(hidden[-1:], norm, 1e-6)
+    if kind == "bf16":
+        w = orc.f32_to_bf16(rng.standard_normal((V, H), dtype=np.float32) * 0.05)
+        ref = orc.linear_weight_bf16(n, w)
+        head = um.LmHead(ctx, dev(norm), 1e-6, weight=dev(w.view(np.int16)), where=um.MEMORY_DEVICE)
+        tol = 1e-5
+    else:
+        q = rng.integers(-127, 128, (V, H), dtype=np.int8)
+        sc = (rng.random((V, H // 32), dtype=np.float32) * 0.002 + 0.001).astype(np.float32)
+        mode = um.QUANT_WEIGHTS_ONLY if kind == "int8" else um.QUANT_DYNAMIC
+        ref = orc.int8_linear(q, sc, n) if kind == "int8" else orc.int8_linear_dynamic(q, sc, n)
+        head = um.LmHead(ctx, dev(norm), 1e-6, q=dev(q), scales=dev(sc), mode=mode,
+                         where=um.MEMORY_DEVICE)
+        tol = 1e-5 if kind == "int8" else 3e-3
+    assert head.precision == {"bf16": "bf16_weights_fp32", "int8": "int8_weights_fp32",
+                              "w8a8": "int8_weights_dynamic_activations"}[kind]
+    out = torch.full((V,), float("nan"), device="cuda")
+    head.logits(ctx, dev(hidden), out)
+    got = out.cpu().numpy().reshape(1, V)
+    assert np.all(np.isfinite(got))
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    say(f"  normwise={err:.3e}")
+    assert err <= tol, err
+    if V == 1000 and kind == "bf16":
+        bad = hidden.copy()
+        bad[-1, 3] = np.inf
+        with pytest.raises(um.UocrError) as e:
+            head.logits(ctx, dev(bad), out)
+        assert e.value.status == um.NUMERICAL
+        with pytest.raises(um.UocrError) as e:
+            head.logits(ctx, dev(hidden)[:0], out)
+        assert e.value.status == um.SHAPE
+    head.close()

@@ -132,6 +132,13 @@ void collect_timings(uocr_gpu_ctx* ctx) {
 
 }  // namespace
 
+struct uocr_lm_head {
+  int device = 0;
+  uocr::LmHeadView view{};
+  std::vector<void*> allocations;
+  size_t bytes = 0;
+};
+
 struct uocr_moe_layer {
   uocr_moe_config cfg{};
   DeviceLayer dev{};
@@ -863,6 +870,128 @@ int uocr_rms_norm(uocr_gpu_ctx* ctx, const float* x, size_t rows, size_t width,
   uocr::launch_rms_norm(x, (int)rows, (int)width, nn, ctx->err, ctx->stream);
   HIP_TRY(hipGetLastError(), "kernel launch");
   return read_and_clear_error(ctx);
+}
+
+
+// ------------------------------------------------- vocabulary projection
+
+int uocr_lm_head_create(uocr_gpu_ctx* ctx, const uocr_lm_head_weights* w, uocr_memory where,
+                        uocr_lm_head** out) {
+  if (!ctx || !w || !out) return fail(UOCR_ERR_SHAPE, "null handle");
+  *out = nullptr;
+  const size_t V = w->vocab_size, H = w->hidden_size;
+  if (V == 0 || H == 0) return fail(UOCR_ERR_SHAPE, "lm_head must be [vocab, hidden]");
+  if (V > (size_t)INT32_MAX / 2 || H > 65536) return fail(UOCR_ERR_UNSUPPORTED, "lm_head too large");
+  if (!w->norm_weight) return fail(UOCR_ERR_FORMAT, "missing model.norm.weight");
+  if (!std::isfinite(w->rms_norm_eps) || w->rms_norm_eps <= 0.f)
+    return fail(UOCR_ERR_SHAPE, "invalid normalization parameters");
+  const bool quant = w->q != nullptr;
+  if (quant) {
+    if (w->quant_mode != UOCR_QUANT_WEIGHTS_ONLY && w->quant_mode != UOCR_QUANT_DYNAMIC_ACTIVATIONS)
+      return fail(UOCR_ERR_SHAPE, "an INT8 lm_head needs a quantization mode");
+    if (!w->scales) return fail(UOCR_ERR_FORMAT, "missing lm_head.weight.q8_scales");
+    if (H % 32) return fail(UOCR_ERR_SHAPE, "INT8 lm_head width must be a multiple of 32");
+  } else {
+    if (w->quant_mode != UOCR_QUANT_NONE)
+      return fail(UOCR_ERR_FORMAT, "quantized lm_head without INT8 weights");
+    if (!w->weight) return fail(UOCR_ERR_FORMAT, "missing lm_head.weight");
+  }
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  auto* head = new uocr_lm_head();
+  head->device = ctx->device;
+  head->view.V = (int)V;
+  head->view.H = (int)H;
+  head->view.eps = w->rms_norm_eps;
+  head->view.kind = !quant ? 0 : (w->quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS ? 2 : 1);
+  auto finish = [&](int status) {
+    if (status) uocr_lm_head_destroy(head);
+    return status;
+  };
+  auto alloc_copy = [&](const void* src, size_t bytes, void** dst) -> int {
+    hipError_t e = hipMalloc(dst, bytes);
+    if (e != hipSuccess) return hip_fail(e, "lm_head allocation");
+    head->allocations.push_back(*dst);
+    head->bytes += bytes;
+    if ((e = hipMemcpyAsync(*dst, src, bytes, kind_of(where), ctx->stream)) != hipSuccess)
+      return hip_fail(e, "lm_head upload");
+    return UOCR_OK;
+  };
+  void* p = nullptr;
+  int r = alloc_copy(w->norm_weight, H * 4, &p);
+  if (r) return finish(r);
+  head->view.norm_w = static_cast<const float*>(p);
+  if (quant) {
+    if ((r = alloc_copy(w->q, V * H, &p))) return finish(r);
+    head->view.q = static_cast<const int8_t*>(p);
+    if ((r = alloc_copy(w->scales, V * (H / 32) * 4, &p))) return finish(r);
+    head->view.s = static_cast<const float*>(p);
+  } else {
+    if ((r = alloc_copy(w->weight, V * H * 2, &p))) return finish(r);
+    head->view.w = static_cast<const uint16_t*>(p);
+  }
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "lm_head upload");
+  *out = head;
+  return UOCR_OK;
+}
+
+int uocr_lm_head_logits_async(uocr_gpu_ctx* ctx, const uocr_lm_head* head, const float* hidden,
+                              size_t T, float* logits) {
+  if (!ctx || !head) return fail(UOCR_ERR_SHAPE, "null handle");
+  if (T == 0 || !hidden) return fail(UOCR_ERR_SHAPE, "missing final hidden state");
+  if (!logits) return fail(UOCR_ERR_SHAPE, "null logits");
+  if (head->device != ctx->device) return fail(UOCR_ERR_SHAPE, "lm_head lives on another device");
+  HIP_TRY(hipSetDevice(ctx->device), "set device");
+  const uocr::LmHeadView& v = head->view;
+  const float* last = hidden + (T - 1) * (size_t)v.H;
+  if (uocr::lm_head_fast(v.H)) {
+    uocr::launch_lm_head(last, v, logits, ctx->err, ctx->stream);
+  } else {
+    // Other widths: the norm into scratch, then the single-matrix operators.
+    const size_t blocks = (size_t)v.H / 32;
+    if (align256((size_t)v.H * 4) + align256(v.H) + blocks * 4 > ctx->scratch_limit)
+      return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");
+    float* xn = reinterpret_cast<float*>(ctx->scratch);
+    uocr::RowNorm nn;
+    nn.w = v.norm_w;
+    nn.eps = v.eps;
+    nn.out = xn;
+    uocr::launch_rms_norm(last, 1, v.H, nn, ctx->err, ctx->stream);
+    if (v.kind == 0) {
+      uocr::launch_linear_bf16(xn, 1, v.H, v.w, v.V, logits, ctx->stream);
+    } else if (v.kind == 1) {
+      uocr::launch_int8_linear(v.q, v.s, v.V, v.H, xn, 1, logits, ctx->stream);
+    } else {
+      int8_t* xq = reinterpret_cast<int8_t*>(ctx->scratch + align256((size_t)v.H * 4));
+      float* xs = reinterpret_cast<float*>(ctx->scratch + align256((size_t)v.H * 4) + align256(v.H));
+      uocr::launch_int8_dynamic(v.q, v.s, v.V, v.H, xn, logits, nullptr, xq, xs, ctx->err,
+                                ctx->stream);
+    }
+  }
+  HIP_TRY(hipGetLastError(), "kernel launch");
+  return UOCR_OK;
+}
+
+int uocr_lm_head_logits(uocr_gpu_ctx* ctx, const uocr_lm_head* head, const float* hidden,
+                        size_t T, float* logits) {
+  int r = uocr_lm_head_logits_async(ctx, head, hidden, T, logits);
+  if (r) return r;
+  return read_and_clear_error(ctx);
+}
+
+const char* uocr_lm_head_precision(const uocr_lm_head* head) {
+  if (!head) return "";
+  return head->view.kind == 0   ? "bf16_weights_fp32"
+         : head->view.kind == 1 ? "int8_weights_fp32"
+                                : "int8_weights_dynamic_activations";
+}
+
+size_t uocr_lm_head_device_bytes(const uocr_lm_head* head) { return head ? head->bytes : 0; }
+
+void uocr_lm_head_destroy(uocr_lm_head* head) {
+  if (!head) return;
+  if (hipSetDevice(head->device) == hipSuccess)
+    for (void* p : head->allocations) (void)hipFree(p);
+  delete head;
 }
 
 }  // extern "C"

@@ -160,6 +160,12 @@ int uocr_model_experts(uocr_gpu_ctx* ctx, const uocr_model* m, size_t layer, con
   return guarded([&] { m->model->experts(ctx, layer, x, T, y, flags); });
 }
 
+int uocr_model_logits(uocr_gpu_ctx* ctx, const uocr_model* m, const float* hidden, size_t T,
+                      float* logits) {
+  if (!ctx || !m) return uocr::host::set_last_error(UOCR_ERR_SHAPE, "null argument");
+  return guarded([&] { m->model->logits(ctx, hidden, T, logits); });
+}
+
 void uocr_model_destroy(uocr_model* m) { delete m; }
 
 }  // extern "C"

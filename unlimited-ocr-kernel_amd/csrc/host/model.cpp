@@ -91,6 +91,45 @@ const uint16_t* bf16_of(const Checkpoint& ck, const std::string& name) {
   return reinterpret_cast<const uint16_t*>(w.bytes);
 }
 
+// A vector tensor widened to f32 (Tensor::to_f32, src/checkpoint.rs:79-101):
+// BF16 and F16 widen exactly, F32 is copied.
+std::vector<float> f32_of(const Checkpoint& ck, const std::string& name) {
+  const WeightView w = ck.tensor(name);
+  size_t n = 1;
+  for (size_t d : *w.shape) n *= d;
+  std::vector<float> out(n);
+  for (size_t i = 0; i < n; i++) {
+    uint32_t bits;
+    if (w.dtype == DType::F32) {
+      std::memcpy(&bits, w.bytes + 4 * i, 4);
+    } else if (w.dtype == DType::BF16) {
+      uint16_t h;
+      std::memcpy(&h, w.bytes + 2 * i, 2);
+      bits = (uint32_t)h << 16;
+    } else if (w.dtype == DType::F16) {
+      uint16_t h;
+      std::memcpy(&h, w.bytes + 2 * i, 2);
+      const uint32_t sign = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 0x1f, man = h & 0x3ff;
+      if (ex == 0x1f) {
+        bits = sign | 0x7f800000u | (man << 13);  // inf / nan
+      } else if (ex != 0) {
+        bits = sign | ((ex + 112) << 23) | (man << 13);
+      } else if (man == 0) {
+        bits = sign;  // signed zero
+      } else {
+        // Subnormal half: man * 2^-24, exact in f32.
+        float f = (float)man * 5.9604644775390625e-8f;
+        std::memcpy(&bits, &f, 4);
+        bits |= sign;
+      }
+    } else {
+      throw OcrError(ErrorKind::Unsupported, name + ": expected a floating-point tensor");
+    }
+    std::memcpy(&out[i], &bits, 4);
+  }
+  return out;
+}
+
 // Copies the per-expert tensors of one kind into one [E, rows, cols] buffer.
 template <typename T, typename Get>
 std::vector<T> gather(size_t experts, size_t elems, Get get) {
@@ -194,12 +233,42 @@ std::unique_ptr<Model> Model::load_with_quantization(const std::string& director
         gpu, handle, &iw, UOCR_MEMORY_HOST,
         mode == QuantizationMode::WeightsOnly ? UOCR_QUANT_WEIGHTS_ONLY : UOCR_QUANT_DYNAMIC_ACTIVATIONS));
   }
+  // Decoder::logits: model.norm.weight, and lm_head.weight in BF16 or, when
+  // the overlay holds it, INT8 (src/decoder/mod.rs:99-112, 367-379).
+  const std::vector<float> final_norm = f32_of(*ck, "model.norm.weight");
+  uocr_lm_head_weights lw{};
+  lw.vocab_size = (uint32_t)c.vocab_size;
+  lw.hidden_size = (uint32_t)H;
+  lw.rms_norm_eps = c.rms_norm_eps;
+  lw.norm_weight = final_norm.data();
+  const Int8Matrix* head_q = q ? q->get("lm_head.weight") : nullptr;
+  if (head_q) {
+    lw.q = head_q->weights().data();
+    lw.scales = head_q->scales().data();
+    lw.quant_mode = mode == QuantizationMode::WeightsOnly ? UOCR_QUANT_WEIGHTS_ONLY
+                                                          : UOCR_QUANT_DYNAMIC_ACTIVATIONS;
+  } else {
+    lw.weight = bf16_of(*ck, "lm_head.weight");
+    lw.quant_mode = UOCR_QUANT_NONE;
+  }
+  check(uocr_lm_head_create(gpu, &lw, UOCR_MEMORY_HOST, &m->lm_head_));
   return m;
 }
 
 Model::~Model() {
   for (uocr_moe_layer* l : layers_)
     if (l) uocr_moe_layer_destroy(l);
+  if (lm_head_) uocr_lm_head_destroy(lm_head_);
+}
+
+void Model::logits(CpuContext& cpu, const float* hidden, size_t T, float* logits) const {
+  if (cpu.backend() != Backend::Gpu || !cpu.gpu())
+    throw OcrError(ErrorKind::Unsupported, "the vocabulary projection runs on Backend::Gpu");
+  this->logits(cpu.gpu(), hidden, T, logits);
+}
+
+void Model::logits(uocr_gpu_ctx* gpu, const float* hidden, size_t T, float* logits) const {
+  check(uocr_lm_head_logits(gpu, lm_head_, hidden, T, logits));
 }
 
 const char* Model::precision() const {

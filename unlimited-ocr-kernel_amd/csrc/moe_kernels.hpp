@@ -147,4 +147,20 @@ bool row_norm_fusable(int width);
 void launch_rms_norm(const float* x, int rows, int width, const RowNorm& nn, int* err,
                      hipStream_t s);
 
+// lmhead.hip: the vocabulary projection of one hidden row.
+struct LmHeadView {
+  int V = 0, H = 0;
+  int kind = 0;                 // 0 BF16, 1 INT8 weight-only, 2 W8A8
+  float eps = 0.0f;
+  const float* norm_w = nullptr;  // [H] f32
+  const uint16_t* w = nullptr;    // [V, H] bf16
+  const int8_t* q = nullptr;      // [V, H]
+  const float* s = nullptr;       // [V, H/32]
+};
+// The one-launch path: widths that are multiples of 64, up to 2048.
+bool lm_head_fast(int H);
+// logits[V] of `hidden` (one row of H): RMSNorm, then the projection.
+void launch_lm_head(const float* hidden, const LmHeadView& head, float* logits, int* err,
+                    hipStream_t s);
+
 }  // namespace uocr

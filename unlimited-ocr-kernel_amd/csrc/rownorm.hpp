@@ -1,0 +1,77 @@
+// RMSNorm of one row held by a workgroup of 256 threads (thread i holds
+// float4 chunks i and i + 256: widths up to 2048), shared by the combine,
+// the standalone norm and the vocabulary projection so that all give the
+// same bits.
+#pragma once
+
+#include "common.hpp"
+
+namespace uocr {
+
+// One row (token) per workgroup of 256 threads; thread i holds float4
+// chunks i and i + 256 of the row (widths up to 2048).
+constexpr int kRowThreads = 256, kRowChunks = 2;
+
+// RMSNorm of a row held as float4 chunks (src/cpu/ops.rs:362-423, center =
+// false): variance = sum(v^2) / W, scale = 1 / sqrt(variance + eps),
+// out = v * scale * w. Non-finite row or weight -> Numerical (:382-389).
+// The sum runs per thread over its chunks (x, y, z, w in turn), then over
+// the wave and the four waves in order, so the standalone and the fused
+// norms give the same bits. Writes the normalised row and, when hi is set,
+// its bf16 planes (hi = bf16(v), lo = bf16(v - hi) when lo is set).
+__device__ inline void norm_row(const float4 (&v)[kRowChunks], int width, const float* __restrict__ w,
+                                float eps, float* __restrict__ out, uint16_t* __restrict__ hi,
+                                uint16_t* __restrict__ lo, int* err) {
+  __shared__ float partial[kRowThreads / 64];
+  __shared__ int bad_any;
+  const int tid = threadIdx.x;
+  if (tid == 0) bad_any = 0;
+  __syncthreads();
+  float ss = 0.0f;
+  bool bad = false;
+  float4 wv[kRowChunks];
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (tid + kRowThreads * it) * 4;
+    if (i >= width) break;
+    wv[it] = *reinterpret_cast<const float4*>(w + i);
+    const float4 x = v[it];
+    bad |= !isfinite(x.x) || !isfinite(x.y) || !isfinite(x.z) || !isfinite(x.w);
+    bad |= !isfinite(wv[it].x) || !isfinite(wv[it].y) || !isfinite(wv[it].z) || !isfinite(wv[it].w);
+    ss = fmaf(x.x, x.x, ss);
+    ss = fmaf(x.y, x.y, ss);
+    ss = fmaf(x.z, x.z, ss);
+    ss = fmaf(x.w, x.w, ss);
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) partial[tid >> 6] = ss;
+  if (bad) bad_any = 1;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  if (bad_any && tid == 0) raise_error(err, kErrNumerical);
+  const float scale = 1.0f / sqrtf(total / (float)width + eps);
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (tid + kRowThreads * it) * 4;
+    if (i >= width) break;
+    const float4 x = v[it];
+    const float o[4] = {x.x * scale * wv[it].x, x.y * scale * wv[it].y, x.z * scale * wv[it].z,
+                        x.w * scale * wv[it].w};
+    *reinterpret_cast<float4*>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+    if (hi) {
+      uint16_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        h[j] = __builtin_bit_cast(uint16_t, (__bf16)o[j]);
+        l[j] = __builtin_bit_cast(uint16_t, (__bf16)(o[j] - __uint_as_float((uint32_t)h[j] << 16)));
+      }
+      *reinterpret_cast<uint2*>(hi + i) =
+          make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+      if (lo)
+        *reinterpret_cast<uint2*>(lo + i) =
+            make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    }
+  }
+}
+
+}  // namespace uocr

@@ -45,6 +45,9 @@ EXPORTS = [
     "uocr_checkpoint_count", "uocr_checkpoint_name", "uocr_checkpoint_metadata",
     "uocr_checkpoint_tensor", "uocr_overlay_validate", "uocr_config_load", "uocr_model_load",
     "uocr_model_precision", "uocr_model_layer", "uocr_model_experts", "uocr_model_destroy",
+    "uocr_lm_head_create", "uocr_lm_head_logits", "uocr_lm_head_logits_async",
+    "uocr_lm_head_precision", "uocr_lm_head_device_bytes", "uocr_lm_head_destroy",
+    "uocr_model_logits",
 ]
 DTYPES = ["BF16", "F16", "F32", "I64", "I8"]
 
@@ -80,6 +83,12 @@ class Int8Weights(ctypes.Structure):
         "expert_gate", "expert_gate_scales", "expert_up", "expert_up_scales", "expert_down",
         "expert_down_scales", "shared_gate", "shared_gate_scales", "shared_up",
         "shared_up_scales", "shared_down", "shared_down_scales")]
+
+
+class LmHeadWeights(ctypes.Structure):
+    _fields_ = [("vocab_size", _U32), ("hidden_size", _U32), ("rms_norm_eps", ctypes.c_float),
+                ("norm_weight", _P), ("weight", _P), ("q", _P), ("scales", _P),
+                ("quant_mode", ctypes.c_int)]
 
 
 class PhaseTime(ctypes.Structure):
@@ -152,6 +161,14 @@ def _load():
         "uocr_model_layer": (_P, [_P, _SZ]),
         "uocr_model_experts": (ctypes.c_int, [_P, _P, _SZ, _P, _SZ, _P, _U32]),
         "uocr_model_destroy": (None, [_P]),
+        "uocr_lm_head_create": (ctypes.c_int, [_P, ctypes.POINTER(LmHeadWeights), ctypes.c_int,
+                                               ctypes.POINTER(_P)]),
+        "uocr_lm_head_logits": (ctypes.c_int, [_P, _P, _P, _SZ, _P]),
+        "uocr_lm_head_logits_async": (ctypes.c_int, [_P, _P, _P, _SZ, _P]),
+        "uocr_lm_head_precision": (ctypes.c_char_p, [_P]),
+        "uocr_lm_head_device_bytes": (_SZ, [_P]),
+        "uocr_lm_head_destroy": (None, [_P]),
+        "uocr_model_logits": (ctypes.c_int, [_P, _P, _P, _SZ, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -295,6 +312,49 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
               ctypes.byref(tr) if tr is not None else None))
 
 
+class LmHead:
+    """Decoder::logits: the last hidden row, RMSNorm with the final norm
+    weight (f32 [H]), then the vocabulary projection — BF16 weight bits
+    [V, H], or an INT8 overlay (q [V, H], scales [V, H/32]) weight-only or,
+    with QUANT_DYNAMIC_ACTIVATIONS, W8A8."""
+
+    def __init__(self, ctx: Context, norm_weight, eps: float, weight=None, q=None, scales=None,
+                 mode: int = 0, where: int = 0):
+        self.handle = None
+        src = weight if q is None else q
+        V, H = src.shape
+        keep = [norm_weight, weight, q, scales]
+        w = LmHeadWeights(V, H, eps, _ptr(norm_weight), _ptr(weight), _ptr(q), _ptr(scales), mode)
+        h = _P()
+        _check(lib.uocr_lm_head_create(ctx.handle, ctypes.byref(w), where, ctypes.byref(h)))
+        del keep
+        self.handle = h
+        self.vocab = V
+
+    def logits(self, ctx: Context, hidden, out, sync: bool = True):
+        fn = lib.uocr_lm_head_logits if sync else lib.uocr_lm_head_logits_async
+        _check(fn(ctx.handle, self.handle, _ptr(hidden), hidden.shape[0], _ptr(out)))
+
+    @property
+    def precision(self) -> str:
+        return lib.uocr_lm_head_precision(self.handle).decode()
+
+    @property
+    def device_bytes(self) -> int:
+        return lib.uocr_lm_head_device_bytes(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib.uocr_lm_head_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def block_forward(ctx: Context, layers, x, y, flags: int = 0, sync: bool = True):
     arr = (_P * len(layers))(*[l.handle.value for l in layers])
     fn = lib.uocr_moe_block_forward if sync else lib.uocr_moe_block_forward_async
@@ -417,3 +477,8 @@ class Model:
     def experts(self, ctx, layer: int, x, y, flags: int = 0):
         _check(lib.uocr_model_experts(ctx.handle, self.handle, layer, _ptr(x), x.shape[0], _ptr(y),
                                       flags))
+
+    def logits(self, ctx, hidden, out):
+        """Decoder::logits: out[vocab] from the last row of hidden[T, H]."""
+        _check(lib.uocr_model_logits(ctx.handle, self.handle, _ptr(hidden), hidden.shape[0],
+                                     _ptr(out)))
