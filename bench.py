@@ -68,6 +68,22 @@ def expert_bytes_int8(rows, cols):
     return rows * cols + rows * (cols // 32) * 4
 
 
+def gate_traffic():
+    """HBM bytes per gate/up launch (BF16 activations) from the committed
+    rocprofv3 counter summary of the same workload: scaled MB read + written
+    of the gate/up kernel row. None when the summary is not there."""
+    path = os.path.join(REPO, "profiles", "prefill_stack_T4096_counters.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if "mfma_group_kernel<8, 32, 4, false, true>" in line:
+                    cells = [c.strip().replace(",", "") for c in line.split("|")]
+                    return int((float(cells[3]) + float(cells[5])) * 1e6)
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def decode_bytes(int8: bool, unique_experts: float, T: int = 1) -> float:
     """Algorithmic HBM bytes of one small-batch layer call: unique active
     experts, shared expert, router, x and y."""
@@ -368,7 +384,9 @@ def main():
         "roofline": None if value is None else {
             "bound": "mfma", "achieved": round(achieved, 2),
             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": gate_traffic(),
+            "traffic_source": "profiles/prefill_stack_T4096_counters.md (FETCH_SIZE + "
+                              "WRITE_SIZE per dispatch, copy-calibrated)",
             "kernel": "mfma_group_kernel gate/up (SiLU-gated), one launch per layer",
             "kernel_ms": round(gate_avg_ms, 4),
             "layer_frac": round(layer_s_flop / BF16_PEAK_TFLOPS, 4)},
