@@ -10,7 +10,9 @@ MoE-layer tokens/s = 4096 * 12 / step time, inputs resident in HBM.
 Secondary workloads (same JSON line, "secondary"): batch-1 decode with the
 INT8 block-32 overlay and with BF16 weights (rotating over 12 distinct layers
 so the 256 MB MALL cannot hold the working set), and the 1024-token prefill
-with Zipf(1.1) expert popularity in both activation precision classes, and
+with Zipf(1.1) expert popularity in both activation precision classes, the
+INT8-overlay layer at 512 tokens with uniform routing (W8A8 under
+DynamicActivations, and weight-only), and
 the vocabulary projection (final RMSNorm + 129280 x 1280 lm_head) in BF16,
 INT8 weight-only and W8A8.
 
@@ -50,8 +52,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--secondary",
-                    default="decode_int8,decode_bf16,decode_int8_t16,prefill1024,lm_head_bf16,"
-                            "lm_head_int8,lm_head_w8a8",
+                    default="decode_int8,decode_bf16,decode_int8_t16,prefill1024,"
+                            "prefill_w8a8_t512,prefill_int8_t512,lm_head_bf16,lm_head_int8,"
+                            "lm_head_w8a8",
                     help="comma list of secondary workloads, or 'none'")
     ap.add_argument("--cpu-sample", type=int, default=512,
                     help="tokens of the headline workload timed on the CPU oracle (0: skip)")
@@ -287,6 +290,52 @@ def main():
                                    4)})
             log(f"prefill1024 {cls}: {ms:.3f} ms")
         layer.close()
+
+    # ------------------------------------- INT8 prefill (weight-only, W8A8)
+    def prefill_int8(quant: int):
+        """The INT8-overlay layer at T=512 with uniform-random routing
+        (random router rows, no popularity bias): multi-row groups run the
+        weight-only dequant (FP32 math), single-row groups W8A8 under
+        DynamicActivations (src/decoder/mod.rs:103-104)."""
+        kind = "w8a8" if quant == um.QUANT_DYNAMIC else "int8"
+        T = 512
+        log(f"prefill {kind} T={T}, uniform routing")
+        w = syn.moe_weights_device(H, I, E, SH, seed=3)
+        torch.cuda.synchronize()
+        layer = um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE)
+        del w
+        q = syn.int8_overlay_device(H, I, E, SH, seed=103)
+        torch.cuda.synchronize()
+        layer.attach_int8(ctx, q, um.MEMORY_DEVICE, quant)
+        del q
+        torch.cuda.empty_cache()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0)
+        xp = torch.randn((T, H), generator=gen, device="cuda")
+        yp = torch.empty_like(xp)
+        for _ in range(args.warmup):
+            um.forward(ctx, layer, xp, yp, sync=False)
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            um.forward(ctx, layer, xp, yp, sync=False)
+        sync()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        layer.close()
+        torch.cuda.empty_cache()
+        # Every expert is touched at T=512: all INT8 weights and scales are read.
+        nbytes = (E * 3 * I * H + 3 * S * H) * (1 + 4 / 32) + ROUTER_BYTES + 2 * T * H * 4
+        log(f"prefill {kind} T={T}: {ms:.3f} ms")
+        return {"workload": f"prefill-{kind}-T{T}-uniform", "tokens": T,
+                "value": round(T / (ms / 1e3), 1), "unit": "tokens/s (one layer)",
+                "ms_per_step": round(ms, 4),
+                "hbm_frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                "mfma_frac": round(FLOP_PER_TOKEN * T / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+    for key, quant in (("prefill_w8a8_t512", um.QUANT_DYNAMIC),
+                       ("prefill_int8_t512", um.QUANT_WEIGHTS_ONLY)):
+        if key in wanted:
+            secondary.append(prefill_int8(quant))
 
     # ------------------------------------------------ vocabulary projection
     def lm_head(kind: str):

@@ -355,12 +355,26 @@ def test_full_bf16_mfma(ctx, full_bf16, T):
                 flags=um.FLAG_FORCE_MFMA | um.FLAG_BF16_ACTIVATIONS)
 
 
-def test_int8_forced_mfma_is_unsupported(ctx, full_int8):
-    say("INT8 weights with the MFMA engine forced -> Unsupported")
-    x = dev(syn.activations(32, 1280, seed=1))
-    with pytest.raises(um.UocrError) as e:
-        um.forward(ctx, full_int8.layer, x, torch.empty_like(x), flags=um.FLAG_FORCE_MFMA)
-    assert e.value.status == um.UNSUPPORTED
+@pytest.mark.parametrize("T", [17, 64, 512])
+def test_int8_mfma(ctx, full_int8, full_dynamic, T):
+    """INT8 overlays on the MFMA engine: the dequantised weight (q * s, f32)
+    as exact bf16 hi + lo planes and three product terms (FP32 class), or
+    two with BF16 activations. Under DynamicActivations the groups of one
+    row take the W8A8 path (src/decoder/mod.rs:103-104); T = 17 and 64 leave
+    several such groups among 64 experts."""
+    x = syn.activations(T, 1280, seed=700 + T)
+    for case, name in ((full_int8, "weight-only"), (full_dynamic, "dynamic")):
+        say(f"INT8 MFMA {name} T={T}")
+        check_layer(case, ctx, x)
+        if T == 64:
+            say(f"INT8 MFMA {name} T={T} bf16 activations")
+            check_layer(case, ctx, x, tol=BF16_TOL, flags=um.FLAG_BF16_ACTIVATIONS)
+            say(f"INT8 small-batch engine forced {name} T={T}")
+            check_layer(case, ctx, x, flags=um.FLAG_FORCE_GEMV)
+    if T == 64:
+        _, tr = full_dynamic.run(ctx, x)
+        counts = np.diff(tr["expert_offsets"])
+        assert (counts == 1).any(), counts  # the W8A8 single-row path ran
 
 
 @pytest.fixture(scope="module")

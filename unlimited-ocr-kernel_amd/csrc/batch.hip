@@ -30,14 +30,17 @@ struct TileInfo {
   bool routed;
 };
 
+// singles: only routed groups of a single row (the W8A8 rows the MFMA engine
+// leaves to this engine under DynamicActivations).
 __device__ __forceinline__ bool load_tile(const DeviceLayer& L, const Scratch& S, int T,
-                                          int mchunk, TileInfo& ti) {
+                                          int mchunk, int singles, TileInfo& ti) {
   const int tile = blockIdx.y;
   if (tile >= S.counters[0]) return false;
   ti.g = S.tiles[2 * tile];
   ti.r0 = S.tiles[2 * tile + 1];
   ti.routed = ti.g < L.E;
   ti.group_rows = ti.routed ? S.offsets[ti.g + 1] - S.offsets[ti.g] : T;
+  if (singles && !(ti.routed && ti.group_rows == 1)) return false;
   ti.n = min(mchunk, ti.group_rows - ti.r0);
   return ti.n > 0;
 }
@@ -144,10 +147,10 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
 // (Decoder::feed_forward, src/decoder/mod.rs:114-122).
 template <int KIND, int KH>
 __global__ __launch_bounds__(256) void batch_gateup_kernel(DeviceLayer L, Scratch S, int T,
-                                                           int mchunk) {
+                                                           int mchunk, int singles) {
   __shared__ __align__(16) BatchSmem sm;
   TileInfo ti;
-  if (!load_tile(L, S, T, mchunk, ti)) return;
+  if (!load_tile(L, S, T, mchunk, singles, ti)) return;
   const int W = L.width(ti.g);
   const int k0 = 16 * blockIdx.x;
   if (k0 >= W) return;
@@ -192,10 +195,10 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
 
 template <int KIND>
 __global__ __launch_bounds__(256) void batch_down_kernel(DeviceLayer L, Scratch S, int T,
-                                                         int mchunk) {
+                                                         int mchunk, int singles) {
   __shared__ __align__(16) BatchSmem sm;
   TileInfo ti;
-  if (!load_tile(L, S, T, mchunk, ti)) return;
+  if (!load_tile(L, S, T, mchunk, singles, ti)) return;
   if (ti.routed && L.I <= kNarrowK)
     down_body<KIND, kNarrowK>(L, S, sm, ti);
   else
@@ -311,12 +314,12 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(
 
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        int mchunk, hipStream_t s) {
-  const dim3 grid((L.S + 15) / 16, tiles_bound);
+                        int mchunk, int singles, hipStream_t s) {
+  const dim3 grid(((singles ? L.I : L.S) + 15) / 16, tiles_bound);
   if (L.H <= 1280)
-    batch_gateup_kernel<KIND, 1280><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk);
+    batch_gateup_kernel<KIND, 1280><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
   else
-    batch_gateup_kernel<KIND, kWideK><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk);
+    batch_gateup_kernel<KIND, kWideK><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
 }
 
 }  // namespace
@@ -326,20 +329,20 @@ bool batch_supported(const DeviceLayer& L) {
 }
 
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s) {
+                         int mchunk, hipStream_t s, bool singles) {
   if (L.quant_mode == 0)
-    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, s);
+    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, singles, s);
   else
-    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, s);
+    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, singles, s);
 }
 
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s) {
+                       hipStream_t s, bool singles) {
   const dim3 grid(L.H / 32, tiles_bound);
   if (L.quant_mode == 0)
-    batch_down_kernel<kBF16><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk);
+    batch_down_kernel<kBF16><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
   else
-    batch_down_kernel<kInt8><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk);
+    batch_down_kernel<kInt8><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
 }
 
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,

@@ -93,7 +93,10 @@ constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at maximum).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int WAVES, int BK, int NBUF, bool SPLIT, bool GATEUP>
+// SPLITB: INT8-overlay weights as dequantised bf16 hi + lo planes (a third
+// product term), y always f32; groups of one row are skipped when the
+// overlay runs DynamicActivations (the batch engine's W8A8 path owns them).
+template <int WAVES, int BK, int NBUF, bool SPLIT, bool GATEUP, bool SPLITB = false>
 __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
                                                                    MfmaPlanes P, int T) {
   // Waves form a 2 x (WAVES/2) grid over the 256 x 256 tile; each owns 128
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   constexpr int kWn = WAVES / 2;
   constexpr int kWc = kTileN / kWn;
   constexpr int kNi = kWc / 32;
-  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo]
+  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
   __shared__ int arow[kTileM];
 
   // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
@@ -145,6 +148,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   const int K = GATEUP ? L.H : W;
   const int n0 = ntile * kTileN;
   const int group_rows = routed ? S.offsets[g + 1] - S.offsets[g] : T;
+  if (SPLITB && routed && group_rows == 1 && L.quant_mode == kQuantDynamic)
+    return;
   const int mrows = min(kTileM, group_rows - r0);
   const int base = routed ? S.offsets[g] : 0;
 
@@ -177,7 +182,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   constexpr int kRowDiv = 16 / kCpr;
   auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
   const uint32_t plane_bytes = (uint32_t)kTileM * BK * 2;
-  const uint32_t stage_bytes = (SPLIT ? 3 : 2) * plane_bytes;
+  constexpr int kPlanes = 2 + (SPLIT ? 1 : 0) + (SPLITB ? 1 : 0);
+  const uint32_t stage_bytes = kPlanes * plane_bytes;
+  const uint32_t blo_plane = (SPLIT ? 3 : 2) * plane_bytes;  // B lo, when SPLITB
 
   // Per-lane source offsets of this wave's segments (k = 0).
   const uint32_t row_bytes = (uint32_t)K * 2;
@@ -202,10 +209,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
     a_lo_src = routed ? P.h_lo : P.hs_lo;
     a_rows = routed ? (uint32_t)T * L.K : (uint32_t)T;
   }
-  const uint16_t* wmat = GATEUP ? L.w13 + L.w13_offset(g) : L.w2 + L.w2_offset(g);
+  const uint16_t* wmat;
+  const uint16_t* wmat_lo = nullptr;
+  if constexpr (SPLITB) {
+    wmat = GATEUP ? L.dq13 + L.w13_offset(g) : L.dq2 + L.w2_offset(g);
+    wmat_lo = wmat + (GATEUP ? L.n13() : L.n2());
+  } else {
+    wmat = GATEUP ? L.w13 + L.w13_offset(g) : L.w2 + L.w2_offset(g);
+  }
   const i32x4 rs_a = buffer_rsrc(a_hi_src, a_rows * row_bytes);
   const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
   const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes);
+  const i32x4 rs_bl = buffer_rsrc(SPLITB ? wmat_lo : wmat, (uint32_t)N * row_bytes);
   // LDS byte address of this wave's first segment of stage buffer 0.
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds) +
@@ -218,6 +233,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
       buffer_load_lds16(rs_a, st + i * 1024u, a_off[i] + kb);
       buffer_load_lds16(rs_b, st + plane_bytes + i * 1024u, b_off[i] + kb);
       if constexpr (SPLIT) buffer_load_lds16(rs_l, st + 2 * plane_bytes + i * 1024u, a_off[i] + kb);
+      if constexpr (SPLITB) buffer_load_lds16(rs_bl, st + blo_plane + i * 1024u, b_off[i] + kb);
     }
   };
 
@@ -250,7 +266,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   // groups before either reads stage ks + 1.
   static_assert(WAVES == 8, "the ping-pong schedule pairs two waves per SIMD");
   constexpr int kDepth = NBUF - 1;
-  constexpr int kLps = kSegPerWave * (SPLIT ? 3 : 2);
+  constexpr int kLps = kSegPerWave * kPlanes;
   constexpr int kSub = BK / 16;
   const int grp = wave >> 2;
   for (int i = 0; i < kDepth; i++)
@@ -266,7 +282,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
     const bool steady = ks + kDepth < nk;
     if (steady) issue((ks + kDepth) % NBUF, (ks + kDepth) * BK);
     const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
-    bf16x8 fa[kSub][4], fl[kSub][SPLIT ? 4 : 1], fb[kSub][kNi];
+    bf16x8 fa[kSub][4], fl[kSub][SPLIT ? 4 : 1], fb[kSub][kNi], fbl[kSub][SPLITB ? kNi : 1];
     auto frag = [&](const char* plane, int row, int c) {
       return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
     };
@@ -274,7 +290,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
     for (int sub = 0; sub < kSub; sub++) {
       const int c = 2 * sub + fc;
 #pragma unroll
-      for (int ni = 0; ni < kNi; ni++) fb[sub][ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
+      for (int ni = 0; ni < kNi; ni++) {
+        fb[sub][ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
+        if constexpr (SPLITB) fbl[sub][ni] = frag(cur + blo_plane, wn * kWc + ni * 32 + fr, c);
+      }
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) {
         fa[sub][mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
@@ -299,6 +318,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[sub][mi], fb[sub][ni], acc[mi][ni], 0, 0, 0);
           if constexpr (SPLIT)
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[sub][mi], fb[sub][ni],
+                                                                  acc[mi][ni], 0, 0, 0);
+          if constexpr (SPLITB)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[sub][mi], fbl[sub][ni],
                                                                   acc[mi][ni], 0, 0, 0);
         }
     __builtin_amdgcn_sched_barrier(0);
@@ -335,8 +357,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
         }
     }
   } else {
-    // FP32-class: y in f32. BF16 activations: y rounded to bf16 (the
-    // combine's operands), in the first half of the same buffer.
+    // FP32-class and INT8 weights: y in f32. BF16 weights with BF16
+    // activations: y rounded to bf16 (the combine's operands), in the first
+    // half of the same buffer.
     float* out = routed ? S.y : S.ys;
     uint16_t* out16 = reinterpret_cast<uint16_t*>(out);
 #pragma unroll
@@ -350,7 +373,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
           const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           if (row >= mrows) continue;
           const size_t at = (size_t)(base + r0 + row) * L.H + col;
-          if constexpr (SPLIT)
+          if constexpr (SPLIT || SPLITB)
             out[at] = acc[mi][ni][r];
           else
             out16[at] = bf16_bits(acc[mi][ni][r]);
@@ -359,14 +382,49 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   }
 }
 
-template <int BK, int NBUF, bool SPLIT>
+template <int BK, int NBUF, int PLANES>
 constexpr size_t mfma_lds_bytes() {
-  return (size_t)NBUF * (SPLIT ? 3 : 2) * kTileM * BK * sizeof(uint16_t);
+  return (size_t)NBUF * PLANES * kTileM * BK * sizeof(uint16_t);
 }
 // BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class
-// (hi + lo planes): 32-deep stages, three buffers (144 KiB).
+// (hi + lo planes): 32-deep stages, three buffers (144 KiB). INT8 overlay
+// (dequantised weight hi + lo planes, and the activation's lo plane in the
+// FP32 class): 16-deep stages, four buffers (96 / 128 KiB).
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBkSplit = 32, kBufSplit = 3;
+constexpr int kBkQ = 16, kBufQ = 4;
 constexpr int kWaves = 8;
+
+// INT8 overlay -> bf16 planes of the dequantised weight: w = q * s rounded to
+// f32 as Int8Matrix::linear does (src/cpu/quantized.rs:119-131), then hi =
+// bf16(w) and lo = bf16(w - hi) (|w - hi - lo| <= 2^-16 |w|). Row-major
+// [rows, cols] with scales [rows, cols / 32].
+__global__ void dequant_planes_kernel(const int8_t* __restrict__ q, const float* __restrict__ sc,
+                                      size_t n, int cols, uint16_t* __restrict__ hi,
+                                      uint16_t* __restrict__ lo) {
+  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n;
+       i += (size_t)gridDim.x * blockDim.x * 4) {
+    const char4 v = *reinterpret_cast<const char4*>(q + i);
+    const int8_t qv[4] = {v.x, v.y, v.z, v.w};
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const size_t e = i + j;
+      const float w = (float)qv[j] * sc[(e / cols) * (cols / 32) + (e % cols) / 32];
+      h[j] = bf16_bits(w);
+      l[j] = bf16_bits(w - __uint_as_float((uint32_t)h[j] << 16));
+    }
+    *reinterpret_cast<uint2*>(hi + i) =
+        make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+    *reinterpret_cast<uint2*>(lo + i) =
+        make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+  }
+}
+
+void launch_dequant_planes(const int8_t* q, const float* sc, size_t n, int cols, uint16_t* hi,
+                           uint16_t* lo, hipStream_t s) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(dequant_planes_kernel, dim3(4096), dim3(256), 0, s, q, sc, n, cols, hi, lo);
+}
 
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
   if (n == 0) return;
@@ -390,13 +448,21 @@ static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                         int tiles_bound, bool bf16_only, hipStream_t s) {
-  const dim3 grid(mfma_grid(L, tiles_bound, GATEUP));
-  if (bf16_only)
+  const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(kWaves * 64);
+  if (L.quant_mode != kQuantNone) {
+    if (bf16_only)
+      mfma_group_kernel<kWaves, kBkQ, kBufQ, false, GATEUP, true>
+          <<<grid, block, mfma_lds_bytes<kBkQ, kBufQ, 3>(), s>>>(L, S, P, T);
+    else
+      mfma_group_kernel<kWaves, kBkQ, kBufQ, true, GATEUP, true>
+          <<<grid, block, mfma_lds_bytes<kBkQ, kBufQ, 4>(), s>>>(L, S, P, T);
+  } else if (bf16_only) {
     mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, GATEUP>
-        <<<grid, dim3(kWaves * 64), mfma_lds_bytes<kBkBf16, kBufBf16, false>(), s>>>(L, S, P, T);
-  else
+        <<<grid, block, mfma_lds_bytes<kBkBf16, kBufBf16, 2>(), s>>>(L, S, P, T);
+  } else {
     mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, GATEUP>
-        <<<grid, dim3(kWaves * 64), mfma_lds_bytes<kBkSplit, kBufSplit, true>(), s>>>(L, S, P, T);
+        <<<grid, block, mfma_lds_bytes<kBkSplit, kBufSplit, 3>(), s>>>(L, S, P, T);
+  }
 }
 
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -410,18 +476,25 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
 }
 
 void mfma_init_attributes() {
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, true>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, false>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<kBkBf16, kBufBf16, false>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, true>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
-  (void)hipFuncSetAttribute((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, false>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)mfma_lds_bytes<kBkSplit, kBufSplit, true>());
+  auto set = [](const void* k, size_t bytes) {
+    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  };
+  set((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, true>,
+      mfma_lds_bytes<kBkBf16, kBufBf16, 2>());
+  set((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, false>,
+      mfma_lds_bytes<kBkBf16, kBufBf16, 2>());
+  set((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, true>,
+      mfma_lds_bytes<kBkSplit, kBufSplit, 3>());
+  set((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, false>,
+      mfma_lds_bytes<kBkSplit, kBufSplit, 3>());
+  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, false, true, true>,
+      mfma_lds_bytes<kBkQ, kBufQ, 3>());
+  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, false, false, true>,
+      mfma_lds_bytes<kBkQ, kBufQ, 3>());
+  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, true, true, true>,
+      mfma_lds_bytes<kBkQ, kBufQ, 4>());
+  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, true, false, true>,
+      mfma_lds_bytes<kBkQ, kBufQ, 4>());
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
 

@@ -9,6 +9,9 @@ namespace uocr {
 
 // Expert "groups": 0..E-1 are the routed experts, E is the fused shared
 // expert (width S = I * n_shared_experts).
+// uocr_quant_mode values (uocr_moe.h), for device code.
+constexpr int kQuantNone = 0, kQuantWeightsOnly = 1, kQuantDynamic = 2;
+
 struct DeviceLayer {
   int H, I, S, E, K;
   int normalize;
@@ -27,8 +30,14 @@ struct DeviceLayer {
   const int8_t* q2;
   const float* s2;
   const float* norm_w;       // [H] post-attention RMSNorm weight (f32)
+  // INT8 overlay dequantised (q * s) as bf16 planes for the MFMA engine:
+  // hi at dq13[0, n13), lo at dq13[n13, 2 n13); likewise dq2.
+  const uint16_t* dq13;
+  const uint16_t* dq2;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
+  __host__ __device__ size_t n13() const { return ((size_t)E * 2 * I + 2 * (size_t)S) * H; }
+  __host__ __device__ size_t n2() const { return ((size_t)E * I + S) * H; }
   __host__ __device__ size_t w13_offset(int g) const { return (size_t)g * 2 * I * H; }
   __host__ __device__ size_t w2_offset(int g) const { return (size_t)g * H * I; }
   __host__ __device__ size_t s13_offset(int g) const { return (size_t)g * 2 * I * (H / 32); }
@@ -84,9 +93,9 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 // logits, then one workgroup that routes and builds the dispatch.
 bool batch_supported(const DeviceLayer& L);
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s);
+                         int mchunk, hipStream_t s, bool singles = false);
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s);
+                       hipStream_t s, bool singles = false);
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
                         hipStream_t s);
 
@@ -112,6 +121,8 @@ struct MfmaPlanes {
   uint16_t* hs_lo;
 };
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
+void launch_dequant_planes(const int8_t* q, const float* sc, size_t n, int cols, uint16_t* hi,
+                           uint16_t* lo, hipStream_t s);
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                         int tiles_bound, bool bf16_only, hipStream_t s);
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
