@@ -307,21 +307,24 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    // ---- compute phase
+    // ---- compute phase. Gate/up puts the weight fragment first, so each
+    // accumulator holds a [32 features x 32 tokens] block (lane l owns token
+    // l % 32 and four consecutive features per register quad: h leaves in
+    // 8-byte stores). Down keeps [32 tokens x 32 features] (lane l owns
+    // feature l % 32: a half-wave writes 32 adjacent outputs of one row).
+    auto mma = [&](const bf16x8& a, const bf16x8& b, floatx16& c) {
+      c = GATEUP ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0)
+                 : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    };
 #pragma unroll
     for (int sub = 0; sub < kSub; sub++)
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
 #pragma unroll
         for (int ni = 0; ni < kNi; ni++) {
-          acc[mi][ni] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[sub][mi], fb[sub][ni], acc[mi][ni], 0, 0, 0);
-          if constexpr (SPLIT)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[sub][mi], fb[sub][ni],
-                                                                  acc[mi][ni], 0, 0, 0);
-          if constexpr (SPLITB)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[sub][mi], fbl[sub][ni],
-                                                                  acc[mi][ni], 0, 0, 0);
+          mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
+          if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
+          if constexpr (SPLITB) mma(fa[sub][mi], fbl[sub][ni], acc[mi][ni]);
         }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -329,34 +332,46 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   }
   if (!grp) __syncthreads();
 
-  // Output element (mi, ni, r) of this lane: row 128 wm + 32 mi + 8 (r/4) +
-  // 4 (lane/32) + r%4, column kWc wn + 32 ni + lane%32.
   const int wcol0 = n0 + wn * kWc;
   if (wcol0 >= N) return;
   if (GATEUP) {
+    // Output element (mi, ni, r) of this lane: token row 128 wm + 32 mi +
+    // lane%32, feature column kWc wn + 32 ni + 8 (r/4) + 4 (lane/32) + r%4;
+    // registers 4j .. 4j+3 are four consecutive features of one token.
     // Columns 64b .. 64b+63 of the wave are one (gate, up) block pair.
+    // SiLU(g) u = g / (1 + exp(-g)) u with a hardware reciprocal.
     uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
     uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
 #pragma unroll
     for (int bp = 0; bp < kNi / 2; bp++) {
       if (wcol0 + 64 * bp >= N) break;
-      const int col = (wcol0 + 64 * bp) / 2 + fr;  // hidden column of this lane
+      const int col0 = (wcol0 + 64 * bp) / 2 + 4 * fc;  // hidden column of register 0
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++)
+      for (int mi = 0; mi < 4; mi++) {
+        const int row = wm * 128 + 32 * mi + fr;
+        if (row >= mrows) continue;
+        const size_t at0 = (size_t)(base + r0 + row) * W + col0;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row < mrows) {
-            const float gv = acc[mi][2 * bp][r];
-            const float h = __fdividef(gv, 1.0f + __expf(-gv)) * acc[mi][2 * bp + 1][r];
-            const size_t at = (size_t)(base + r0 + row) * W + col;
-            const uint16_t hb = bf16_bits(h);
-            h_hi[at] = hb;
-            if constexpr (SPLIT) h_lo[at] = bf16_bits(h - __uint_as_float((uint32_t)hb << 16));
+        for (int j = 0; j < 4; j++) {
+          uint32_t hb[4], lb[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float gv = acc[mi][2 * bp][4 * j + i];
+            const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][2 * bp + 1][4 * j + i];
+            hb[i] = bf16_bits(h);
+            if constexpr (SPLIT) lb[i] = bf16_bits(h - __uint_as_float(hb[i] << 16));
           }
+          *reinterpret_cast<uint2*>(h_hi + at0 + 8 * j) =
+              make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+          if constexpr (SPLIT)
+            *reinterpret_cast<uint2*>(h_lo + at0 + 8 * j) =
+                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
         }
+      }
     }
   } else {
+    // Output element (mi, ni, r) of this lane: row 128 wm + 32 mi + 8 (r/4)
+    // + 4 (lane/32) + r%4, column kWc wn + 32 ni + lane%32.
     // FP32-class and INT8 weights: y in f32. BF16 weights with BF16
     // activations: y rounded to bf16 (the combine's operands), in the first
     // half of the same buffer.
