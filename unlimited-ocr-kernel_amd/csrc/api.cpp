@@ -320,6 +320,8 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     return fail(UOCR_ERR_UNSUPPORTED, "small-batch engine needs hidden and shared widths <= 2048");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
   const int bm = mfma ? uocr::kMfmaBM : uocr::kGemvChunk;
+  // The MFMA engine runs an expert's last tile of <= 128 rows as 128 x 512 items.
+  const int narrow = mfma ? uocr::kMfmaBM / 2 : 0;
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
@@ -349,7 +351,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
                                     S.logits, S.topk_ids, S.topk_w, S.chunk_counts, S.err, st);
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
-      uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.chunk_counts,
+      uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, narrow, S.chunk_counts,
                                     S.offsets, S.perm_rows, S.perm_w, S.inv_pos, S.tiles,
                                     S.counters, st);
       phase_end(ctx);
@@ -364,7 +366,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
                         S.err, st);
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
-      uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, S.offsets, S.perm_rows,
+      uocr::launch_dispatch(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, narrow, S.offsets, S.perm_rows,
                             S.perm_w, S.inv_pos, S.tiles, S.counters, st);
       phase_end(ctx);
     }

@@ -21,13 +21,55 @@ int max_tiles(int T, int K, int E, int bm) {
 constexpr int kDispatchThreads = 1024;
 constexpr int kDispatchWaves = kDispatchThreads / 64;
 
+// Row tiles, written by one wave: lane e holds expert e's row count c (0
+// past E). Routed tiles of bm rows go expert-major into a first list; when
+// narrow > 0, an expert's last tile of at most `narrow` rows goes instead to
+// a second list placed after the first (the MFMA engine runs those as 128 x
+// 512 items); the shared expert's tiles follow. counters: [0] all tiles,
+// [1] routed tiles, [2] routed tiles of the first list.
+__device__ void write_tiles(int lane, int c, int T, int bm, int narrow, int* __restrict__ tiles,
+                            int* __restrict__ counters, int shared_group) {
+  const int full = c / bm, rem = c - full * bm;
+  const bool nar = narrow > 0 && rem > 0 && rem <= narrow;
+  const int nsq = full + ((rem > 0 && !nar) ? 1 : 0);
+  const int packed = nsq | ((nar ? 1 : 0) << 16);  // both counts stay below 2^16
+  int incl = packed;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  const int excl = incl - packed;
+  const int total = __shfl(incl, 63);
+  const int routed_sq = total & 0xffff, routed_tiles = routed_sq + (total >> 16);
+  const int sq0 = excl & 0xffff, nr0 = excl >> 16;
+  for (int i = 0; i < nsq; i++) {
+    tiles[2 * (sq0 + i)] = lane;
+    tiles[2 * (sq0 + i) + 1] = i * bm;
+  }
+  if (nar) {
+    tiles[2 * (routed_sq + nr0)] = lane;
+    tiles[2 * (routed_sq + nr0) + 1] = full * bm;
+  }
+  const int shared_tiles = (T + bm - 1) / bm;
+  for (int i = lane; i < shared_tiles; i += 64) {
+    tiles[2 * (routed_tiles + i)] = shared_group;
+    tiles[2 * (routed_tiles + i) + 1] = i * bm;
+  }
+  if (lane == 0) {
+    counters[0] = routed_tiles + shared_tiles;
+    counters[1] = routed_tiles;
+    counters[2] = routed_sq;
+  }
+}
+
 // One workgroup. Tokens are taken 1024 at a time (one per thread); inside a
 // wave the rank of a token among earlier tokens of the same expert comes
 // from a ballot, across waves from an LDS prefix, across chunks from a
 // running count — together the stable counting sort.
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int* __restrict__ ids, const float* __restrict__ w, int T, int E, int K, int bm,
-    int* __restrict__ offsets, int* __restrict__ perm_rows, float* __restrict__ perm_w,
+    int narrow, int* __restrict__ offsets, int* __restrict__ perm_rows, float* __restrict__ perm_w,
     int* __restrict__ inv_pos, int* __restrict__ tiles, int* __restrict__ counters) {
   __shared__ int count[64];
   __shared__ int base[64];
@@ -59,29 +101,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       offsets[lane] = excl;
     }
     if (lane == 0) offsets[E] = T * K;
-    // Row tiles of bm rows per expert, then the shared expert's tiles.
-    int nt = lane < E ? (c + bm - 1) / bm : 0;
-    int tincl = nt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      int v = __shfl_up(tincl, o);
-      if (lane >= o) tincl += v;
-    }
-    int tstart = tincl - nt;
-    for (int i = 0; i < nt; i++) {
-      tiles[2 * (tstart + i)] = lane;
-      tiles[2 * (tstart + i) + 1] = i * bm;
-    }
-    int routed_tiles = __shfl(tincl, 63);
-    int shared_tiles = (T + bm - 1) / bm;
-    for (int i = lane; i < shared_tiles; i += 64) {
-      tiles[2 * (routed_tiles + i)] = E;
-      tiles[2 * (routed_tiles + i) + 1] = i * bm;
-    }
-    if (lane == 0) {
-      counters[0] = routed_tiles + shared_tiles;
-      counters[1] = routed_tiles;
-    }
+    write_tiles(lane, c, T, bm, narrow, tiles, counters, E);
   }
   __syncthreads();
   for (int c0 = 0; c0 < T; c0 += kDispatchThreads) {
@@ -155,7 +175,7 @@ constexpr int kFusedThreads = 256;  // 16 chunk rows x 16 expert quads per pass
 // dispatch (src/decoder/mod.rs:124-183).
 __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
     const int* __restrict__ chunk_counts, const int* __restrict__ ids, const float* __restrict__ w,
-    int nchunks, int T, int E, int K, int bm, int* __restrict__ offsets,
+    int nchunks, int T, int E, int K, int bm, int narrow, int* __restrict__ offsets,
     int* __restrict__ perm_rows, float* __restrict__ perm_w, int* __restrict__ inv_pos,
     int* __restrict__ tiles, int* __restrict__ counters) {
   __shared__ __attribute__((aligned(16))) int part_tot[16][64];
@@ -207,28 +227,7 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
     if (c == 0) {
       if (lane < E) offsets[lane] = excl;
       if (lane == 0) offsets[E] = T * K;
-      const int nt = lane < E ? (total + bm - 1) / bm : 0;
-      int tincl = nt;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(tincl, o);
-        if (lane >= o) tincl += v;
-      }
-      const int tstart = tincl - nt;
-      for (int i = 0; i < nt; i++) {
-        tiles[2 * (tstart + i)] = lane;
-        tiles[2 * (tstart + i) + 1] = i * bm;
-      }
-      const int routed_tiles = __shfl(tincl, 63);
-      const int shared_tiles = (T + bm - 1) / bm;
-      for (int i = lane; i < shared_tiles; i += 64) {
-        tiles[2 * (routed_tiles + i)] = E;
-        tiles[2 * (routed_tiles + i) + 1] = i * bm;
-      }
-      if (lane == 0) {
-        counters[0] = routed_tiles + shared_tiles;
-        counters[1] = routed_tiles;
-      }
+      write_tiles(lane, total, T, bm, narrow, tiles, counters, E);
     }
   }
   if (tid < 64) emask[tid] = 0ull;
@@ -261,19 +260,20 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
 }
 
 void launch_dispatch_chunked(const int* ids, const float* w, int T, int E, int K, int bm,
-                             const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
+                             int narrow, const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
                              int* inv_pos, int* tiles, int* counters, hipStream_t s) {
   const int nchunks = (T + kChunk - 1) / kChunk;
   hipLaunchKernelGGL(dispatch_fused_kernel, dim3(nchunks), dim3(kFusedThreads), 0, s, chunk_counts,
-                     ids, w, nchunks, T, E, K, bm, offsets, perm_rows, perm_w, inv_pos, tiles,
-                     counters);
+                     ids, w, nchunks, T, E, K, bm, narrow, offsets, perm_rows, perm_w, inv_pos,
+                     tiles, counters);
 }
 
-void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,
+void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int narrow,
+                     int* offsets,
                      int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
                      hipStream_t s) {
   hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, ids, w, T, E, K, bm,
-                     offsets, perm_rows, perm_w, inv_pos, tiles, counters);
+                     narrow, offsets, perm_rows, perm_w, inv_pos, tiles, counters);
 }
 
 }  // namespace uocr

@@ -93,64 +93,32 @@ constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at maximum).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// One work item: a TM x TN output tile of group g, rows r0.. of the group,
+// columns n0... Two shapes share the code: 256 x 256 (waves 2 x 4) for
+// groups with more than 128 rows left, and 128 x 512 (waves 1 x 8) for the
+// last tile of a group when at most 128 rows remain — a cold expert then
+// streams its weights in half as many items without computing a mostly
+// empty 256-row tile. Either way a wave owns 128 rows and 64 columns as 4 x 2
+// MFMA tiles, so the fragment reads per wave are the same.
+//
 // SPLITB: INT8-overlay weights as dequantised bf16 hi + lo planes (a third
-// product term), y always f32; groups of one row are skipped when the
-// overlay runs DynamicActivations (the batch engine's W8A8 path owns them).
-template <int WAVES, int BK, int NBUF, bool SPLIT, bool GATEUP, bool SPLITB = false>
-__global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
-                                                                   MfmaPlanes P, int T) {
-  // Waves form a 2 x (WAVES/2) grid over the 256 x 256 tile; each owns 128
-  // rows and kWc columns as 4 x kNi MFMA tiles.
-  constexpr int kWn = WAVES / 2;
-  constexpr int kWc = kTileN / kWn;
+// product term), y always f32.
+template <int TM, int BK, int NBUF, bool SPLIT, bool GATEUP, bool SPLITB>
+__device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S,
+                                          const MfmaPlanes& P, int T, int g, int r0, int n0,
+                                          uint16_t* lds) {
+  constexpr int WAVES = 8;
+  constexpr int TN = 256 * 256 / TM;      // 256 or 512
+  constexpr int kWm = TM / 128;            // wave rows
+  constexpr int kWn = WAVES / kWm;         // wave columns
+  constexpr int kWc = TN / kWn;            // 64 columns per wave
   constexpr int kNi = kWc / 32;
-  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
-  __shared__ int arow[kTileM];
-
-  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
-  // items are listed shared-expert first, then routed (each in row-tile,
-  // column-tile order), and cut into 8 contiguous ranges of equal cost, one
-  // per XCD: an item costs its K depth, so the deeper shared items of the
-  // down GEMM do not pile up on one XCD, neighbouring items (same expert,
-  // same rows) meet in one L2, and an XCD's deeper items start first.
-  const int routed_tiles = S.counters[1];
-  const int all_tiles = S.counters[0];
-  const int n_routed = GATEUP ? 2 * L.I : L.H;
-  const int n_shared = GATEUP ? 2 * L.S : L.H;
-  const int nt_routed = (n_routed + kTileN - 1) / kTileN;
-  const int nt_shared = (n_shared + kTileN - 1) / kTileN;
-  const long long routed_items = (long long)routed_tiles * nt_routed;
-  const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
-  const long long c_shared = GATEUP ? L.H : L.S, c_routed = GATEUP ? L.H : L.I;
-  const long long shared_cost = shared_items * c_shared;
-  const long long total_cost = shared_cost + routed_items * c_routed;
-  // First item of XCD x: the first whose cost prefix reaches x / 8 of the total.
-  auto first_item = [&](int x) -> long long {
-    const long long b = total_cost * x / kXcds;
-    if (b <= shared_cost) return (b + c_shared - 1) / c_shared;
-    return shared_items + (b - shared_cost + c_routed - 1) / c_routed;
-  };
-  const int xcd = blockIdx.x % kXcds;
-  const long long item = first_item(xcd) + blockIdx.x / kXcds;
-  if (item >= first_item(xcd + 1)) return;
-  int tile, ntile;
-  if (item < shared_items) {
-    tile = routed_tiles + (int)(item / nt_shared);
-    ntile = (int)(item % nt_shared);
-  } else {
-    tile = (int)((item - shared_items) / nt_routed);
-    ntile = (int)((item - shared_items) % nt_routed);
-  }
-  const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
   const bool routed = g < L.E;
   const int W = L.width(g);
   const int N = GATEUP ? 2 * W : L.H;
   const int K = GATEUP ? L.H : W;
-  const int n0 = ntile * kTileN;
   const int group_rows = routed ? S.offsets[g + 1] - S.offsets[g] : T;
-  if (SPLITB && routed && group_rows == 1 && L.quant_mode == kQuantDynamic)
-    return;
-  const int mrows = min(kTileM, group_rows - r0);
+  const int mrows = min(TM, group_rows - r0);
   const int base = routed ? S.offsets[g] : 0;
 
   const int tid = threadIdx.x;
@@ -158,43 +126,54 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   const int wave = tid >> 6;
   const int wm = wave / kWn, wn = wave % kWn;
 
-  if (tid < kTileM) {
-    int src = -1;
-    if (tid < mrows) {
-      if (GATEUP)
-        src = routed ? S.perm_rows[base + r0 + tid] : r0 + tid;
-      else
-        src = base + r0 + tid;
-    }
-    arow[tid] = src;
-  }
-  __syncthreads();
+  // Source row of tile row r (gate/up: the token, gathered through the
+  // dispatch permutation; down: the dispatched row), -1 past the group.
+  auto a_source = [&](int r) -> int {
+    if (r >= mrows) return -1;
+    if (GATEUP) return routed ? S.perm_rows[base + r0 + r] : r0 + r;
+    return base + r0 + r;
+  };
 
-  // ---- LDS tiles. A stage holds the A plane(s) and B, each [256 rows][BK]
-  // bf16 with no padding: chunk c (8 bf16) of row r sits at position
-  // c ^ swz(r), which spreads the 16-byte fragment reads of 16 consecutive
-  // rows over all LDS banks. Loads arrive as 1 KB wave segments of
-  // kSegRows rows (lane l -> row l / kCpr, position l % kCpr).
+  // ---- LDS tiles. A stage holds the A plane(s) ([TM rows][BK]) and the B
+  // plane(s) ([TN rows][BK]), bf16 with no padding: chunk c (8 bf16) of row
+  // r sits at position c ^ swz(r), which spreads the 16-byte fragment reads
+  // of 16 consecutive rows over all LDS banks. Loads arrive as 1 KB wave
+  // segments of kSegRows rows (lane l -> row l / kCpr, position l % kCpr).
   constexpr int kCpr = BK / 8;                 // 16-byte chunks per row
   constexpr int kSegRows = 64 / kCpr;          // rows per 1 KB segment
-  constexpr int kSegs = kTileM / kSegRows;     // segments per plane
-  constexpr int kSegPerWave = kSegs / WAVES;   // per wave, per plane
+  // Segments per wave and plane. When a plane has fewer segments than there
+  // are waves (128 rows of 16-deep stages), waves past the last segment load
+  // a copy of segment wave % count (the same bytes to the same place), so
+  // every wave issues the same number of loads per stage.
+  constexpr int kSegTotA = TM / kSegRows, kSegTotB = TN / kSegRows;
+  constexpr int kSegA = kSegTotA >= WAVES ? kSegTotA / WAVES : 1;
+  constexpr int kSegB = kSegTotB >= WAVES ? kSegTotB / WAVES : 1;
+  static_assert(kSegTotA % WAVES == 0 || WAVES % kSegTotA == 0, "A segments");
+  static_assert(kSegTotB % WAVES == 0, "B segments");
+  const int segA0 = kSegTotA >= WAVES ? wave * kSegA : wave % kSegTotA;
   constexpr int kRowDiv = 16 / kCpr;
   auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
-  const uint32_t plane_bytes = (uint32_t)kTileM * BK * 2;
-  constexpr int kPlanes = 2 + (SPLIT ? 1 : 0) + (SPLITB ? 1 : 0);
-  const uint32_t stage_bytes = kPlanes * plane_bytes;
-  const uint32_t blo_plane = (SPLIT ? 3 : 2) * plane_bytes;  // B lo, when SPLITB
+  constexpr uint32_t a_plane = (uint32_t)TM * BK * 2, b_plane = (uint32_t)TN * BK * 2;
+  constexpr int kAPlanes = SPLIT ? 2 : 1, kBPlanes = SPLITB ? 2 : 1;
+  constexpr uint32_t stage_bytes = kAPlanes * a_plane + kBPlanes * b_plane;
+  // Plane order in a stage: A hi, B, [A lo], [B lo].
+  constexpr uint32_t b_at = a_plane, alo_at = a_plane + b_plane,
+                     blo_at = a_plane + b_plane + (SPLIT ? a_plane : 0);
 
   // Per-lane source offsets of this wave's segments (k = 0).
   const uint32_t row_bytes = (uint32_t)K * 2;
-  uint32_t a_off[kSegPerWave], b_off[kSegPerWave];
+  uint32_t a_off[kSegA], b_off[kSegB];
 #pragma unroll
-  for (int i = 0; i < kSegPerWave; i++) {
-    const int r = (wave * kSegPerWave + i) * kSegRows + lane / kCpr;
+  for (int i = 0; i < kSegA; i++) {
+    const int r = (segA0 + i) * kSegRows + lane / kCpr;
     const int c = (lane % kCpr) ^ swz(r);
-    const int src_row = arow[r];
+    const int src_row = a_source(r);
     a_off[i] = src_row >= 0 ? (uint32_t)src_row * row_bytes + 16u * c : kDmaOut;
+  }
+#pragma unroll
+  for (int i = 0; i < kSegB; i++) {
+    const int r = (wave * kSegB + i) * kSegRows + lane / kCpr;
+    const int c = (lane % kCpr) ^ swz(r);
     b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes + 16u * c : kDmaOut;
   }
   const uint16_t* a_hi_src;
@@ -221,19 +200,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
   const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes);
   const i32x4 rs_bl = buffer_rsrc(SPLITB ? wmat_lo : wmat, (uint32_t)N * row_bytes);
-  // LDS byte address of this wave's first segment of stage buffer 0.
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
-      (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds) +
-      (uint32_t)wave * kSegPerWave * 1024u);
+  // LDS byte addresses of this wave's first A and B segments of stage buffer 0.
+  const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds);
+  const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_base + (uint32_t)segA0 * 1024u);
+  const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_base + b_at + (uint32_t)wave * kSegB * 1024u);
   auto issue = [&](int buf, int k0) {
-    const uint32_t st = lds0 + (uint32_t)buf * stage_bytes;
+    const uint32_t st = (uint32_t)buf * stage_bytes;
     const uint32_t kb = (uint32_t)k0 * 2u;
 #pragma unroll
-    for (int i = 0; i < kSegPerWave; i++) {
-      buffer_load_lds16(rs_a, st + i * 1024u, a_off[i] + kb);
-      buffer_load_lds16(rs_b, st + plane_bytes + i * 1024u, b_off[i] + kb);
-      if constexpr (SPLIT) buffer_load_lds16(rs_l, st + 2 * plane_bytes + i * 1024u, a_off[i] + kb);
-      if constexpr (SPLITB) buffer_load_lds16(rs_bl, st + blo_plane + i * 1024u, b_off[i] + kb);
+    for (int i = 0; i < kSegA; i++) {
+      buffer_load_lds16(rs_a, lds_a + st + i * 1024u, a_off[i] + kb);
+      if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + kb);
+    }
+#pragma unroll
+    for (int i = 0; i < kSegB; i++) {
+      buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + kb);
+      if constexpr (SPLITB) buffer_load_lds16(rs_bl, lds_b + st + (blo_at - b_at) + i * 1024u, b_off[i] + kb);
     }
   };
 
@@ -264,9 +246,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   // the end of a memory phase "own loads of stage ks + 1 landed" is
   // vmcnt <= (kDepth - 1) * kLps; the barrier then publishes them to both
   // groups before either reads stage ks + 1.
-  static_assert(WAVES == 8, "the ping-pong schedule pairs two waves per SIMD");
   constexpr int kDepth = NBUF - 1;
-  constexpr int kLps = kSegPerWave * kPlanes;
+  constexpr int kLps = kSegA * kAPlanes + kSegB * kBPlanes;
   constexpr int kSub = BK / 16;
   const int grp = wave >> 2;
   for (int i = 0; i < kDepth; i++)
@@ -291,13 +272,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
       const int c = 2 * sub + fc;
 #pragma unroll
       for (int ni = 0; ni < kNi; ni++) {
-        fb[sub][ni] = frag(cur + plane_bytes, wn * kWc + ni * 32 + fr, c);
-        if constexpr (SPLITB) fbl[sub][ni] = frag(cur + blo_plane, wn * kWc + ni * 32 + fr, c);
+        fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
+        if constexpr (SPLITB) fbl[sub][ni] = frag(cur + blo_at, wn * kWc + ni * 32 + fr, c);
       }
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) {
         fa[sub][mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
-        if constexpr (SPLIT) fl[sub][mi] = frag(cur + 2 * plane_bytes, wm * 128 + mi * 32 + fr, c);
+        if constexpr (SPLIT) fl[sub][mi] = frag(cur + alo_at, wm * 128 + mi * 32 + fr, c);
       }
     }
     if (steady)
@@ -397,17 +378,126 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mfma_group_kernel(DeviceLayer L
   }
 }
 
-template <int BK, int NBUF, int PLANES>
-constexpr size_t mfma_lds_bytes() {
-  return (size_t)NBUF * PLANES * kTileM * BK * sizeof(uint16_t);
+// Item costs for the XCD split, in units of one 32-deep k step of a 256 x
+// 256 tile (8) — a 128 x 512 item moves 1.25x the bytes of a square one for
+// the same MFMA work, so it counts 9.
+constexpr int kCostSquare = 8, kCostWide = 9;
+
+// Which variants run the 128 x 512 shape. The FP32-class BF16 engine moves
+// as many bytes per stage in either shape (the A planes are hi + lo), so a
+// small group's last tile costs half. With one activation plane the wide
+// stage moves 1.25x the bytes and a small group's items are bound by their
+// weight stream from HBM, which the shape does not shorten: measured on the
+// 12-layer 4096-token stack, square items only are faster there (4.59 vs
+// 4.69 ms) and on the 512-token INT8 layer (0.40 vs 0.43 ms), while the
+// FP32 class gains (7.21 -> 6.91 ms; 1024 tokens 0.32 -> 0.27 ms).
+template <bool SPLIT, bool SPLITB>
+constexpr bool use_wide_items() { return SPLIT && !SPLITB; }
+
+// Groups of one row are skipped when the overlay runs DynamicActivations
+// (the batch engine's W8A8 path owns them). NBUF_W: stage buffers of the
+// 128 x 512 shape.
+template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool SPLITB = false>
+__global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
+                                                            MfmaPlanes P, int T) {
+  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
+  constexpr bool kWide = use_wide_items<SPLIT, SPLITB>();
+
+  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
+  // square items (shared expert first, then routed, each in row-tile,
+  // column-tile order) are cut into 8 contiguous ranges of equal cost, one
+  // per XCD, and so are the 128 x 512 items; an XCD interleaves its two
+  // ranges. An item costs its K depth times its shape's cost,
+  // so the deeper shared items of the down GEMM do not pile up on one XCD,
+  // neighbouring square items (same expert, same rows) meet in one L2, an
+  // XCD's deeper items start first, and the weight streams of the small
+  // groups (one wide item per 512 columns, little reuse) spread over every
+  // XCD's path to HBM.
+  const int all_tiles = S.counters[0];
+  const int routed_tiles = S.counters[1];
+  const int square_tiles = kWide ? S.counters[2] : routed_tiles;
+  const int n_routed = GATEUP ? 2 * L.I : L.H;
+  const int n_shared = GATEUP ? 2 * L.S : L.H;
+  const int nt_routed = (n_routed + kTileN - 1) / kTileN;
+  const int nt_wide = (n_routed + 2 * kTileN - 1) / (2 * kTileN);
+  const int nt_shared = (n_shared + kTileN - 1) / kTileN;
+  const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
+  const long long square_items = (long long)square_tiles * nt_routed;
+  const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
+  const long long c_shared = (GATEUP ? L.H : L.S) * kCostSquare;
+  const long long c_square = (GATEUP ? L.H : L.I) * kCostSquare;
+  const long long c_wide = (GATEUP ? L.H : L.I) * kCostWide;
+  const long long cost1 = shared_items * c_shared;
+  const long long cost_sq = cost1 + square_items * c_square;
+  const long long cost_wd = wide_items * c_wide;
+  // First square item of XCD x: the first whose cost prefix reaches x / 8 of
+  // the square cost; likewise the first wide item.
+  auto first_sq = [&](int x) -> long long {
+    const long long b = cost_sq * x / kXcds;
+    if (b <= cost1) return (b + c_shared - 1) / c_shared;
+    return shared_items + (b - cost1 + c_square - 1) / c_square;
+  };
+  auto first_wd = [&](int x) -> long long { return (cost_wd * x / kXcds + c_wide - 1) / c_wide; };
+  const int xcd = blockIdx.x % kXcds;
+  const long long j = blockIdx.x / kXcds;
+  const long long sq0 = first_sq(xcd), n_sq = first_sq(xcd + 1) - sq0;
+  const long long wd0 = first_wd(xcd), n_wd = first_wd(xcd + 1) - wd0;
+  const long long n_xcd = n_sq + n_wd;
+  if (j >= n_xcd) return;
+  // The XCD's j-th workgroup: its wide items are spread evenly between its
+  // square ones (local slot j is wide when floor(j n_wd / n) steps), so the
+  // HBM-bound weight streams of small groups run alongside the L2-resident
+  // square work instead of all at once.
+  const long long wd_before = j * n_wd / n_xcd;
+  const bool take_wide = (j + 1) * n_wd / n_xcd > wd_before;
+  const long long item = take_wide ? shared_items + square_items + wd0 + wd_before
+                                   : sq0 + (j - wd_before);
+  int tile, ntile;
+  bool wide = false;
+  if (item < shared_items) {
+    tile = routed_tiles + (int)(item / nt_shared);
+    ntile = (int)(item % nt_shared);
+  } else if (item < shared_items + square_items) {
+    const long long i = item - shared_items;
+    tile = (int)(i / nt_routed);
+    ntile = (int)(i % nt_routed);
+  } else {
+    const long long i = item - shared_items - square_items;
+    tile = square_tiles + (int)(i / nt_wide);
+    ntile = (int)(i % nt_wide);
+    wide = true;
+  }
+  const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
+  if (SPLITB && g < L.E && L.quant_mode == kQuantDynamic &&
+      S.offsets[g + 1] - S.offsets[g] == 1)
+    return;
+  if constexpr (kWide) {
+    if (wide) {
+      mfma_item<128, BK, NBUF_W, SPLIT, GATEUP, SPLITB>(L, S, P, T, g, r0, ntile * 2 * kTileN, lds);
+      return;
+    }
+  }
+  mfma_item<256, BK, NBUF, SPLIT, GATEUP, SPLITB>(L, S, P, T, g, r0, ntile * kTileN, lds);
 }
-// BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class
-// (hi + lo planes): 32-deep stages, three buffers (144 KiB). INT8 overlay
-// (dequantised weight hi + lo planes, and the activation's lo plane in the
-// FP32 class): 16-deep stages, four buffers (96 / 128 KiB).
-constexpr int kBkBf16 = 32, kBufBf16 = 4, kBkSplit = 32, kBufSplit = 3;
-constexpr int kBkQ = 16, kBufQ = 4;
-constexpr int kWaves = 8;
+
+// Dynamic LDS of one shape: NBUF stages of the A planes (TM rows) and the B
+// planes (256 * 256 / TM rows), BK deep.
+constexpr size_t stage_lds(int TM, int BK, int NBUF, int a_planes, int b_planes) {
+  return (size_t)NBUF * (a_planes * TM + b_planes * (kTileM * kTileN / TM)) * BK * sizeof(uint16_t);
+}
+template <int BK, int NBUF, int NBUF_W, int AP, int BP, bool WIDE>
+constexpr size_t mfma_lds_bytes() {
+  const size_t sq = stage_lds(256, BK, NBUF, AP, BP);
+  const size_t wd = WIDE ? stage_lds(128, BK, NBUF_W, AP, BP) : 0;
+  return sq > wd ? sq : wd;
+}
+// BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class (hi +
+// lo planes): 32-deep stages, three buffers (144 KiB either shape). INT8
+// overlay (dequantised weight hi + lo planes, and the activation's lo plane
+// in the FP32 class): 16-deep stages, four buffers (96 / 128 KiB). The
+// wide-shape counts apply only where use_wide_items() enables that shape.
+constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 4, kBkSplit = 32, kBufSplit = 3;
+constexpr int kBkQ = 16, kBufQ = 4, kBufQW = 3;
 
 // INT8 overlay -> bf16 planes of the dequantised weight: w = q * s rounded to
 // f32 as Int8Matrix::linear does (src/cpu/quantized.rs:119-131), then hi =
@@ -449,34 +539,43 @@ void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, h
 }
 
 // Workgroups: 8 XCDs times the most items one XCD can take. Items are
-// bounded by every row tile times the widest column count; an XCD's range
-// holds an eighth of the cost, so at most (bound / 8) * (deepest / shallowest
-// item) + 2 items.
+// bounded by every row tile times the widest column count of square items
+// (a 128 x 512 item replaces two square ones); an XCD's two ranges hold an
+// eighth of their cost each, so at most (bound / 8) * (dearest / cheapest
+// item) + 4 items.
 static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   const int n = gateup ? std::max(2 * L.S, 2 * L.I) : L.H;
   const long long items = (long long)tiles_bound * ((n + kTileN - 1) / kTileN);
-  const long long deep = gateup ? 1 : std::max(L.S, L.I), shallow = gateup ? 1 : std::min(L.S, L.I);
-  const long long per_xcd = (items * deep + kXcds * shallow - 1) / (kXcds * shallow) + 2;
+  const long long k_routed = gateup ? L.H : L.I, k_shared = gateup ? L.H : L.S;
+  const long long dear = std::max(k_shared * kCostSquare, k_routed * kCostWide);
+  const long long cheap = std::min(k_shared, k_routed) * kCostSquare;
+  // Two ranges per XCD (square, wide), each at most one item over its share.
+  const long long per_xcd = (items * dear + kXcds * cheap - 1) / (kXcds * cheap) + 4;
   return (unsigned)(per_xcd * kXcds);
 }
+
+#define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, SPLITB) \
+  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, SPLITB>
+#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP) \
+  mfma_lds_bytes<BK, NBUF, NBUFW, AP, BP, use_wide_items<(AP > 1), (BP > 1)>()>()
 
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                         int tiles_bound, bool bf16_only, hipStream_t s) {
-  const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(kWaves * 64);
+  const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(512);
   if (L.quant_mode != kQuantNone) {
     if (bf16_only)
-      mfma_group_kernel<kWaves, kBkQ, kBufQ, false, GATEUP, true>
-          <<<grid, block, mfma_lds_bytes<kBkQ, kBufQ, 3>(), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQW, false, GATEUP, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQW, 1, 2), s>>>(L, S, P, T);
     else
-      mfma_group_kernel<kWaves, kBkQ, kBufQ, true, GATEUP, true>
-          <<<grid, block, mfma_lds_bytes<kBkQ, kBufQ, 4>(), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQW, true, GATEUP, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQW, 2, 2), s>>>(L, S, P, T);
   } else if (bf16_only) {
-    mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, GATEUP>
-        <<<grid, block, mfma_lds_bytes<kBkBf16, kBufBf16, 2>(), s>>>(L, S, P, T);
+    UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false)
+        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, 1), s>>>(L, S, P, T);
   } else {
-    mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, GATEUP>
-        <<<grid, block, mfma_lds_bytes<kBkSplit, kBufSplit, 3>(), s>>>(L, S, P, T);
+    UOCR_MFMA_KERNEL(kBkSplit, kBufSplit, kBufSplit, true, GATEUP, false)
+        <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, 1), s>>>(L, S, P, T);
   }
 }
 
@@ -494,22 +593,16 @@ void mfma_init_attributes() {
   auto set = [](const void* k, size_t bytes) {
     (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   };
-  set((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, true>,
-      mfma_lds_bytes<kBkBf16, kBufBf16, 2>());
-  set((const void*)mfma_group_kernel<kWaves, kBkBf16, kBufBf16, false, false>,
-      mfma_lds_bytes<kBkBf16, kBufBf16, 2>());
-  set((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, true>,
-      mfma_lds_bytes<kBkSplit, kBufSplit, 3>());
-  set((const void*)mfma_group_kernel<kWaves, kBkSplit, kBufSplit, true, false>,
-      mfma_lds_bytes<kBkSplit, kBufSplit, 3>());
-  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, false, true, true>,
-      mfma_lds_bytes<kBkQ, kBufQ, 3>());
-  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, false, false, true>,
-      mfma_lds_bytes<kBkQ, kBufQ, 3>());
-  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, true, true, true>,
-      mfma_lds_bytes<kBkQ, kBufQ, 4>());
-  set((const void*)mfma_group_kernel<kWaves, kBkQ, kBufQ, true, false, true>,
-      mfma_lds_bytes<kBkQ, kBufQ, 4>());
+#define UOCR_MFMA_ATTR(BK, NBUF, NBUFW, SPLIT, SPLITB, AP, BP)                              \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, true, SPLITB),                \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP));                                            \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, false, SPLITB),               \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP));
+  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, 1)
+  UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2, 1)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQW, false, true, 1, 2)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQW, true, true, 2, 2)
+#undef UOCR_MFMA_ATTR
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
 

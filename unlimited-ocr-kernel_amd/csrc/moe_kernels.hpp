@@ -81,10 +81,13 @@ void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, in
                              int* chunk_counts, int* err, hipStream_t s);
 
 // dispatch.hip
+// narrow > 0 moves each expert's last tile of at most `narrow` rows into a
+// second routed list (counters[2] = tiles of the first list).
 void launch_dispatch_chunked(const int* ids, const float* w, int T, int E, int K, int bm,
-                             const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
+                             int narrow, const int* chunk_counts, int* offsets, int* perm_rows, float* perm_w,
                              int* inv_pos, int* tiles, int* counters, hipStream_t s);
-void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int* offsets,
+void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm, int narrow,
+                     int* offsets,
                      int* perm_rows, float* perm_w, int* inv_pos, int* tiles, int* counters,
                      hipStream_t s);
 
