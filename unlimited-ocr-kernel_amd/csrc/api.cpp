@@ -326,16 +326,13 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
   if (engine == Engine::Decode) {
-    // One token: three launches with no routing launch of their own (the
-    // router rides with the shared gate/up, top-k with the routed gate/up).
-    phase_begin(ctx, kRouter);
+    // One token: two launches with no routing launch of their own (every
+    // routed gate/up workgroup computes the router logits and routes).
+    phase_begin(ctx, kGateUp);
     uocr::launch_decode_stage(1, L, S, residual, y, st);
     phase_end(ctx);
-    phase_begin(ctx, kGateUp);
-    uocr::launch_decode_stage(2, L, S, residual, y, st);
-    phase_end(ctx);
     phase_begin(ctx, kDown);
-    uocr::launch_decode_stage(3, L, S, residual, y, st);
+    uocr::launch_decode_stage(2, L, S, residual, y, st);
     phase_end(ctx);
   } else {
     if (T <= (size_t)uocr::kGemvChunk && !mfma) {

@@ -1,11 +1,14 @@
 // One-token (decode) expert engine: bound by the bytes of the active
-// experts' weights. Three launches, and no cross-workgroup synchronisation
-// inside a launch (kernel boundaries order everything):
-//   stage 1  router logits          + shared-expert gate/up  -> h_shared
-//   stage 2  routed gate/up         + shared-expert down     -> y_shared
-//            (every wave routes the token itself from the E logits)
-//   stage 3  routed down of all K experts for an 8-feature block, then the
-//            ordered combine of that block.
+// experts' weights. Two launches, and no cross-workgroup synchronisation
+// inside a launch (the kernel boundary orders them):
+//   gate/up  shared-expert workgroups stream their gate/up rows at once;
+//            routed workgroups first compute all E router logits
+//            themselves (the router is 160 KiB, read from L2 by every
+//            routed workgroup, instead of a launch of its own and a
+//            dependent read of its output), route the token in LDS, and
+//            stream the gate/up rows of the expert of their slot
+//   down     routed down of all K experts and the shared-expert down for an
+//            8-feature block, then the ordered combine of that block.
 // Weights are read with range-checked buffer loads (out-of-range chunks
 // read as zero without a memory access), all issued before the first use,
 // and before the activation row is staged into LDS.
@@ -60,78 +63,85 @@ __device__ __forceinline__ const void* w2_of(const DeviceLayer& L, int g) {
                        : (const void*)(L.q2 + L.w2_offset(g));
 }
 
-// Stage 1. Workgroups [0, nr): router rows 8b .. 8b+7 (BF16 router, FP32
-// x). Workgroups [nr, nr + S/4): shared-expert hidden values 4b' .. 4b'+3,
-// h = silu(gate) * up, into gu[K*I ..].
+constexpr int kUpWaves = 8;                     // waves per gate/up workgroup
+constexpr int kHidPerWg = kUpWaves * 4;         // hidden values per gate/up workgroup
+
+struct GateUpSmem {
+  float xl[kWide];
+  int8_t xq[kWide];
+  float xs[kWide / kQBlock];
+  float logits[64];
+  unsigned long long mask;
+  RouteSmem rs;
+};
+
+// Stages the activation row (wave 0) into LDS, quantised per 32-block for
+// W8A8; the caller's loads stay in flight meanwhile.
 template <int KIND, int KH>
-__global__ __launch_bounds__(64) void decode_stage1_kernel(DeviceLayer L, Scratch S) {
-  __shared__ __align__(16) RowSmem sm;
-  const int lane = threadIdx.x;
-  const int q = lane >> 4;
-  const int nr = (L.E + 7) / 8;
-  const int b = blockIdx.x;
-  if (b < nr) {
-    RowPair<kBF16, KH> P;
-    const int ra = 8 * b + q, rb = ra + 4;
-    issue_rows(P, L.router, nullptr, L.E, L.H, ra, rb);
+__device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
+                                        int wave, int lane) {
+  if (wave == 0) {
     RowStage<KH> X;
     load_row(X, S.xn, L.H, lane);
     store_row(X, sm.xl, L.H, lane);
-    __syncthreads();
-    float r0, r1;
-    dot_rows(P, L.H, sm.xl, nullptr, nullptr, r0, r1);
-    if ((lane & 15) == 0) {
-      if (ra < L.E) S.logits[ra] = r0;
-      if (rb < L.E) S.logits[rb] = r1;
-    }
-    return;
   }
-  const int k = 4 * (b - nr) + q;  // shared hidden index (< S by the grid)
-  const int ra = gate_row(k);
-  RowPair<KIND, KH> P;
-  issue_rows(P, w13_of<KIND>(L, L.E), s13_of<KIND>(L, L.E), 2 * L.S, L.H, ra, ra + 32);
-  RowStage<KH> X;
-  load_row(X, S.xn, L.H, lane);
-  store_row(X, sm.xl, L.H, lane);
   __syncthreads();
   if constexpr (KIND == kW8A8) {
-    quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
+    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
     __syncthreads();
   }
-  float r0, r1;
-  dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
-  if ((lane & 15) == 0) S.gu[(size_t)L.K * L.I + k] = silu(r0) * r1;
 }
 
-// Stage 2. Workgroups [0, K * I/4): routed hidden values 4b' .. 4b'+3 of
-// the expert in ascending slot b / (I/4), into gu[slot * I ..]. Workgroups
-// after that: shared-expert down rows 8b' .. 8b'+7 -> ys. Workgroup 0 also
-// writes the routing and the one-token dispatch (ids, weights, offsets,
-// permutation, row tiles).
+// Gate/up. Workgroups [0, S/32): shared-expert hidden values 32b .. 32b+31
+// (4 per wave: its 4 gate rows and the 4 matching up rows), h =
+// silu(gate) * up into gu[K*I ..]. Workgroups after that: routed slot
+// s = b' / (I/32), hidden values 32 (b' % (I/32)) .., into gu[s * I ..];
+// the first routed workgroup also writes the logits, the routing and the
+// one-token dispatch (ids, weights, offsets, permutation, row tiles).
 template <int KIND, int KH>
-__global__ __launch_bounds__(64) void decode_stage2_kernel(DeviceLayer L, Scratch S) {
-  __shared__ __align__(16) RowSmem sm;
-  __shared__ __align__(16) RouteSmem rs;
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLayer L, Scratch S) {
+  __shared__ __align__(16) GateUpSmem sm;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
-  const int per_expert = L.I / 4;
-  const int nrouted = L.K * per_expert;
+  const int n_shared = L.S / kHidPerWg;
+  const int per_expert = L.I / kHidPerWg;
   const int b = blockIdx.x;
-  if (b < nrouted) {
-    // The logit load goes first: routing waits for it alone, while the
-    // activation row is still in flight.
-    const float logit = lane < L.E ? S.logits[lane] : 0.0f;
-    RowStage<KH> X;
-    load_row(X, S.xn, L.H, lane);
-    const LdsRoute r = route_lds(logit, L.E, L.K, rs);
-    const int slot = b / per_expert;
-    const int g = clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(r.mask, slot)), L.E);
-    const int k = 4 * (b - slot * per_expert) + q;
+  if (b < n_shared) {
+    const int k = b * kHidPerWg + 4 * wave + q;
     const int ra = gate_row(k);
     RowPair<KIND, KH> P;
-    issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
-    if (b == 0) {
-      const float w = route_lds_weight(r, L.K, L.normalize, L.scale, rs);
+    issue_rows(P, w13_of<KIND>(L, L.E), s13_of<KIND>(L, L.E), 2 * L.S, L.H, ra, ra + 32);
+    stage_x<KIND, KH>(L, S, sm, wave, lane);
+    float r0, r1;
+    dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
+    if ((lane & 15) == 0) S.gu[(size_t)L.K * L.I + k] = silu(r0) * r1;
+    return;
+  }
+  const int rb = b - n_shared;
+  const int slot = rb / per_expert;
+  // Router rows 8 wave + q and 8 wave + q + 4 (BF16 router, FP32 x; rows
+  // past E read as zero), then the logits into LDS.
+  {
+    RowPair<kBF16, KH> R;
+    issue_rows(R, L.router, nullptr, L.E, L.H, 8 * wave + q, 8 * wave + q + 4);
+    stage_x<KIND, KH>(L, S, sm, wave, lane);
+    float r0, r1;
+    dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
+    if ((lane & 15) == 0) {
+      sm.logits[8 * wave + q] = r0;
+      sm.logits[8 * wave + q + 4] = r1;
+    }
+  }
+  __syncthreads();
+  // Wave 0 routes the token and publishes the selection; the first routed
+  // workgroup's wave 0 also writes the logits, the routing and the
+  // one-token dispatch (ids, weights, offsets, permutation, row tiles).
+  if (wave == 0) {
+    const LdsRoute r = route_wave_lds(sm.logits[lane], L.E, L.K, sm.rs);
+    if (lane == 0) sm.mask = r.mask;
+    if (rb == 0) {
+      const float w = route_wave_weight(r, L.K, L.normalize, L.scale, sm.rs);
       if (!r.ok && lane == 0) raise_error(S.err, kErrNumerical);
       const unsigned long long below_mask = r.mask & ((1ull << lane) - 1ull);
       const int asc = __popcll(below_mask);  // ascending slot / selected ids below lane
@@ -144,93 +154,84 @@ __global__ __launch_bounds__(64) void decode_stage2_kernel(DeviceLayer L, Scratc
         S.tiles[2 * asc] = lane;
         S.tiles[2 * asc + 1] = 0;
       }
-      if (lane < L.E) S.offsets[lane] = asc;
+      if (lane < L.E) {
+        S.offsets[lane] = asc;
+        S.logits[lane] = sm.logits[lane];
+      }
       if (lane == 0) {
         S.offsets[L.E] = L.K;
         S.tiles[2 * L.K] = L.E;
         S.tiles[2 * L.K + 1] = 0;
         S.counters[0] = L.K + 1;
         S.counters[1] = L.K;
+        S.counters[2] = L.K;
       }
     }
-    store_row(X, sm.xl, L.H, lane);
-    __syncthreads();
-    if constexpr (KIND == kW8A8) {
-      quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
-      __syncthreads();
-    }
-    float r0, r1;
-    dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
-    if ((lane & 15) == 0) S.gu[(size_t)slot * L.I + k] = silu(r0) * r1;
-    return;
   }
-  const int ra = 8 * (b - nrouted) + q, rb = ra + 4;
-  RowPair<KIND, kWide> P;
-  issue_rows(P, w2_of<KIND>(L, L.E), s2_of<KIND>(L, L.E), L.H, L.S, ra, rb);
-  RowStage<kWide> Hs;
-  load_row(Hs, S.gu + (size_t)L.K * L.I, L.S, lane);
-  store_row(Hs, sm.xl, L.S, lane);
   __syncthreads();
-  if constexpr (KIND == kW8A8) {
-    quantize_lds(sm.xl, L.S, sm.xq, sm.xs, lane, S.err);
-    __syncthreads();
-  }
+  const int g = clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, slot)), L.E);
+  const int k = kHidPerWg * (rb - slot * per_expert) + 4 * wave + q;
+  const int ra = gate_row(k);
+  RowPair<KIND, KH> P;
+  issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
   float r0, r1;
-  dot_rows(P, L.S, sm.xl, sm.xq, sm.xs, r0, r1);
-  if ((lane & 15) == 0) {
-    if (ra < L.H) S.ys[ra] = r0;
-    if (rb < L.H) S.ys[rb] = r1;
-  }
+  dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
+  if ((lane & 15) == 0) S.gu[(size_t)slot * L.I + k] = silu(r0) * r1;
 }
 
-struct Stage3Smem {
-  float hl[kMaxK][kNarrow];
-  int8_t hq[kMaxK][kNarrow];
-  float hs[kMaxK][kNarrow / kQBlock];
-  float yl[kMaxK][8];
+struct DownSmem {
+  float hl[kMaxK + 2][kNarrow];
+  int8_t hq[kMaxK + 2][kNarrow];
+  float hs[kMaxK + 2][kNarrow / kQBlock];
+  float yl[kMaxK + 2][8];
 };
 
-// Stage 3: one workgroup per 8 output features, wave w = routed expert in
-// ascending slot w, then the ordered combine of the 8 features:
-// out = (residual +) (ys + p_0 y_0 + p_1 y_1 + ...), mul then add.
+// Down: one workgroup per 8 output features; wave w < K = routed expert in
+// ascending slot w, waves K and K+1 = the two halves of the shared expert's
+// reduction (S/2 columns each); then the ordered combine of the 8 features:
+// out = (residual +) ((y_s0 + y_s1) + p_0 y_0 + p_1 y_1 + ...), mul then add.
 template <int KIND>
-__global__ __launch_bounds__(64 * kMaxK) void decode_stage3_kernel(DeviceLayer L, Scratch S,
-                                                                   const float* residual,
-                                                                   float* out) {
-  __shared__ __align__(16) Stage3Smem sm;
+__global__ __launch_bounds__(64 * (kMaxK + 2)) void decode_down_kernel(DeviceLayer L, Scratch S,
+                                                                       const float* residual,
+                                                                       float* out) {
+  __shared__ __align__(16) DownSmem sm;
   // Wave-uniform (scalar) so the per-wave buffer bases stay scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int f0 = 8 * blockIdx.x;
-  // Hidden row first, then the expert id (scalar load) and its weights;
-  // the combine inputs are loaded now and used last.
+  const bool routed = wave < L.K;
+  const int half = L.S / 2;
+  // This wave's hidden row: an expert's I values, or half the shared S.
+  const int n = routed ? L.I : half;
+  const float* hrow = routed ? S.gu + (size_t)wave * L.I
+                             : S.gu + (size_t)L.K * L.I + (size_t)(wave - L.K) * half;
   RowStage<kNarrow> Hr;
-  load_row(Hr, S.gu + (size_t)wave * L.I, L.I, lane);
-  const int g = clamp_group(__builtin_amdgcn_readfirstlane(S.tiles[2 * wave]), L.E);
-  const int ra = f0 + q, rb = ra + 4;
+  load_row(Hr, hrow, n, lane);
+  const int g = routed ? clamp_group(__builtin_amdgcn_readfirstlane(S.tiles[2 * wave]), L.E) : L.E;
   RowPair<KIND, kNarrow> P;
-  issue_rows(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, ra, rb);
-  const float ys_f = S.ys[f0 + (lane & 7)];
-  const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
+  issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.width(g),
+                  routed ? 0 : (wave - L.K) * half, n, f0 + q, f0 + q + 4);
+  // The combine inputs are loaded now and used last.
   float pw[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; j++) pw[j] = j < L.K ? S.perm_w[j] : 0.0f;
-  store_row(Hr, sm.hl[wave], L.I, lane);
+  const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
+  store_row(Hr, sm.hl[wave], n, lane);
   __syncthreads();
   if constexpr (KIND == kW8A8) {
-    quantize_lds(sm.hl[wave], L.I, sm.hq[wave], sm.hs[wave], lane, S.err);
+    quantize_lds(sm.hl[wave], n, sm.hq[wave], sm.hs[wave], lane, S.err);
     __syncthreads();
   }
   float r0, r1;
-  dot_rows(P, L.I, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1);
+  dot_rows(P, n, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1);
   if ((lane & 15) == 0) {
     sm.yl[wave][q] = r0;
     sm.yl[wave][q + 4] = r1;
   }
   __syncthreads();
   if (wave == 0 && lane < 8) {
-    float acc = ys_f;
+    float acc = sm.yl[L.K][lane] + sm.yl[L.K + 1][lane];
 #pragma unroll
     for (int j = 0; j < kMaxK; j++)
       if (j < L.K) acc = acc + pw[j] * sm.yl[j][lane];
@@ -243,11 +244,10 @@ template <int KIND, int KH>
 void launch_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
                   float* out, hipStream_t s) {
   if (stage == 1)
-    decode_stage1_kernel<KIND, KH><<<dim3((L.E + 7) / 8 + L.S / 4), dim3(64), 0, s>>>(L, S);
-  else if (stage == 2)
-    decode_stage2_kernel<KIND, KH><<<dim3(L.K * (L.I / 4) + L.H / 8), dim3(64), 0, s>>>(L, S);
+    decode_gateup_kernel<KIND, KH>
+        <<<dim3(L.S / kHidPerWg + L.K * (L.I / kHidPerWg)), dim3(64 * kUpWaves), 0, s>>>(L, S);
   else
-    decode_stage3_kernel<KIND><<<dim3(L.H / 8), dim3(64 * L.K), 0, s>>>(L, S, residual, out);
+    decode_down_kernel<KIND><<<dim3(L.H / 8), dim3(64 * (L.K + 2)), 0, s>>>(L, S, residual, out);
 }
 
 template <int KH>
@@ -264,10 +264,13 @@ void launch_kind(int stage, const DeviceLayer& L, const Scratch& S, const float*
 }  // namespace
 
 bool decode_supported(const DeviceLayer& L) {
-  // Stage 1/2 rows reduce over H (<= 2048) and S (<= 2048); stage 3 over
-  // I (<= 1024) with one wave per routed expert; routing is one wave.
+  // Gate/up rows reduce over H (<= 2048), 32 hidden values per workgroup;
+  // the down launch reduces over I (<= 1024, one wave per routed expert) and
+  // the two halves of S (<= 2048, each a whole number of 32-blocks);
+  // routing is one wave over E <= 64 logits.
   return L.H <= kWide && L.S <= kWide && L.I <= kNarrow && L.K >= 1 && L.K <= kMaxK &&
-         L.E <= 64 && L.H % 8 == 0 && L.I % 4 == 0 && L.S % 4 == 0;
+         L.E <= 64 && L.H % 8 == 0 && L.I % kHidPerWg == 0 && L.S % kHidPerWg == 0 &&
+         L.S % 64 == 0;
 }
 
 void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,

@@ -134,9 +134,10 @@ constexpr int kMfmaBM = 256;
 void mfma_init_attributes();
 constexpr int kGemvChunk = 16;
 
-// decode.hip: one-token expert engine, three launches (stage 1: router
-// logits + shared gate/up; stage 2: routed gate/up + shared down; stage 3:
-// routed down + ordered combine into out).
+// decode.hip: one-token expert engine, two launches (stage 1: gate/up of
+// the shared expert and, after routing in every routed workgroup, of the
+// routed experts; stage 2: routed and shared down + ordered combine into
+// out).
 bool decode_supported(const DeviceLayer& L);
 void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
                          float* out, hipStream_t s);

@@ -143,6 +143,73 @@ __device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
   return r;
 }
 
+// Routing of one token by one wave on its own (no workgroup barrier; lane
+// = expert), with as few instructions as the math allows: the maximum and
+// the softmax sum are 16-lane DPP reductions combined over the 4 rows, each
+// lane's rank is the number of larger (probability, -id) keys, read back
+// from the wave's own LDS keys (a wave's LDS operations complete in order;
+// the wave barriers keep the compiler from moving reads above writes). The
+// probabilities are e / sum as ops::softmax computes them; only the order
+// of the 64-term sum differs from the reference's sequential one. Also
+// fills sm.selp with the selected probabilities in rank order for
+// route_wave_weight.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+  return v;
+}
+__device__ inline LdsRoute route_wave_lds(float v, int n, int K, RouteSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  const bool live = lane < n;
+  const bool bad = __ballot(live && (isnan(v) || v == INFINITY)) != 0ull;
+  // Value of lane l (a scalar read).
+  auto at = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+  const float vr = row16_max(live ? v : -INFINITY);
+  const float m = fmaxf(fmaxf(at(vr, 0), at(vr, 16)), fmaxf(at(vr, 32), at(vr, 48)));
+  LdsRoute r;
+  if (bad || !isfinite(m)) {
+    // Distinct ids 0..K-1 with weight 0 keep any dispatch a permutation.
+    r.ok = false;
+    r.rank = lane;
+    r.p = 0.0f;
+    r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
+    return r;
+  }
+  const float ex = live ? expf(v - m) : 0.0f;
+  const float sr = row16_sum(ex);
+  const float sum = (at(sr, 0) + at(sr, 16)) + (at(sr, 32) + at(sr, 48));
+  const float p = ex / sum;
+  const unsigned long long key =
+      live ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane) : 0ull;
+  sm.key[lane] = key;
+  __builtin_amdgcn_wave_barrier();
+  int rank = 0;
+#pragma unroll
+  for (int e = 0; e < 64; e += 2) {
+    const ulonglong2 u = *reinterpret_cast<const ulonglong2*>(&sm.key[e]);
+    rank += (u.x > key ? 1 : 0) + (u.y > key ? 1 : 0);
+  }
+  r.ok = true;
+  r.rank = rank;
+  r.p = p;
+  r.mask = __ballot(live && rank < K);
+  if (live && rank < K) sm.selp[rank] = p;
+  __builtin_amdgcn_wave_barrier();
+  return r;
+}
+
+// route_lds_weight for a route_wave_lds result of the same wave.
+__device__ inline float route_wave_weight(const LdsRoute& r, int K, int normalize, float scale,
+                                          const RouteSmem& sm) {
+  if (!r.ok) return 0.0f;
+  float den = -0.0f;
+  for (int j = 0; j < K; j++) den += sm.selp[j];
+  den = normalize ? den + 1e-20f : 1.0f;
+  return r.p / den * scale;
+}
+
 // Routing weights of the selected lanes (route_lds ranks < K): the
 // renormalisation sums the top-k probabilities in selection order
 // (src/decoder/moe.rs:21-25), then scales (:26-28).

@@ -60,19 +60,23 @@ struct RowPair {
   float sa[kC], sb[kC];
 };
 
-// Issues every load of a RowPair. Rows outside [0, rows) and chunks past K
-// read as zero; `w` / `s` are the matrix and (INT8) its [rows, K/32] scales.
+// Issues every load of a RowPair: columns [c0, c0 + K) of rows ra and rb
+// of a row-major [rows, ld] matrix (c0 a multiple of 32). Rows outside
+// [0, rows) and chunks past K read as zero; `w` / `s` are the matrix and
+// (INT8) its [rows, ld/32] scales.
 template <int KIND, int KMAX>
-__device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w, const float* s,
-                                           int rows, int K, int ra, int rb) {
+__device__ __forceinline__ void issue_rows_cols(RowPair<KIND, KMAX>& P, const void* w,
+                                                const float* s, int rows, int ld, int c0, int K,
+                                                int ra, int rb) {
   using RP = RowPair<KIND, KMAX>;
   constexpr int kBytes = KIND == kBF16 ? 2 : 1;
   const int j = threadIdx.x & (kLpr - 1);
   const int nchunks = K / RP::kElems;
-  const uint32_t row_bytes = (uint32_t)K * kBytes;
+  const uint32_t row_bytes = (uint32_t)ld * kBytes;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)rows * row_bytes);
-  const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes : kOut;
-  const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes : kOut;
+  const uint32_t col = (uint32_t)c0 * kBytes;
+  const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes + col : kOut;
+  const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes + col : kOut;
   if constexpr (KIND == kBF16) {
 #pragma unroll
     for (int m = 0; m < RP::kC; m++) {
@@ -84,10 +88,11 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
   } else {
     // Each chunk's scales are issued with its weights, so chunk m can be
     // used as soon as its four loads are back.
-    const int nblk = K / kQBlock;
+    const int nblk = ld / kQBlock;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)rows * nblk * 4u);
-    const uint32_t sa = ra >= 0 && ra < rows ? (uint32_t)ra * nblk * 4u : kOut;
-    const uint32_t sb = rb >= 0 && rb < rows ? (uint32_t)rb * nblk * 4u : kOut;
+    const uint32_t bcol = (uint32_t)(c0 / kQBlock) * 4u;
+    const uint32_t sa = ra >= 0 && ra < rows ? (uint32_t)ra * nblk * 4u + bcol : kOut;
+    const uint32_t sb = rb >= 0 && rb < rows ? (uint32_t)rb * nblk * 4u + bcol : kOut;
 #pragma unroll
     for (int m = 0; m < RP::kC; m++) {
       const int c = j + kLpr * m;
@@ -99,6 +104,13 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
       P.sb[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sb + bo, 0, 0));
     }
   }
+}
+
+// Rows ra and rb of a row-major [rows, K] matrix with K <= KMAX.
+template <int KIND, int KMAX>
+__device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w, const float* s,
+                                           int rows, int K, int ra, int rb) {
+  issue_rows_cols(P, w, s, rows, K, 0, K, ra, rb);
 }
 
 // Dots both rows with the LDS activation row (xl, or xq/xs for a W8A8
