@@ -257,10 +257,10 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = L.E, K = L.K;
   const bool mine = wave < T;
-  // Waves past T route a neutral row so every wave meets every barrier.
+  // Waves past T route a neutral row (their result is not used).
   const float v = mine && lane < E ? S.logits[(size_t)wave * E + lane] : 0.0f;
-  const LdsRoute r = route_lds(v, E, K, rs[wave]);
-  const float w = route_lds_weight(r, K, L.normalize, L.scale, rs[wave]);
+  const LdsRoute r = route_wave_lds(v, E, K, rs[wave]);
+  const float w = route_wave_weight(r, K, L.normalize, L.scale, rs[wave]);
   if (mine && !r.ok && lane == 0) raise_error(S.err, kErrNumerical);
   if (lane == 0) masks[wave] = mine ? r.mask : 0ull;
   __syncthreads();

@@ -236,8 +236,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     for (int r = 0; r < 4; r++) part[wave][4 * (lane >> 4) + r][ni * 16 + ar] = acc[ni][r];
   __syncthreads();
   // Wave partial sums in wave order (deterministic); each wave then routes
-  // two tokens with the LDS top-k (every wave makes the same calls: they
-  // synchronise the workgroup).
+  // two tokens on its own with the wave top-k.
   for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
     const int tl = wave * (kRouteChunk / kRouteWaves) + j;
     const int t = t0 + tl;
@@ -246,8 +245,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
 #pragma unroll
     for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][lane];
     if (live && lane < E) logits[(size_t)t * E + lane] = v;
-    const LdsRoute r = route_lds(live ? v : 0.0f, E, K, rs[wave]);
-    const float wgt = route_lds_weight(r, K, normalize, scale, rs[wave]);
+    const LdsRoute r = route_wave_lds(live ? v : 0.0f, E, K, rs[wave]);
+    const float wgt = route_wave_weight(r, K, normalize, scale, rs[wave]);
     if (!live) continue;
     if (!r.ok && lane == 0) raise_error(err, kErrNumerical);
     if ((r.mask >> lane) & 1ull) {

@@ -61,7 +61,7 @@ __device__ inline WaveRoute route_wave(float v, int n, int K, int normalize, flo
 
 namespace uocr {
 
-// LDS staging for route_lds (one token per wave).
+// LDS staging for route_wave_lds (one token per wave).
 struct RouteSmem {
   __attribute__((aligned(16))) float v[64];
   __attribute__((aligned(16))) unsigned long long key[64];
@@ -74,74 +74,6 @@ struct LdsRoute {
   float p;                   // this lane's probability
   unsigned long long mask;   // bit e set: expert e selected
 };
-
-// The same routing as route_wave with every reduction done through LDS, for
-// a workgroup of exactly one wave: the maximum and the softmax sum are read
-// back sequentially (expert 0 first, the order of ops::softmax), and each
-// lane's rank is the number of larger (probability, -id) keys. v holds the
-// lane's logit (lanes >= n unused). Every wave of the workgroup must call it
-// (it synchronises the workgroup); each wave passes its own RouteSmem.
-__device__ inline LdsRoute route_lds(float v, int n, int K, RouteSmem& sm) {
-  const int lane = threadIdx.x & 63;
-  // Every pass reads all 64 entries with the loop fully unrolled (reads in
-  // flight together); padding entries are neutral: -inf for the maximum,
-  // +0 for the sum (adding +0 to a positive sum changes nothing), key 0 for
-  // the ranks.
-  sm.v[lane] = lane < n ? v : -INFINITY;
-  __syncthreads();
-  float m = -INFINITY;
-  bool bad = false;
-#pragma unroll
-  for (int e = 0; e < 64; e += 4) {
-    const float4 u = *reinterpret_cast<const float4*>(&sm.v[e]);
-    bad |= isnan(u.x) || u.x == INFINITY || isnan(u.y) || u.y == INFINITY;
-    bad |= isnan(u.z) || u.z == INFINITY || isnan(u.w) || u.w == INFINITY;
-    m = fmaxf(fmaxf(m, u.x), u.y);
-    m = fmaxf(fmaxf(m, u.z), u.w);
-  }
-  // Every wave passes every barrier below whatever its logits: a wave with
-  // non-finite logits computes on neutral values and reports !ok.
-  const bool ok = !bad && isfinite(m);
-  const float ex = ok && lane < n ? expf(v - m) : 0.0f;
-  __syncthreads();
-  sm.v[lane] = ok ? ex : 1.0f;
-  __syncthreads();
-  float sum = -0.0f;
-#pragma unroll
-  for (int e = 0; e < 64; e += 4) {
-    const float4 u = *reinterpret_cast<const float4*>(&sm.v[e]);
-    sum += u.x;
-    sum += u.y;
-    sum += u.z;
-    sum += u.w;
-  }
-  const float p = ex / sum;
-  const unsigned long long key =
-      lane < n ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane)
-               : 0ull;
-  sm.key[lane] = key;
-  __syncthreads();
-  int rank = 0;
-#pragma unroll
-  for (int e = 0; e < 64; e += 2) {
-    const ulonglong2 u = *reinterpret_cast<const ulonglong2*>(&sm.key[e]);
-    rank += (u.x > key ? 1 : 0) + (u.y > key ? 1 : 0);
-  }
-  LdsRoute r;
-  if (!ok) {
-    // Distinct ids 0..K-1 with weight 0 keep any dispatch a permutation.
-    r.ok = false;
-    r.rank = lane;
-    r.p = 0.0f;
-    r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
-    return r;
-  }
-  r.ok = true;
-  r.rank = rank;
-  r.p = p;
-  r.mask = __ballot(lane < n && rank < K);
-  return r;
-}
 
 // Routing of one token by one wave on its own (no workgroup barrier; lane
 // = expert), with as few instructions as the math allows: the maximum and
@@ -200,23 +132,11 @@ __device__ inline LdsRoute route_wave_lds(float v, int n, int K, RouteSmem& sm) 
   return r;
 }
 
-// route_lds_weight for a route_wave_lds result of the same wave.
-__device__ inline float route_wave_weight(const LdsRoute& r, int K, int normalize, float scale,
-                                          const RouteSmem& sm) {
-  if (!r.ok) return 0.0f;
-  float den = -0.0f;
-  for (int j = 0; j < K; j++) den += sm.selp[j];
-  den = normalize ? den + 1e-20f : 1.0f;
-  return r.p / den * scale;
-}
-
-// Routing weights of the selected lanes (route_lds ranks < K): the
+// Routing weights of the selected lanes (route_wave_lds ranks < K): the
 // renormalisation sums the top-k probabilities in selection order
 // (src/decoder/moe.rs:21-25), then scales (:26-28).
-__device__ inline float route_lds_weight(const LdsRoute& r, int K, int normalize, float scale,
-                                         RouteSmem& sm) {
-  if (r.ok && r.rank < K) sm.selp[r.rank] = r.p;
-  __syncthreads();
+__device__ inline float route_wave_weight(const LdsRoute& r, int K, int normalize, float scale,
+                                          const RouteSmem& sm) {
   if (!r.ok) return 0.0f;
   float den = -0.0f;
   for (int j = 0; j < K; j++) den += sm.selp[j];
