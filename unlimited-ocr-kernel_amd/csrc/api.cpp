@@ -320,7 +320,8 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     return fail(UOCR_ERR_UNSUPPORTED, "small-batch engine needs hidden and shared widths <= 2048");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
   const int bm = mfma ? uocr::kMfmaBM : uocr::kGemvChunk;
-  // The MFMA engine runs an expert's last tile of <= 128 rows as 128 x 512 items.
+  // The MFMA engine may run an expert's last tile of <= 128 rows as 128 x 512
+  // items and one of <= 64 rows as 64 x 1024 items.
   const int narrow = mfma ? uocr::kMfmaBM / 2 : 0;
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)

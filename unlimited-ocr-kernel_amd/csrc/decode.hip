@@ -165,6 +165,7 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
         S.counters[0] = L.K + 1;
         S.counters[1] = L.K;
         S.counters[2] = L.K;
+        S.counters[3] = L.K;
       }
     }
   }

@@ -77,6 +77,14 @@ __device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, uint32_t lds_addr,
                : "memory");
 }
 
+// The same for 4 bytes per lane (lane l's dword lands at M0 + 4 l).
+__device__ __forceinline__ void buffer_load_lds4(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory");
+}
+
 __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   const unsigned long long a = reinterpret_cast<unsigned long long>(base);
   i32x4 r;
@@ -94,24 +102,28 @@ constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // One work item: a TM x TN output tile of group g, rows r0.. of the group,
-// columns n0... Two shapes share the code: 256 x 256 (waves 2 x 4) for
-// groups with more than 128 rows left, and 128 x 512 (waves 1 x 8) for the
-// last tile of a group when at most 128 rows remain — a cold expert then
-// streams its weights in half as many items without computing a mostly
-// empty 256-row tile. Either way a wave owns 128 rows and 64 columns as 4 x 2
-// MFMA tiles, so the fragment reads per wave are the same.
+// columns n0... Three shapes share the code: 256 x 256 (waves 2 x 4) for
+// groups with more than 128 rows left, 128 x 512 (waves 1 x 8) for the last
+// tile of a group when at most 128 rows remain, and 64 x 1024 (waves 1 x 8)
+// when at most 64 remain — a small group then streams its weights in fewer
+// items without computing a mostly empty 256-row tile. A wave owns 128 rows
+// x 64 columns (4 x 2 MFMA tiles) or 64 x 128 (2 x 4): the same number of
+// accumulators and fragment reads per wave.
 //
-// SPLITB: INT8-overlay weights as dequantised bf16 hi + lo planes (a third
-// product term), y always f32.
-template <int TM, int BK, int NBUF, bool SPLIT, bool GATEUP, bool SPLITB>
+// Q8: INT8-overlay weights, streamed as int8 with their block scales and
+// dequantised in registers into bf16 hi + lo fragments (a third product
+// term), y always f32.
+template <int TM, int BK, int NBUF, bool SPLIT, bool GATEUP, bool Q8>
 __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S,
                                           const MfmaPlanes& P, int T, int g, int r0, int n0,
                                           uint16_t* lds) {
   constexpr int WAVES = 8;
-  constexpr int TN = 256 * 256 / TM;      // 256 or 512
-  constexpr int kWm = TM / 128;            // wave rows
+  constexpr int TN = 256 * 256 / TM;      // 256, 512 or 1024
+  constexpr int kMi = TM >= 128 ? 4 : TM / 32;  // 32-row MFMA tiles per wave
+  constexpr int kWr = 32 * kMi;            // rows per wave: 128, or 64
+  constexpr int kWm = TM / kWr;            // wave rows
   constexpr int kWn = WAVES / kWm;         // wave columns
-  constexpr int kWc = TN / kWn;            // 64 columns per wave
+  constexpr int kWc = TN / kWn;            // 64 columns per wave (128 for TM = 64)
   constexpr int kNi = kWc / 32;
   const bool routed = g < L.E;
   const int W = L.width(g);
@@ -134,34 +146,45 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     return base + r0 + r;
   };
 
-  // ---- LDS tiles. A stage holds the A plane(s) ([TM rows][BK]) and the B
-  // plane(s) ([TN rows][BK]), bf16 with no padding: chunk c (8 bf16) of row
-  // r sits at position c ^ swz(r), which spreads the 16-byte fragment reads
-  // of 16 consecutive rows over all LDS banks. Loads arrive as 1 KB wave
-  // segments of kSegRows rows (lane l -> row l / kCpr, position l % kCpr).
-  constexpr int kCpr = BK / 8;                 // 16-byte chunks per row
+  // ---- LDS tiles. A stage holds the A plane(s) ([TM rows][BK] bf16) and
+  // B: BF16 weights as a [TN rows][BK] bf16 plane; INT8 overlays (Q8) as
+  // their int8 rows ([TN][BK] bytes, BK = 32: one scale block) and the f32
+  // block scale of each row. No padding: 16-byte chunk c of a bf16 row r
+  // sits at position c ^ swz(r), which spreads the 16-byte fragment reads
+  // of 16 consecutive rows over all LDS banks (int8 rows: c ^ ((r >> 3) & 1)
+  // over their two chunks). Loads arrive as 1 KB wave segments (lane l ->
+  // row l / chunks-per-row, position l % chunks-per-row).
+  constexpr int kCpr = BK / 8;                 // 16-byte chunks per A row
   constexpr int kSegRows = 64 / kCpr;          // rows per 1 KB segment
+  constexpr int kCprB = Q8 ? BK / 16 : kCpr;   // 16-byte chunks per B row
+  constexpr int kSegRowsB = 64 / kCprB;
+  static_assert(!Q8 || BK == 32, "INT8 stages are one 32-block deep");
   // Segments per wave and plane. When a plane has fewer segments than there
   // are waves (128 rows of 16-deep stages), waves past the last segment load
   // a copy of segment wave % count (the same bytes to the same place), so
   // every wave issues the same number of loads per stage.
-  constexpr int kSegTotA = TM / kSegRows, kSegTotB = TN / kSegRows;
+  constexpr int kSegTotA = TM / kSegRows, kSegTotB = TN / kSegRowsB;
   constexpr int kSegA = kSegTotA >= WAVES ? kSegTotA / WAVES : 1;
   constexpr int kSegB = kSegTotB >= WAVES ? kSegTotB / WAVES : 1;
   static_assert(kSegTotA % WAVES == 0 || WAVES % kSegTotA == 0, "A segments");
-  static_assert(kSegTotB % WAVES == 0, "B segments");
+  static_assert(kSegTotB % WAVES == 0 || WAVES % kSegTotB == 0, "B segments");
   const int segA0 = kSegTotA >= WAVES ? wave * kSegA : wave % kSegTotA;
+  const int segB0 = kSegTotB >= WAVES ? wave * kSegB : wave % kSegTotB;
   constexpr int kRowDiv = 16 / kCpr;
   auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
-  constexpr uint32_t a_plane = (uint32_t)TM * BK * 2, b_plane = (uint32_t)TN * BK * 2;
-  constexpr int kAPlanes = SPLIT ? 2 : 1, kBPlanes = SPLITB ? 2 : 1;
-  constexpr uint32_t stage_bytes = kAPlanes * a_plane + kBPlanes * b_plane;
-  // Plane order in a stage: A hi, B, [A lo], [B lo].
+  auto swzb = [&](int r) { return Q8 ? (r >> 3) & 1 : swz(r); };
+  constexpr uint32_t a_plane = (uint32_t)TM * BK * 2;
+  constexpr uint32_t b_plane = (uint32_t)TN * BK * (Q8 ? 1 : 2);
+  constexpr uint32_t s_plane = Q8 ? (uint32_t)TN * 4 : 0;
+  constexpr int kAPlanes = SPLIT ? 2 : 1;
+  constexpr uint32_t stage_bytes = kAPlanes * a_plane + b_plane + s_plane;
+  // Plane order in a stage: A hi, B, [A lo], [B scales].
   constexpr uint32_t b_at = a_plane, alo_at = a_plane + b_plane,
-                     blo_at = a_plane + b_plane + (SPLIT ? a_plane : 0);
+                     s_at = a_plane + b_plane + (SPLIT ? a_plane : 0);
 
   // Per-lane source offsets of this wave's segments (k = 0).
   const uint32_t row_bytes = (uint32_t)K * 2;
+  const uint32_t row_bytes_b = (uint32_t)K * (Q8 ? 1 : 2);
   uint32_t a_off[kSegA], b_off[kSegB];
 #pragma unroll
   for (int i = 0; i < kSegA; i++) {
@@ -172,9 +195,22 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   }
 #pragma unroll
   for (int i = 0; i < kSegB; i++) {
-    const int r = (wave * kSegB + i) * kSegRows + lane / kCpr;
-    const int c = (lane % kCpr) ^ swz(r);
-    b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes + 16u * c : kDmaOut;
+    const int r = (segB0 + i) * kSegRowsB + lane / kCprB;
+    const int c = (lane % kCprB) ^ swzb(r);
+    b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes_b + 16u * c : kDmaOut;
+  }
+  // Q8 block scales: dword loads of 64 rows each, kSegSW per wave per stage
+  // (when there are fewer 64-row segments than waves, waves past them
+  // repeat segment wave % count).
+  constexpr int kSegS = TN / 64;
+  constexpr int kSegSW = kSegS >= WAVES ? kSegS / WAVES : 1;
+  const int segS = kSegS >= WAVES ? wave * kSegSW : wave % kSegS;
+  const int nblk = K / kQBlock;
+  uint32_t s_off[kSegSW];
+#pragma unroll
+  for (int i = 0; i < kSegSW; i++) {
+    const int r = (segS + i) * 64 + lane;
+    s_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * nblk * 4u : kDmaOut;
   }
   const uint16_t* a_hi_src;
   const uint16_t* a_lo_src;
@@ -188,22 +224,24 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     a_lo_src = routed ? P.h_lo : P.hs_lo;
     a_rows = routed ? (uint32_t)T * L.K : (uint32_t)T;
   }
-  const uint16_t* wmat;
-  const uint16_t* wmat_lo = nullptr;
-  if constexpr (SPLITB) {
-    wmat = GATEUP ? L.dq13 + L.w13_offset(g) : L.dq2 + L.w2_offset(g);
-    wmat_lo = wmat + (GATEUP ? L.n13() : L.n2());
+  // B: BF16 weights, or the INT8 overlay's int8 rows and block scales.
+  const void* wmat;
+  const float* wscale = nullptr;
+  if constexpr (Q8) {
+    wmat = GATEUP ? (const void*)(L.q13 + L.w13_offset(g)) : (const void*)(L.q2 + L.w2_offset(g));
+    wscale = GATEUP ? L.s13 + L.s13_offset(g) : L.s2 + L.s2_offset(g);
   } else {
-    wmat = GATEUP ? L.w13 + L.w13_offset(g) : L.w2 + L.w2_offset(g);
+    wmat = GATEUP ? (const void*)(L.w13 + L.w13_offset(g)) : (const void*)(L.w2 + L.w2_offset(g));
   }
   const i32x4 rs_a = buffer_rsrc(a_hi_src, a_rows * row_bytes);
   const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
-  const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes);
-  const i32x4 rs_bl = buffer_rsrc(SPLITB ? wmat_lo : wmat, (uint32_t)N * row_bytes);
+  const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes_b);
+  const i32x4 rs_s = buffer_rsrc(Q8 ? (const void*)wscale : wmat, Q8 ? (uint32_t)N * nblk * 4u : 0u);
   // LDS byte addresses of this wave's first A and B segments of stage buffer 0.
   const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds);
   const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_base + (uint32_t)segA0 * 1024u);
-  const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_base + b_at + (uint32_t)wave * kSegB * 1024u);
+  const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_base + b_at + (uint32_t)segB0 * 1024u);
+  const uint32_t lds_s = __builtin_amdgcn_readfirstlane(lds_base + s_at + (uint32_t)segS * 256u);
   auto issue = [&](int buf, int k0) {
     const uint32_t st = (uint32_t)buf * stage_bytes;
     const uint32_t kb = (uint32_t)k0 * 2u;
@@ -213,15 +251,18 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
       if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + kb);
     }
 #pragma unroll
-    for (int i = 0; i < kSegB; i++) {
-      buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + kb);
-      if constexpr (SPLITB) buffer_load_lds16(rs_bl, lds_b + st + (blo_at - b_at) + i * 1024u, b_off[i] + kb);
+    for (int i = 0; i < kSegB; i++)
+      buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + (Q8 ? (uint32_t)k0 : kb));
+    if constexpr (Q8) {
+#pragma unroll
+      for (int i = 0; i < kSegSW; i++)
+        buffer_load_lds4(rs_s, lds_s + st + i * 256u, s_off[i] + (uint32_t)(k0 / kQBlock) * 4u);
     }
   };
 
-  floatx16 acc[4][kNi];
+  floatx16 acc[kMi][kNi];
 #pragma unroll
-  for (int mi = 0; mi < 4; mi++)
+  for (int mi = 0; mi < kMi; mi++)
 #pragma unroll
     for (int ni = 0; ni < kNi; ni++)
 #pragma unroll
@@ -247,7 +288,7 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   // vmcnt <= (kDepth - 1) * kLps; the barrier then publishes them to both
   // groups before either reads stage ks + 1.
   constexpr int kDepth = NBUF - 1;
-  constexpr int kLps = kSegA * kAPlanes + kSegB * kBPlanes;
+  constexpr int kLps = kSegA * kAPlanes + kSegB + (Q8 ? kSegSW : 0);
   constexpr int kSub = BK / 16;
   const int grp = wave >> 2;
   for (int i = 0; i < kDepth; i++)
@@ -263,22 +304,53 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     const bool steady = ks + kDepth < nk;
     if (steady) issue((ks + kDepth) % NBUF, (ks + kDepth) * BK);
     const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
-    bf16x8 fa[kSub][4], fl[kSub][SPLIT ? 4 : 1], fb[kSub][kNi], fbl[kSub][SPLITB ? kNi : 1];
+    bf16x8 fa[kSub][kMi], fl[kSub][SPLIT ? kMi : 1], fb[kSub][kNi], fbl[kSub][Q8 ? kNi : 1];
     auto frag = [&](const char* plane, int row, int c) {
       return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
     };
+    float bscale[kNi];
+    if constexpr (Q8) {
+#pragma unroll
+      for (int ni = 0; ni < kNi; ni++)
+        bscale[ni] = *reinterpret_cast<const float*>(cur + s_at + (wn * kWc + ni * 32 + fr) * 4);
+    }
 #pragma unroll
     for (int sub = 0; sub < kSub; sub++) {
       const int c = 2 * sub + fc;
 #pragma unroll
       for (int ni = 0; ni < kNi; ni++) {
-        fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
-        if constexpr (SPLITB) fbl[sub][ni] = frag(cur + blo_at, wn * kWc + ni * 32 + fr, c);
+        if constexpr (Q8) {
+          // Eight int8 weights of row (column) wn*64 + 32 ni + fr, k = 16 sub
+          // + 8 fc ..; w = q * s rounded to f32 as Int8Matrix::linear
+          // dequantises (src/cpu/quantized.rs:119-131), then hi = bf16(w),
+          // lo = bf16(w - hi): the same B operand bits as the FP32 reference
+          // would multiply, to 2^-16 relative.
+          const int row = wn * kWc + ni * 32 + fr;
+          const uint2 raw = *reinterpret_cast<const uint2*>(
+              cur + b_at + row * BK + 16 * (sub ^ swzb(row)) + 8 * fc);
+          uint32_t hp[4], lp[4];
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            const uint32_t word = j < 4 ? raw.x : raw.y;
+            const int s0 = 8 * (j & 3), s1 = s0 + 8;
+            const float w0 = (float)(int8_t)((word >> s0) & 0xffu) * bscale[ni];
+            const float w1 = (float)(int8_t)((word >> s1) & 0xffu) * bscale[ni];
+            const uint32_t h0 = bf16_bits(w0), h1 = bf16_bits(w1);
+            const uint32_t l0 = bf16_bits(w0 - __uint_as_float(h0 << 16));
+            const uint32_t l1 = bf16_bits(w1 - __uint_as_float(h1 << 16));
+            hp[j / 2] = h0 | (h1 << 16);
+            lp[j / 2] = l0 | (l1 << 16);
+          }
+          fb[sub][ni] = as_bf16x8(make_uint4(hp[0], hp[1], hp[2], hp[3]));
+          fbl[sub][ni] = as_bf16x8(make_uint4(lp[0], lp[1], lp[2], lp[3]));
+        } else {
+          fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
+        }
       }
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++) {
-        fa[sub][mi] = frag(cur, wm * 128 + mi * 32 + fr, c);
-        if constexpr (SPLIT) fl[sub][mi] = frag(cur + alo_at, wm * 128 + mi * 32 + fr, c);
+      for (int mi = 0; mi < kMi; mi++) {
+        fa[sub][mi] = frag(cur, wm * kWr + mi * 32 + fr, c);
+        if constexpr (SPLIT) fl[sub][mi] = frag(cur + alo_at, wm * kWr + mi * 32 + fr, c);
       }
     }
     if (steady)
@@ -300,12 +372,12 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
 #pragma unroll
     for (int sub = 0; sub < kSub; sub++)
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++)
+      for (int mi = 0; mi < kMi; mi++)
 #pragma unroll
         for (int ni = 0; ni < kNi; ni++) {
           mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
           if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
-          if constexpr (SPLITB) mma(fa[sub][mi], fbl[sub][ni], acc[mi][ni]);
+          if constexpr (Q8) mma(fa[sub][mi], fbl[sub][ni], acc[mi][ni]);
         }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -328,8 +400,8 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
       if (wcol0 + 64 * bp >= N) break;
       const int col0 = (wcol0 + 64 * bp) / 2 + 4 * fc;  // hidden column of register 0
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++) {
-        const int row = wm * 128 + 32 * mi + fr;
+      for (int mi = 0; mi < kMi; mi++) {
+        const int row = wm * kWr + 32 * mi + fr;
         if (row >= mrows) continue;
         const size_t at0 = (size_t)(base + r0 + row) * W + col0;
 #pragma unroll
@@ -359,17 +431,17 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     float* out = routed ? S.y : S.ys;
     uint16_t* out16 = reinterpret_cast<uint16_t*>(out);
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mi = 0; mi < kMi; mi++)
 #pragma unroll
       for (int ni = 0; ni < kNi; ni++) {
         const int col = wcol0 + ni * 32 + fr;
         if (col >= N) continue;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int row = wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int row = wm * kWr + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           if (row >= mrows) continue;
           const size_t at = (size_t)(base + r0 + row) * L.H + col;
-          if constexpr (SPLIT || SPLITB)
+          if constexpr (SPLIT || Q8)
             out[at] = acc[mi][ni][r];
           else
             out16[at] = bf16_bits(acc[mi][ni][r]);
@@ -380,8 +452,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
 
 // Item costs for the XCD split, in units of one 32-deep k step of a 256 x
 // 256 tile (8) — a 128 x 512 item moves 1.25x the bytes of a square one for
-// the same MFMA work, so it counts 9.
-constexpr int kCostSquare = 8, kCostWide = 9;
+// the same MFMA work, so it counts 9; a 64 x 1024 item (INT8 rows: about
+// the bytes of a square one) counts 8.
+constexpr int kCostSquare = 8, kCostWide = 9, kCostTiny = 8;
 
 // Which variants run the 128 x 512 shape. The FP32-class BF16 engine moves
 // as many bytes per stage in either shape (the A planes are hi + lo), so a
@@ -391,113 +464,147 @@ constexpr int kCostSquare = 8, kCostWide = 9;
 // 12-layer 4096-token stack, square items only are faster there (4.59 vs
 // 4.69 ms) and on the 512-token INT8 layer (0.40 vs 0.43 ms), while the
 // FP32 class gains (7.21 -> 6.91 ms; 1024 tokens 0.32 -> 0.27 ms).
-template <bool SPLIT, bool SPLITB>
-constexpr bool use_wide_items() { return SPLIT && !SPLITB; }
+template <bool SPLIT, bool Q8>
+constexpr bool use_wide_items() { return SPLIT || Q8; }
+// 64 x 1024 items: the INT8 engine only (its stages are 32-deep int8 rows,
+// so three stages of 1024 B rows still fit; a bf16 B plane of 1024 rows
+// leaves room for two).
+template <bool SPLIT, bool Q8>
+constexpr bool use_tiny_items() { return Q8; }
 
 // Groups of one row are skipped when the overlay runs DynamicActivations
 // (the batch engine's W8A8 path owns them). NBUF_W: stage buffers of the
 // 128 x 512 shape.
-template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool SPLITB = false>
+template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8 = false>
 __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
                                                             MfmaPlanes P, int T) {
   extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
-  constexpr bool kWide = use_wide_items<SPLIT, SPLITB>();
+  constexpr bool kWide = use_wide_items<SPLIT, Q8>();
+  constexpr bool kTiny = kWide && use_tiny_items<SPLIT, Q8>();
 
   // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
   // square items (shared expert first, then routed, each in row-tile,
   // column-tile order) are cut into 8 contiguous ranges of equal cost, one
-  // per XCD, and so are the 128 x 512 items; an XCD interleaves its two
-  // ranges. An item costs its K depth times its shape's cost,
-  // so the deeper shared items of the down GEMM do not pile up on one XCD,
-  // neighbouring square items (same expert, same rows) meet in one L2, an
-  // XCD's deeper items start first, and the weight streams of the small
-  // groups (one wide item per 512 columns, little reuse) spread over every
-  // XCD's path to HBM.
+  // per XCD, and so are the small-group items (128 x 512, then 64 x 1024);
+  // an XCD interleaves its two ranges. An item costs its K depth times its
+  // shape's cost, so the deeper shared items of the down GEMM do not pile
+  // up on one XCD, neighbouring square items (same expert, same rows) meet
+  // in one L2, an XCD's deeper items start first, and the weight streams of
+  // the small groups (little reuse) spread over every XCD's path to HBM.
+  // Tile lists (dispatch): routed [0, c2) square, [c2, c3) last tiles of
+  // <= 128 rows, [c3, c1) last tiles of <= 64 rows, then the shared tiles;
+  // a variant without a shape runs those tiles with the next larger one.
   const int all_tiles = S.counters[0];
   const int routed_tiles = S.counters[1];
   const int square_tiles = kWide ? S.counters[2] : routed_tiles;
+  const int wide_end = kTiny ? S.counters[3] : routed_tiles;
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
   const int nt_routed = (n_routed + kTileN - 1) / kTileN;
   const int nt_wide = (n_routed + 2 * kTileN - 1) / (2 * kTileN);
+  const int nt_tiny = (n_routed + 4 * kTileN - 1) / (4 * kTileN);
   const int nt_shared = (n_shared + kTileN - 1) / kTileN;
   const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
   const long long square_items = (long long)square_tiles * nt_routed;
-  const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
+  const long long wide_items = (long long)(wide_end - square_tiles) * nt_wide;
+  const long long tiny_items = (long long)(routed_tiles - wide_end) * nt_tiny;
   const long long c_shared = (GATEUP ? L.H : L.S) * kCostSquare;
   const long long c_square = (GATEUP ? L.H : L.I) * kCostSquare;
   const long long c_wide = (GATEUP ? L.H : L.I) * kCostWide;
+  const long long c_tiny = (GATEUP ? L.H : L.I) * kCostTiny;
   const long long cost1 = shared_items * c_shared;
   const long long cost_sq = cost1 + square_items * c_square;
   const long long cost_wd = wide_items * c_wide;
+  const long long cost_sm = cost_wd + tiny_items * c_tiny;
   // First square item of XCD x: the first whose cost prefix reaches x / 8 of
-  // the square cost; likewise the first wide item.
+  // the square cost; likewise the first small-group item.
   auto first_sq = [&](int x) -> long long {
     const long long b = cost_sq * x / kXcds;
     if (b <= cost1) return (b + c_shared - 1) / c_shared;
     return shared_items + (b - cost1 + c_square - 1) / c_square;
   };
-  auto first_wd = [&](int x) -> long long { return (cost_wd * x / kXcds + c_wide - 1) / c_wide; };
+  auto first_sm = [&](int x) -> long long {
+    const long long b = cost_sm * x / kXcds;
+    if (b <= cost_wd) return (b + c_wide - 1) / c_wide;
+    return wide_items + (b - cost_wd + c_tiny - 1) / c_tiny;
+  };
   const int xcd = blockIdx.x % kXcds;
   const long long j = blockIdx.x / kXcds;
   const long long sq0 = first_sq(xcd), n_sq = first_sq(xcd + 1) - sq0;
-  const long long wd0 = first_wd(xcd), n_wd = first_wd(xcd + 1) - wd0;
-  const long long n_xcd = n_sq + n_wd;
+  const long long sm0 = first_sm(xcd), n_sm = first_sm(xcd + 1) - sm0;
+  const long long n_xcd = n_sq + n_sm;
   if (j >= n_xcd) return;
-  // The XCD's j-th workgroup: its wide items are spread evenly between its
-  // square ones (local slot j is wide when floor(j n_wd / n) steps), so the
-  // HBM-bound weight streams of small groups run alongside the L2-resident
-  // square work instead of all at once.
-  const long long wd_before = j * n_wd / n_xcd;
-  const bool take_wide = (j + 1) * n_wd / n_xcd > wd_before;
-  const long long item = take_wide ? shared_items + square_items + wd0 + wd_before
-                                   : sq0 + (j - wd_before);
-  int tile, ntile;
-  bool wide = false;
-  if (item < shared_items) {
-    tile = routed_tiles + (int)(item / nt_shared);
-    ntile = (int)(item % nt_shared);
-  } else if (item < shared_items + square_items) {
-    const long long i = item - shared_items;
-    tile = (int)(i / nt_routed);
-    ntile = (int)(i % nt_routed);
+  // The XCD's j-th workgroup: its small-group items are spread evenly
+  // between its square ones (local slot j is small when floor(j n_sm / n)
+  // steps), so the HBM-bound weight streams of small groups run alongside
+  // the L2-resident square work instead of all at once.
+  const long long sm_before = j * n_sm / n_xcd;
+  const bool take_small = (j + 1) * n_sm / n_xcd > sm_before;
+  int tile, ntile, shape = 0;  // 0: 256 x 256, 1: 128 x 512, 2: 64 x 1024
+  if (take_small) {
+    const long long i = sm0 + sm_before;
+    if (i < wide_items) {
+      tile = square_tiles + (int)(i / nt_wide);
+      ntile = (int)(i % nt_wide);
+      shape = 1;
+    } else {
+      tile = wide_end + (int)((i - wide_items) / nt_tiny);
+      ntile = (int)((i - wide_items) % nt_tiny);
+      shape = 2;
+    }
   } else {
-    const long long i = item - shared_items - square_items;
-    tile = square_tiles + (int)(i / nt_wide);
-    ntile = (int)(i % nt_wide);
-    wide = true;
+    const long long item = sq0 + (j - sm_before);
+    if (item < shared_items) {
+      tile = routed_tiles + (int)(item / nt_shared);
+      ntile = (int)(item % nt_shared);
+    } else {
+      const long long i = item - shared_items;
+      tile = (int)(i / nt_routed);
+      ntile = (int)(i % nt_routed);
+    }
   }
   const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
-  if (SPLITB && g < L.E && L.quant_mode == kQuantDynamic &&
+  if (Q8 && g < L.E && L.quant_mode == kQuantDynamic &&
       S.offsets[g + 1] - S.offsets[g] == 1)
     return;
-  if constexpr (kWide) {
-    if (wide) {
-      mfma_item<128, BK, NBUF_W, SPLIT, GATEUP, SPLITB>(L, S, P, T, g, r0, ntile * 2 * kTileN, lds);
+  if constexpr (kTiny) {
+    if (shape == 2) {
+      mfma_item<64, BK, NBUF_W, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * 4 * kTileN, lds);
       return;
     }
   }
-  mfma_item<256, BK, NBUF, SPLIT, GATEUP, SPLITB>(L, S, P, T, g, r0, ntile * kTileN, lds);
+  if constexpr (kWide) {
+    if (shape == 1) {
+      mfma_item<128, BK, NBUF_W, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * 2 * kTileN, lds);
+      return;
+    }
+  }
+  mfma_item<256, BK, NBUF, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * kTileN, lds);
 }
 
-// Dynamic LDS of one shape: NBUF stages of the A planes (TM rows) and the B
-// planes (256 * 256 / TM rows), BK deep.
-constexpr size_t stage_lds(int TM, int BK, int NBUF, int a_planes, int b_planes) {
-  return (size_t)NBUF * (a_planes * TM + b_planes * (kTileM * kTileN / TM)) * BK * sizeof(uint16_t);
+// Dynamic LDS of one shape: NBUF stages of the A planes (TM rows, bf16) and
+// B (256 * 256 / TM rows: bf16, or int8 plus one f32 scale per row), BK deep.
+constexpr size_t stage_lds(int TM, int BK, int NBUF, int a_planes, bool q8) {
+  const size_t tn = (size_t)kTileM * kTileN / TM;
+  return (size_t)NBUF * ((size_t)a_planes * TM * BK * 2 + (q8 ? tn * BK + tn * 4 : tn * BK * 2));
 }
-template <int BK, int NBUF, int NBUF_W, int AP, int BP, bool WIDE>
+template <int BK, int NBUF, int NBUF_W, int AP, bool Q8, bool WIDE, bool TINY>
 constexpr size_t mfma_lds_bytes() {
-  const size_t sq = stage_lds(256, BK, NBUF, AP, BP);
-  const size_t wd = WIDE ? stage_lds(128, BK, NBUF_W, AP, BP) : 0;
-  return sq > wd ? sq : wd;
+  const size_t sq = stage_lds(256, BK, NBUF, AP, Q8);
+  const size_t wd = WIDE ? stage_lds(128, BK, NBUF_W, AP, Q8) : 0;
+  const size_t ty = TINY ? stage_lds(64, BK, NBUF_W, AP, Q8) : 0;
+  const size_t m = sq > wd ? sq : wd;
+  return m > ty ? m : ty;
 }
 // BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class (hi +
 // lo planes): 32-deep stages, three buffers (144 KiB either shape). INT8
-// overlay (dequantised weight hi + lo planes, and the activation's lo plane
-// in the FP32 class): 16-deep stages, four buffers (96 / 128 KiB). The
-// wide-shape counts apply only where use_wide_items() enables that shape.
+// overlay (int8 rows + scales, 25 / 41 KiB per stage): 32-deep stages (one
+// scale block), four buffers with BF16 activations (100 KiB), three in the
+// FP32 class (123 KiB); three for its 128 x 512 and 64 x 1024 items (up to
+// 132 KiB). The small-shape counts apply only where use_wide_items() /
+// use_tiny_items() enable those shapes.
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 4, kBkSplit = 32, kBufSplit = 3;
-constexpr int kBkQ = 16, kBufQ = 4, kBufQW = 3;
+constexpr int kBkQ = 32, kBufQ = 4, kBufQS = 3;
 
 // INT8 overlay -> bf16 planes of the dequantised weight: w = q * s rounded to
 // f32 as Int8Matrix::linear does (src/cpu/quantized.rs:119-131), then hi =
@@ -554,10 +661,11 @@ static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   return (unsigned)(per_xcd * kXcds);
 }
 
-#define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, SPLITB) \
-  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, SPLITB>
-#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP) \
-  mfma_lds_bytes<BK, NBUF, NBUFW, AP, BP, use_wide_items<(AP > 1), (BP > 1)>()>()
+#define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, Q8) \
+  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, Q8>
+#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8)                      \
+  mfma_lds_bytes<BK, NBUF, NBUFW, AP, Q8, use_wide_items<(AP > 1), Q8>(), \
+                 use_tiny_items<(AP > 1), Q8>()>()
 
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -565,17 +673,17 @@ static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(512);
   if (L.quant_mode != kQuantNone) {
     if (bf16_only)
-      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQW, false, GATEUP, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQW, 1, 2), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQS, false, GATEUP, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQS, 1, true), s>>>(L, S, P, T);
     else
-      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQW, true, GATEUP, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQW, 2, 2), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQS, kBufQS, true, GATEUP, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQS, kBufQS, 2, true), s>>>(L, S, P, T);
   } else if (bf16_only) {
     UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false)
-        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, 1), s>>>(L, S, P, T);
+        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false), s>>>(L, S, P, T);
   } else {
     UOCR_MFMA_KERNEL(kBkSplit, kBufSplit, kBufSplit, true, GATEUP, false)
-        <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, 1), s>>>(L, S, P, T);
+        <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, false), s>>>(L, S, P, T);
   }
 }
 
@@ -593,15 +701,15 @@ void mfma_init_attributes() {
   auto set = [](const void* k, size_t bytes) {
     (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   };
-#define UOCR_MFMA_ATTR(BK, NBUF, NBUFW, SPLIT, SPLITB, AP, BP)                              \
-  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, true, SPLITB),                \
-      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP));                                            \
-  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, false, SPLITB),               \
-      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, BP));
-  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, 1)
-  UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2, 1)
-  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQW, false, true, 1, 2)
-  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQW, true, true, 2, 2)
+#define UOCR_MFMA_ATTR(BK, NBUF, NBUFW, SPLIT, Q8, AP)                                      \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, true, Q8),                    \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8));                                            \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, false, Q8),                   \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8));
+  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1)
+  UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQS, false, true, 1)
+  UOCR_MFMA_ATTR(kBkQ, kBufQS, kBufQS, true, true, 2)
 #undef UOCR_MFMA_ATTR
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
