@@ -275,9 +275,9 @@ int read_and_clear_error(uocr_gpu_ctx* ctx) {
 
 // Engine of a forward: the one-token decode engine, the small-batch engine
 // (row tiles of <= 16 tokens, bandwidth-bound) for T <= 16, the MFMA
-// grouped GEMM for larger batches (INT8 overlays through their dequantised
-// bf16 planes; under DynamicActivations the single-row groups still take
-// the small-batch engine's W8A8 path).
+// grouped GEMM for larger batches (INT8 overlays streamed as int8 rows and
+// dequantised in registers; under DynamicActivations the single-row groups
+// still take the small-batch engine's W8A8 path).
 enum class Engine { Decode, Batch, Mfma };
 
 Engine choose_engine(const uocr_moe_layer* layer, size_t T, uint32_t flags) {
@@ -682,25 +682,8 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     return release(fail(r, r == UOCR_ERR_FORMAT ? "invalid INT8 matrix (byte 128)"
                                                  : "INT8 scales must be finite and nonnegative"));
   }
-  // The MFMA engine's operands: q * s as bf16 hi + lo planes (4 B/weight).
-  void *dq13 = nullptr, *dq2 = nullptr;
-  if ((e = alloc(n13 * 4, &dq13)) != hipSuccess || (e = alloc(n2 * 4, &dq2)) != hipSuccess)
-    return release(hip_fail(e, "INT8 plane allocation"));
-  {
-    uint16_t* h13 = static_cast<uint16_t*>(dq13);
-    uint16_t* h2 = static_cast<uint16_t*>(dq2);
-    const int8_t* cq2 = static_cast<const int8_t*>(q2);
-    const float* cs2 = static_cast<const float*>(s2);
-    uocr::launch_dequant_planes(static_cast<const int8_t*>(q13), static_cast<const float*>(s13),
-                                n13, (int)H, h13, h13 + n13, st);
-    uocr::launch_dequant_planes(cq2, cs2, E * H * I, (int)I, h2, h2 + n2, st);
-    uocr::launch_dequant_planes(cq2 + E * H * I, cs2 + E * H * (I / 32), H * S, (int)S,
-                                h2 + E * H * I, h2 + n2 + E * H * I, st);
-    if ((e = hipGetLastError()) != hipSuccess) return release(hip_fail(e, "INT8 planes"));
-  }
   // Replace any previous overlay.
-  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2, (void*)L.dq13,
-                  (void*)L.dq2}) {
+  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2}) {
     if (!p) continue;
     for (auto it = layer->allocations.begin(); it != layer->allocations.end(); ++it)
       if (*it == p) {
@@ -710,9 +693,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     (void)hipFree(p);
   }
   for (void* p : fresh) layer->allocations.push_back(p);
-  layer->bytes += n13 + n13 / 32 * 4 + n2 + n2 / 32 * 4 + (n13 + n2) * 4;
-  L.dq13 = static_cast<const uint16_t*>(dq13);
-  L.dq2 = static_cast<const uint16_t*>(dq2);
+  layer->bytes += n13 + n13 / 32 * 4 + n2 + n2 / 32 * 4;
   L.q13 = static_cast<const int8_t*>(q13);
   L.s13 = static_cast<const float*>(s13);
   L.q2 = static_cast<const int8_t*>(q2);

@@ -606,38 +606,6 @@ constexpr size_t mfma_lds_bytes() {
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 4, kBkSplit = 32, kBufSplit = 3;
 constexpr int kBkQ = 32, kBufQ = 4, kBufQS = 3;
 
-// INT8 overlay -> bf16 planes of the dequantised weight: w = q * s rounded to
-// f32 as Int8Matrix::linear does (src/cpu/quantized.rs:119-131), then hi =
-// bf16(w) and lo = bf16(w - hi) (|w - hi - lo| <= 2^-16 |w|). Row-major
-// [rows, cols] with scales [rows, cols / 32].
-__global__ void dequant_planes_kernel(const int8_t* __restrict__ q, const float* __restrict__ sc,
-                                      size_t n, int cols, uint16_t* __restrict__ hi,
-                                      uint16_t* __restrict__ lo) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 4) {
-    const char4 v = *reinterpret_cast<const char4*>(q + i);
-    const int8_t qv[4] = {v.x, v.y, v.z, v.w};
-    uint16_t h[4], l[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const size_t e = i + j;
-      const float w = (float)qv[j] * sc[(e / cols) * (cols / 32) + (e % cols) / 32];
-      h[j] = bf16_bits(w);
-      l[j] = bf16_bits(w - __uint_as_float((uint32_t)h[j] << 16));
-    }
-    *reinterpret_cast<uint2*>(hi + i) =
-        make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
-    *reinterpret_cast<uint2*>(lo + i) =
-        make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
-  }
-}
-
-void launch_dequant_planes(const int8_t* q, const float* sc, size_t n, int cols, uint16_t* hi,
-                           uint16_t* lo, hipStream_t s) {
-  if (n == 0) return;
-  hipLaunchKernelGGL(dequant_planes_kernel, dim3(4096), dim3(256), 0, s, q, sc, n, cols, hi, lo);
-}
-
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
   if (n == 0) return;
   const size_t threads = (n + 3) / 4;

@@ -30,10 +30,6 @@ struct DeviceLayer {
   const int8_t* q2;
   const float* s2;
   const float* norm_w;       // [H] post-attention RMSNorm weight (f32)
-  // INT8 overlay dequantised (q * s) as bf16 planes for the MFMA engine:
-  // hi at dq13[0, n13), lo at dq13[n13, 2 n13); likewise dq2.
-  const uint16_t* dq13;
-  const uint16_t* dq2;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
   __host__ __device__ size_t n13() const { return ((size_t)E * 2 * I + 2 * (size_t)S) * H; }
@@ -124,8 +120,6 @@ struct MfmaPlanes {
   uint16_t* hs_lo;
 };
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
-void launch_dequant_planes(const int8_t* q, const float* sc, size_t n, int cols, uint16_t* hi,
-                           uint16_t* lo, hipStream_t s);
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                         int tiles_bound, bool bf16_only, hipStream_t s);
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
