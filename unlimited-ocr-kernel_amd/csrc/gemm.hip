@@ -191,7 +191,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     const int r = (segA0 + i) * kSegRows + lane / kCpr;
     const int c = (lane % kCpr) ^ swz(r);
     const int src_row = a_source(r);
-    a_off[i] = src_row >= 0 ? (uint32_t)src_row * row_bytes + 16u * c : kDmaOut;
+    // x planes are row-major [T, H]; the h planes the gate/up epilogue
+    // writes are k-blocked ([W/32][rows][32]: each stage's rows contiguous).
+    a_off[i] = src_row >= 0 ? (uint32_t)src_row * (GATEUP ? row_bytes : 64u) + 16u * c : kDmaOut;
   }
 #pragma unroll
   for (int i = 0; i < kSegB; i++) {
@@ -245,10 +247,11 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   auto issue = [&](int buf, int k0) {
     const uint32_t st = (uint32_t)buf * stage_bytes;
     const uint32_t kb = (uint32_t)k0 * 2u;
+    const uint32_t ka = GATEUP ? kb : (uint32_t)(k0 / 32) * a_rows * 64u;
 #pragma unroll
     for (int i = 0; i < kSegA; i++) {
-      buffer_load_lds16(rs_a, lds_a + st + i * 1024u, a_off[i] + kb);
-      if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + kb);
+      buffer_load_lds16(rs_a, lds_a + st + i * 1024u, a_off[i] + ka);
+      if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + ka);
     }
 #pragma unroll
     for (int i = 0; i < kSegB; i++)
@@ -403,7 +406,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
       for (int mi = 0; mi < kMi; mi++) {
         const int row = wm * kWr + 32 * mi + fr;
         if (row >= mrows) continue;
-        const size_t at0 = (size_t)(base + r0 + row) * W + col0;
+        // h planes k-blocked: [W/32][rows][32], rows = T*K (routed) or T.
+        const size_t hrows = routed ? (size_t)T * L.K : (size_t)T;
+        const size_t at0 = ((size_t)(col0 / 32) * hrows + (base + r0 + row)) * 32 + col0 % 32;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           uint32_t hb[4], lb[4];
