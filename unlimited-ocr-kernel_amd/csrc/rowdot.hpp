@@ -3,10 +3,12 @@
 // chunk loaded with a range-checked buffer load before any is used.
 //
 // Arithmetic is that of Decoder::projection (src/decoder/mod.rs:99-112):
-// BF16 weights widened exactly; INT8 weight-only as the rounded product
-// w * scale dotted in FP32 (src/cpu/quantized.rs:119-131); W8A8 with the
+// BF16 weights widened exactly; INT8 weight-only as q * x summed over each
+// 16-byte chunk and scaled once by its block scale (the reference rounds
+// w = q * scale first, src/cpu/quantized.rs:119-131); W8A8 with the
 // activation row quantised per 32-block and exact i32 block sums
-// (src/cpu/quantized.rs:155-236). Only the FP32 summation order differs.
+// (src/cpu/quantized.rs:155-236). Only the FP32 summation order (and, for
+// INT8, where the scale is applied) differs.
 #pragma once
 
 #include "common.hpp"
@@ -143,20 +145,25 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
         a1 = fmaf(bf16_hi(vb[i]), xv[2 * i + 1], a1);
       }
     } else if constexpr (DOT == kInt8) {
+      // The chunk lies inside one 32-block, so its scale factors out: the
+      // sixteen int8 * x products accumulate first (exact integers times x,
+      // one conversion per byte), then one multiply-add by the block scale.
+      // The reference rounds each dequantised weight first; the sums agree
+      // to FP32 rounding.
       const float4* xp = reinterpret_cast<const float4*>(xl + c * 16);
+      float pa = 0.0f, pb = 0.0f;
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
         const float4 xv = xp[v4];
         const float x4[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-          // The reference multiplies the dequantised (rounded) weight by x.
-          const float da = (float)(int8_t)((va[v4] >> (8 * b)) & 0xff) * P.sa[m];
-          const float db = (float)(int8_t)((vb[v4] >> (8 * b)) & 0xff) * P.sb[m];
-          a0 = fmaf(da, x4[b], a0);
-          a1 = fmaf(db, x4[b], a1);
+          pa = fmaf((float)(int8_t)((va[v4] >> (8 * b)) & 0xff), x4[b], pa);
+          pb = fmaf((float)(int8_t)((vb[v4] >> (8 * b)) & 0xff), x4[b], pb);
         }
       }
+      a0 = fmaf(pa, P.sa[m], a0);
+      a1 = fmaf(pb, P.sb[m], a1);
     } else {
       const int4 xv = *reinterpret_cast<const int4*>(xq + c * 16);
       int pa = __builtin_amdgcn_sdot4((int)va.x, xv.x, 0, false);
