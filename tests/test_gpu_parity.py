@@ -250,6 +250,20 @@ def test_small_layer(ctx, T, quant):
     check_layer(case, ctx, syn.activations(T, SMALL["hidden"], seed=T))
 
 
+# Expert widths beyond 1024 hold each down row of the small-batch engine as
+# two column halves (single-row W8A8 groups too).
+WIDE = dict(hidden=256, inter=1088, experts=8, shared=1)
+
+
+@pytest.mark.parametrize("T", [1, 3, 16])
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY, orc.QUANT_DYNAMIC])
+def test_wide_experts_small_batch(ctx, T, quant):
+    say(f"wide experts T={T} quant={quant}")
+    case = Case(ctx, WIDE, 2, seed=60 + T, quant=quant)
+    check_layer(case, ctx, syn.activations(T, WIDE["hidden"], seed=70 + T),
+                flags=um.FLAG_FORCE_GEMV)
+
+
 @pytest.fixture(scope="module")
 def full_bf16(ctx):
     return Case(ctx, FULL, 6, seed=0)

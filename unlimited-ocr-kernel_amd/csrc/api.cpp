@@ -316,8 +316,12 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   hipStream_t st = ctx->stream;
   const Engine engine = choose_engine(layer, T, flags);
   const bool mfma = engine == Engine::Mfma;
-  if (!mfma && !uocr::batch_supported(L))
-    return fail(UOCR_ERR_UNSUPPORTED, "small-batch engine needs hidden and shared widths <= 2048");
+  // The small-batch engine also takes the single-row W8A8 groups of the
+  // MFMA engine.
+  if ((!mfma || L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS) && !uocr::batch_supported(L))
+    return fail(UOCR_ERR_UNSUPPORTED,
+                "small-batch engine needs widths <= 2048, expert and shared widths that are "
+                "multiples of 16 and a hidden width that is a multiple of 32");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
   const int bm = mfma ? uocr::kMfmaBM : uocr::kGemvChunk;
   // The MFMA engine may run an expert's last tile of <= 128 rows as 128 x 512

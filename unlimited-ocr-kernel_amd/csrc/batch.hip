@@ -1,15 +1,22 @@
 // Small-batch expert engine: row tiles of up to 16 tokens of one expert
-// group (the shared expert is group E). Every workgroup streams a slice of
-// the group's weight rows once, with all of its loads in flight, and dots it
-// with the tile's activation rows staged in LDS. Used for 2 <= T <= 16 and
-// for INT8 weights at any T (tiles of 16 rows).
+// group (the shared expert is group E). A workgroup takes one slice of one
+// tile's weight rows (a unit), issues every load of the slice at once and
+// dots it with the tile's activation rows staged in LDS. The grid is one
+// unit per workgroup, shared-expert units first (they need nothing from
+// the dispatch), then the slices of each routed tile; workgroups are kept
+// small (36 KiB of LDS, <= 168 VGPRs) so that three of them share a CU and
+// their chains of dependent loads overlap. Used for 2 <= T <= 16, and for
+// the single-row W8A8 groups of INT8 layers at any T.
 //
 // Also the fence-free small-batch router (2 <= T <= 16): logits, then one
 // workgroup that routes every token and builds the dispatch.
 //
 // Arithmetic: Decoder::projection / feed_forward (src/decoder/mod.rs:
-// 99-122) per row; INT8 weight-only as the rounded w * scale in FP32; W8A8
-// only for DynamicActivations groups of a single row (:103-104).
+// 99-122) per row; INT8 weight-only as q * x summed per 16-byte chunk and
+// scaled by the chunk's block scale; W8A8 only for DynamicActivations
+// groups of a single row (:103-104).
+#include <type_traits>
+
 #include "common.hpp"
 #include "moe_kernels.hpp"
 #include "routing.hpp"
@@ -20,29 +27,59 @@ namespace uocr {
 namespace {
 
 constexpr int kTileRows = kGemvChunk;  // tokens per row tile
-constexpr int kDotTok = 8;             // tokens per register batch of the dot
-constexpr int kStage = 15360;        // FP32 activations staged per workgroup (60 KiB)
-constexpr int kWideK = 2048;         // widest reduction dimension (H, S)
-constexpr int kNarrowK = 1024;       // widest routed expert width (I)
+constexpr int kDotTok = 4;             // tokens per register batch of the dot
+constexpr int kStage = 9216;           // FP32 activations staged per workgroup (36 KiB)
+constexpr int kWideK = 2048;           // widest reduction dimension (H, S)
+constexpr int kSegK = 1024;            // widest down-projection segment in registers
 
-struct TileInfo {
-  int g, r0, n, group_rows;
+// Three 256-thread workgroups per CU: at most 168 VGPRs per lane. (Four,
+// at 128, spill in the INT8 and BF16 forms and measured slower.)
+#define UOCR_BATCH_ATTR __attribute__((amdgpu_waves_per_eu(3)))
+
+// Down-projection rows of a group of width W: full rows (32 per unit) up to
+// kSegK, otherwise two column halves of seg_of(W) per row (16 rows per unit).
+__host__ __device__ inline int seg_of(int W) {
+  return W <= kSegK ? W : ((W + 1) / 2 + kQBlock - 1) / kQBlock * kQBlock;
+}
+__host__ __device__ inline int down_units(int H, int W) { return W <= kSegK ? H / 32 : H / 16; }
+
+struct Unit {
+  int g, r0, n, group_rows, slice;
   bool routed;
 };
 
-// singles: only routed groups of a single row (the W8A8 rows the MFMA engine
-// leaves to this engine under DynamicActivations).
-__device__ __forceinline__ bool load_tile(const DeviceLayer& L, const Scratch& S, int T,
-                                          int mchunk, int singles, TileInfo& ti) {
-  const int tile = blockIdx.y;
-  if (tile >= S.counters[0]) return false;
-  ti.g = S.tiles[2 * tile];
-  ti.r0 = S.tiles[2 * tile + 1];
-  ti.routed = ti.g < L.E;
-  ti.group_rows = ti.routed ? S.offsets[ti.g + 1] - S.offsets[ti.g] : T;
-  if (singles && !(ti.routed && ti.group_rows == 1)) return false;
-  ti.n = min(mchunk, ti.group_rows - ti.r0);
-  return ti.n > 0;
+// Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
+// holds rows [ts * mchunk, ...) of the shared group), then ur slices of each
+// routed tile of the dispatch list. singles: only routed groups of a single
+// row (the W8A8 rows the MFMA engine leaves to this engine under
+// DynamicActivations).
+__device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
+                                          int nsh, int us, int ur, int singles, Unit& u) {
+  int b = blockIdx.x;
+  if (b < nsh * us) {
+    const int ts = b / us;
+    u.g = L.E;
+    u.routed = false;
+    u.r0 = ts * mchunk;
+    u.slice = b - ts * us;
+    u.group_rows = T;
+    u.n = min(mchunk, T - u.r0);
+    return u.n > 0;
+  }
+  b -= nsh * us;
+  const int i = b / ur;
+  // Both loads in flight together; i stays inside the list's allocation.
+  const int routed_tiles = S.counters[1];
+  const int g = S.tiles[2 * i], r0 = S.tiles[2 * i + 1];
+  if (i >= routed_tiles) return false;
+  u.g = g;
+  u.r0 = r0;
+  u.routed = true;
+  u.slice = b - i * ur;
+  u.group_rows = S.offsets[g + 1] - S.offsets[g];
+  if (singles && u.group_rows != 1) return false;
+  u.n = min(mchunk, u.group_rows - r0);
+  return u.n > 0;
 }
 
 // Row of w13 holding gate value k (up value k is 32 rows further).
@@ -55,24 +92,25 @@ struct BatchSmem {
   const float* rows[kTileRows];
 };
 
-// Stages activation rows [b0, b0 + nb) of the tile into LDS (row-major,
-// stride K) with every thread; `row_of(t)` gives the source row pointer.
+// Stages activation rows [b0, b0 + nb) of the tile into LDS at stride ld
+// (columns [K, ld) zero) with every thread; `row_of(t)` gives the source
+// row pointer. K and ld are multiples of 4.
 template <typename RowOf>
-__device__ __forceinline__ void stage_tile(BatchSmem& sm, int b0, int nb, int K, RowOf row_of) {
+__device__ __forceinline__ void stage_tile(BatchSmem& sm, int b0, int nb, int K, int ld,
+                                           RowOf row_of) {
   if (threadIdx.x < nb) sm.rows[threadIdx.x] = row_of(b0 + threadIdx.x);
   __syncthreads();
-  const int vec = K / 4;
+  const int vec = ld / 4, kvec = K / 4;
   const int total = nb * vec;
-  constexpr int kPer = 8;
+  constexpr int kPer = 4;
   for (int base = 0; base < total; base += kPer * 256) {
     u32x4 v[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int at = base + threadIdx.x + i * 256;
-      if (at < total) {
-        const int t = at / vec;
-        v[i] = reinterpret_cast<const u32x4*>(sm.rows[t])[at - t * vec];
-      }
+      const int t = at / vec, c = at - t * vec;
+      v[i] = u32x4{0u, 0u, 0u, 0u};
+      if (at < total && c < kvec) v[i] = reinterpret_cast<const u32x4*>(sm.rows[t])[c];
     }
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
@@ -102,107 +140,128 @@ __device__ __forceinline__ const float* s2_of(const DeviceLayer& L, int g) {
   return KIND == kBF16 ? nullptr : L.s2 + L.s2_offset(g);
 }
 
-// Dots the loaded rows with the tile's activations in token batches that fit
-// the LDS budget; emit(t, r0, r1) receives every token's two row sums (in
-// every lane of the row's 16-lane group). A single-row tile of an INT8
-// layer in DynamicActivations mode takes the W8A8 dot instead.
-template <int KIND, int KMAX, typename RowOf, typename Emit>
+// Dots the loaded row segments (K columns each; the b segment from column
+// XB of the staged row) with the tile's activations in token batches that
+// fit the LDS budget; emit(t, r0, r1) receives every token's two segment
+// sums (in every lane of the row's 16-lane group). K valid columns of each
+// activation row are staged at stride ld (zero beyond). A single-row tile
+// of an INT8 layer in DynamicActivations mode takes the W8A8 dot instead.
+template <int KIND, int KMAX, int XB, typename RowOf, typename Emit>
 __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
-                                         const RowPair<KIND, KMAX>& P, int K, const TileInfo& ti,
-                                         RowOf row_of, Emit emit) {
+                                         const RowPair<KIND, KMAX>& P, int K, int xb, int cols,
+                                         int ld, const Unit& u, RowOf row_of, Emit emit) {
   const int lane = threadIdx.x & 63;
+  const int xb_off = XB ? xb : 0;
   if constexpr (KIND == kInt8) {
-    if (L.quant_mode == 2 && ti.group_rows == 1) {
-      stage_tile(sm, 0, 1, K, row_of);
-      if (threadIdx.x < 64) quantize_lds(sm.x, K, sm.xq, sm.xs, lane, S.err);
+    if (L.quant_mode == 2 && u.group_rows == 1) {
+      stage_tile(sm, 0, 1, cols, ld, row_of);
+      // The zero columns quantise to zero blocks, so every block a segment
+      // can reach is defined.
+      if (threadIdx.x < 64) quantize_lds(sm.x, ld, sm.xq, sm.xs, lane, S.err);
       __syncthreads();
       float r0, r1;
-      dot_rows_as<kW8A8>(P, K, sm.x, sm.xq, sm.xs, r0, r1);
+      dot_rows_as<kW8A8>(P, K, sm.x, sm.xq, sm.xs, r0, r1, xb_off);
       emit(0, r0, r1);
       return;
     }
   }
   // Tokens staged per pass (LDS budget), dotted kDotTok at a time; the
   // weight rows stay in registers throughout.
-  const int per = kStage / K < kTileRows ? kStage / K : kTileRows;
-  for (int b0 = 0; b0 < ti.n; b0 += per) {
-    const int nb = min(per, ti.n - b0);
+  const int per = kStage / ld < kTileRows ? kStage / ld : kTileRows;
+  for (int b0 = 0; b0 < u.n; b0 += per) {
+    const int nb = min(per, u.n - b0);
     if (b0 > 0) __syncthreads();  // the previous pass is consumed
-    stage_tile(sm, b0, nb, K, row_of);
+    stage_tile(sm, b0, nb, cols, ld, row_of);
     for (int d0 = 0; d0 < nb; d0 += kDotTok) {
-      const int nd = min(kDotTok, nb - d0);
-      float a0[kDotTok], a1[kDotTok];
+      auto run = [&](auto ntc) {
+        constexpr int NT = decltype(ntc)::value;
+        float a0[NT], a1[NT];
 #pragma unroll
-      for (int t = 0; t < kDotTok; t++) a0[t] = a1[t] = 0.0f;
-      dot_rows_multi(P, K, sm.x + d0 * K, K, nd, a0, a1);
+        for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
+        dot_rows_multi(P, K, sm.x + d0 * ld, xb_off, ld, a0, a1);
 #pragma unroll
-      for (int t = 0; t < kDotTok; t++)
-        if (t < nd) emit(b0 + d0 + t, row16_sum(a0[t]), row16_sum(a1[t]));
+        for (int t = 0; t < NT; t++) emit(b0 + d0 + t, row16_sum(a0[t]), row16_sum(a1[t]));
+      };
+      static_assert(kDotTok == 4, "one case per batch size");
+      switch (min(kDotTok, nb - d0)) {
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
+      }
     }
   }
 }
 
-// Gate/up: blockIdx.y = row tile, blockIdx.x = 16 hidden values (each wave
-// 4 gate rows and the 4 matching up rows). h = silu(gate) * up
-// (Decoder::feed_forward, src/decoder/mod.rs:114-122).
+// Gate/up: a unit is 16 hidden values of one tile (each wave 4 gate rows
+// and the 4 matching up rows). h = silu(gate) * up (Decoder::feed_forward,
+// src/decoder/mod.rs:114-122).
 template <int KIND, int KH>
-__global__ __launch_bounds__(256) void batch_gateup_kernel(DeviceLayer L, Scratch S, int T,
-                                                           int mchunk, int singles) {
+__global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_gateup_kernel(
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
   __shared__ __align__(16) BatchSmem sm;
-  TileInfo ti;
-  if (!load_tile(L, S, T, mchunk, singles, ti)) return;
-  const int W = L.width(ti.g);
-  const int k0 = 16 * blockIdx.x;
-  if (k0 >= W) return;
+  Unit u;
+  if (!load_unit(L, S, T, mchunk, nsh, (L.S + 15) / 16, (L.I + 15) / 16, singles, u)) return;
+  const int W = L.width(u.g);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k = k0 + 4 * wave + (lane >> 4);
+  const int k = 16 * u.slice + 4 * wave + (lane >> 4);
   const int ra = gate_row(k);
   RowPair<KIND, KH> P;
-  issue_rows(P, w13_of<KIND>(L, ti.g), s13_of<KIND>(L, ti.g), 2 * W, L.H, ra, ra + 32);
-  const int base = ti.routed ? S.offsets[ti.g] + ti.r0 : ti.r0;
+  issue_rows(P, w13_of<KIND>(L, u.g), s13_of<KIND>(L, u.g), 2 * W, L.H, ra, ra + 32);
+  const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
   auto row_of = [&](int t) {
-    const int row = ti.routed ? S.perm_rows[base + t] : base + t;
+    const int row = u.routed ? S.perm_rows[base + t] : base + t;
     return S.xn + (size_t)row * L.H;
   };
-  float* hout = ti.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
-  const int ld = ti.routed ? L.I : L.S;
-  tile_dot(L, S, sm, P, L.H, ti, row_of, [&](int t, float g, float u) {
-    if ((lane & 15) == 0) hout[(size_t)t * ld + k] = silu(g) * u;
+  float* hout = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
+  const int ld = u.routed ? L.I : L.S;
+  tile_dot<KIND, KH, 0>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
+    if ((lane & 15) == 0 && k < W) hout[(size_t)t * ld + k] = silu(g) * up;
   });
 }
 
-// Down: blockIdx.y = row tile, blockIdx.x = 32 output features (each wave
-// 8 rows of the down matrix). Writes y (routed, dispatched order) or ys.
-template <int KIND, int KMAX>
+// Down: a unit is 32 output features of one tile (each wave 8 full rows of
+// the down matrix), or, for widths beyond kSegK, 16 output features with
+// each row's two column halves in the lanes' two segments. Writes y
+// (routed, dispatched order) or ys.
+template <int KIND, bool HALVES>
 __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
-                                          const TileInfo& ti) {
-  const int W = L.width(ti.g);
+                                          const Unit& u) {
+  const int W = L.width(u.g);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ra = 32 * blockIdx.x + 8 * wave + (lane >> 4), rb = ra + 4;
-  RowPair<KIND, KMAX> P;
-  issue_rows(P, w2_of<KIND>(L, ti.g), s2_of<KIND>(L, ti.g), L.H, W, ra, rb);
-  const int base = ti.routed ? S.offsets[ti.g] + ti.r0 : ti.r0;
-  const float* hin = ti.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
+  const int seg = seg_of(W);
+  const int ra = HALVES ? 16 * u.slice + 4 * wave + (lane >> 4) : 32 * u.slice + 8 * wave + (lane >> 4);
+  const int rb = HALVES ? ra : ra + 4;
+  RowPair<KIND, kSegK> P;
+  issue_segs(P, w2_of<KIND>(L, u.g), s2_of<KIND>(L, u.g), L.H, W, ra, 0, rb, HALVES ? seg : 0, seg);
+  const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
+  const float* hin = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
   auto row_of = [&](int t) { return hin + (size_t)t * W; };
-  float* yout = ti.routed ? S.y + (size_t)base * L.H : S.ys + (size_t)base * L.H;
-  tile_dot(L, S, sm, P, W, ti, row_of, [&](int t, float y0, float y1) {
+  float* yout = u.routed ? S.y + (size_t)base * L.H : S.ys + (size_t)base * L.H;
+  tile_dot<KIND, kSegK, HALVES ? 1 : 0>(L, S, sm, P, seg, seg, W, HALVES ? 2 * seg : W, u, row_of,
+                                        [&](int t, float y0, float y1) {
     if ((lane & 15) == 0) {
-      if (ra < L.H) yout[(size_t)t * L.H + ra] = y0;
-      if (rb < L.H) yout[(size_t)t * L.H + rb] = y1;
+      if (HALVES) {
+        if (ra < L.H) yout[(size_t)t * L.H + ra] = y0 + y1;
+      } else {
+        if (ra < L.H) yout[(size_t)t * L.H + ra] = y0;
+        if (rb < L.H) yout[(size_t)t * L.H + rb] = y1;
+      }
     }
   });
 }
 
 template <int KIND>
-__global__ __launch_bounds__(256) void batch_down_kernel(DeviceLayer L, Scratch S, int T,
-                                                         int mchunk, int singles) {
+__global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_down_kernel(
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
   __shared__ __align__(16) BatchSmem sm;
-  TileInfo ti;
-  if (!load_tile(L, S, T, mchunk, singles, ti)) return;
-  if (ti.routed && L.I <= kNarrowK)
-    down_body<KIND, kNarrowK>(L, S, sm, ti);
+  Unit u;
+  if (!load_unit(L, S, T, mchunk, nsh, down_units(L.H, L.S), down_units(L.H, L.I), singles, u))
+    return;
+  if (L.width(u.g) <= kSegK)
+    down_body<KIND, false>(L, S, sm, u);
   else
-    down_body<KIND, kWideK>(L, S, sm, ti);
+    down_body<KIND, true>(L, S, sm, u);
 }
 
 // ------------------------------------------------------------- small router
@@ -226,20 +285,26 @@ __global__ __launch_bounds__(64) void small_router_kernel(const float* __restric
   load_row(X, x + (size_t)t0 * L.H, nt * L.H, lane);
   store_row(X, xl, nt * L.H, lane);
   __syncthreads();
-  float a0[kRouterTok], a1[kRouterTok];
+  auto run = [&](auto ntc) {
+    constexpr int NT = decltype(ntc)::value;
+    float a0[NT], a1[NT];
 #pragma unroll
-  for (int t = 0; t < kRouterTok; t++) a0[t] = a1[t] = 0.0f;
-  dot_rows_multi(P, L.H, xl, L.H, nt, a0, a1);
+    for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
+    dot_rows_multi(P, L.H, xl, 0, L.H, a0, a1);
 #pragma unroll
-  for (int t = 0; t < kRouterTok; t++) {
-    if (t < nt) {
+    for (int t = 0; t < NT; t++) {
       const float v0 = row16_sum(a0[t]), v1 = row16_sum(a1[t]);
       if ((lane & 15) == 0) {
         if (ra < L.E) S.logits[(size_t)(t0 + t) * L.E + ra] = v0;
         if (rb < L.E) S.logits[(size_t)(t0 + t) * L.E + rb] = v1;
       }
     }
-  }
+  };
+  static_assert(kRouterTok == 2, "one case per token count");
+  if (nt == 2)
+    run(std::integral_constant<int, 2>{});
+  else
+    run(std::integral_constant<int, 1>{});
 }
 
 // One workgroup of 16 waves: wave t routes token t (moe::route,
@@ -312,20 +377,29 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(
   }
 }
 
+// Routed tiles a dispatch can list: one per active group when every group
+// fits one tile, else the dispatch's own bound.
+int routed_bound(const DeviceLayer& L, int T, int tiles_bound, int mchunk) {
+  return T <= mchunk ? min(L.E, T * L.K) : tiles_bound;
+}
+
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, int singles, hipStream_t s) {
-  const dim3 grid(((singles ? L.I : L.S) + 15) / 16, tiles_bound);
+  const int nsh = singles ? 0 : (T + mchunk - 1) / mchunk;
+  const int units = nsh * ((L.S + 15) / 16) + routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16);
   if (L.H <= 1280)
-    batch_gateup_kernel<KIND, 1280><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
+    batch_gateup_kernel<KIND, 1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
   else
-    batch_gateup_kernel<KIND, kWideK><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
+    batch_gateup_kernel<KIND, kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
 }
 
 }  // namespace
 
 bool batch_supported(const DeviceLayer& L) {
-  return L.H <= kWideK && L.S <= kWideK && L.I % 16 == 0 && L.H % 32 == 0;
+  // Down rows are held as one segment up to kSegK or as two halves.
+  return L.H <= kWideK && L.S <= kWideK && L.I <= kWideK && L.I % 16 == 0 && L.S % 16 == 0 &&
+         L.H % 32 == 0;
 }
 
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
@@ -338,11 +412,13 @@ void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tile
 
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
                        hipStream_t s, bool singles) {
-  const dim3 grid(L.H / 32, tiles_bound);
+  const int nsh = singles ? 0 : (T + mchunk - 1) / mchunk;
+  const int units = nsh * down_units(L.H, L.S) +
+                    routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I);
   if (L.quant_mode == 0)
-    batch_down_kernel<kBF16><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
+    batch_down_kernel<kBF16><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
   else
-    batch_down_kernel<kInt8><<<grid, dim3(256), 0, s>>>(L, S, T, mchunk, singles);
+    batch_down_kernel<kInt8><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
 }
 
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,

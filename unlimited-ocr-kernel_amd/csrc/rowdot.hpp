@@ -62,50 +62,56 @@ struct RowPair {
   float sa[kC], sb[kC];
 };
 
-// Issues every load of a RowPair: columns [c0, c0 + K) of rows ra and rb
-// of a row-major [rows, ld] matrix (c0 a multiple of 32). Rows outside
-// [0, rows) and chunks past K read as zero; `w` / `s` are the matrix and
-// (INT8) its [rows, ld/32] scales.
+// Issues every load of a RowPair: two row segments of a row-major
+// [rows, ld] matrix, columns [ca, ca + K) of row ra and [cb, cb + K) of row
+// rb (ca, cb multiples of 32). Rows outside [0, rows) and chunks past the
+// segment or the row read as zero; `w` / `s` are the matrix and (INT8) its
+// [rows, ld/32] scales.
 template <int KIND, int KMAX>
-__device__ __forceinline__ void issue_rows_cols(RowPair<KIND, KMAX>& P, const void* w,
-                                                const float* s, int rows, int ld, int c0, int K,
-                                                int ra, int rb) {
+__device__ __forceinline__ void issue_segs(RowPair<KIND, KMAX>& P, const void* w, const float* s,
+                                           int rows, int ld, int ra, int ca, int rb, int cb,
+                                           int K) {
   using RP = RowPair<KIND, KMAX>;
   constexpr int kBytes = KIND == kBF16 ? 2 : 1;
   const int j = threadIdx.x & (kLpr - 1);
-  const int nchunks = K / RP::kElems;
+  const int na = min(K, ld - ca) / RP::kElems, nb = min(K, ld - cb) / RP::kElems;
   const uint32_t row_bytes = (uint32_t)ld * kBytes;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)rows * row_bytes);
-  const uint32_t col = (uint32_t)c0 * kBytes;
-  const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes + col : kOut;
-  const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes + col : kOut;
+  const uint32_t oa = ra >= 0 && ra < rows ? (uint32_t)ra * row_bytes + (uint32_t)ca * kBytes : kOut;
+  const uint32_t ob = rb >= 0 && rb < rows ? (uint32_t)rb * row_bytes + (uint32_t)cb * kBytes : kOut;
   if constexpr (KIND == kBF16) {
 #pragma unroll
     for (int m = 0; m < RP::kC; m++) {
       const int c = j + kLpr * m;
-      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
-      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
-      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + (c < na ? (uint32_t)c * 16u : kOut), 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + (c < nb ? (uint32_t)c * 16u : kOut), 0, 0);
     }
   } else {
     // Each chunk's scales are issued with its weights, so chunk m can be
     // used as soon as its four loads are back.
     const int nblk = ld / kQBlock;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)rows * nblk * 4u);
-    const uint32_t bcol = (uint32_t)(c0 / kQBlock) * 4u;
-    const uint32_t sa = ra >= 0 && ra < rows ? (uint32_t)ra * nblk * 4u + bcol : kOut;
-    const uint32_t sb = rb >= 0 && rb < rows ? (uint32_t)rb * nblk * 4u + bcol : kOut;
+    const uint32_t sa = ra >= 0 && ra < rows ? ((uint32_t)ra * nblk + (uint32_t)(ca / kQBlock)) * 4u : kOut;
+    const uint32_t sb = rb >= 0 && rb < rows ? ((uint32_t)rb * nblk + (uint32_t)(cb / kQBlock)) * 4u : kOut;
 #pragma unroll
     for (int m = 0; m < RP::kC; m++) {
       const int c = j + kLpr * m;
-      const uint32_t co = c < nchunks ? (uint32_t)c * 16u : kOut;
-      const uint32_t bo = c < nchunks ? (uint32_t)(c >> 1) * 4u : kOut;
-      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + co, 0, 0);
-      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + co, 0, 0);
-      P.sa[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sa + bo, 0, 0));
-      P.sb[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sr, sb + bo, 0, 0));
+      P.wa[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa + (c < na ? (uint32_t)c * 16u : kOut), 0, 0);
+      P.wb[m] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob + (c < nb ? (uint32_t)c * 16u : kOut), 0, 0);
+      P.sa[m] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(sr, sa + (c < na ? (uint32_t)(c >> 1) * 4u : kOut), 0, 0));
+      P.sb[m] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(sr, sb + (c < nb ? (uint32_t)(c >> 1) * 4u : kOut), 0, 0));
     }
   }
+}
+
+// Columns [c0, c0 + K) of rows ra and rb.
+template <int KIND, int KMAX>
+__device__ __forceinline__ void issue_rows_cols(RowPair<KIND, KMAX>& P, const void* w,
+                                                const float* s, int rows, int ld, int c0, int K,
+                                                int ra, int rb) {
+  issue_segs(P, w, s, rows, ld, ra, c0, rb, c0, K);
 }
 
 // Rows ra and rb of a row-major [rows, K] matrix with K <= KMAX.
@@ -118,11 +124,12 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
 // Dots both rows with the LDS activation row (xl, or xq/xs for a W8A8
 // dot); every lane of a 16-lane group returns that group's two row sums.
 // DOT picks the arithmetic: INT8 chunks serve both the weight-only and the
-// W8A8 dot.
+// W8A8 dot. The b segment reads the row from element xb_off on (a multiple
+// of 32; 0 when both segments cover the same columns).
 template <int DOT, int KIND, int KMAX>
 __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K, const float* xl,
                                             const int8_t* xq, const float* xs, float& r0,
-                                            float& r1) {
+                                            float& r1, int xb_off = 0) {
   using RP = RowPair<KIND, KMAX>;
   static_assert((DOT == kBF16) == (KIND == kBF16), "BF16 dots need BF16 chunks");
   const int j = threadIdx.x & (kLpr - 1);
@@ -135,14 +142,16 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
     const u32x4 va = P.wa[m], vb = P.wb[m];
     if constexpr (DOT == kBF16) {
       const float4* xp = reinterpret_cast<const float4*>(xl + c * 8);
-      const float4 x0 = xp[0], x1 = xp[1];
+      const float4* yp = reinterpret_cast<const float4*>(xl + xb_off + c * 8);
+      const float4 x0 = xp[0], x1 = xp[1], y0 = yp[0], y1 = yp[1];
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         a0 = fmaf(bf16_lo(va[i]), xv[2 * i], a0);
         a0 = fmaf(bf16_hi(va[i]), xv[2 * i + 1], a0);
-        a1 = fmaf(bf16_lo(vb[i]), xv[2 * i], a1);
-        a1 = fmaf(bf16_hi(vb[i]), xv[2 * i + 1], a1);
+        a1 = fmaf(bf16_lo(vb[i]), yv[2 * i], a1);
+        a1 = fmaf(bf16_hi(vb[i]), yv[2 * i + 1], a1);
       }
     } else if constexpr (DOT == kInt8) {
       // The chunk lies inside one 32-block, so its scale factors out: the
@@ -151,36 +160,39 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
       // The reference rounds each dequantised weight first; the sums agree
       // to FP32 rounding.
       const float4* xp = reinterpret_cast<const float4*>(xl + c * 16);
+      const float4* yp = reinterpret_cast<const float4*>(xl + xb_off + c * 16);
       float pa = 0.0f, pb = 0.0f;
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
-        const float4 xv = xp[v4];
+        const float4 xv = xp[v4], yv = yp[v4];
         const float x4[4] = {xv.x, xv.y, xv.z, xv.w};
+        const float y4[4] = {yv.x, yv.y, yv.z, yv.w};
 #pragma unroll
         for (int b = 0; b < 4; b++) {
           pa = fmaf((float)(int8_t)((va[v4] >> (8 * b)) & 0xff), x4[b], pa);
-          pb = fmaf((float)(int8_t)((vb[v4] >> (8 * b)) & 0xff), x4[b], pb);
+          pb = fmaf((float)(int8_t)((vb[v4] >> (8 * b)) & 0xff), y4[b], pb);
         }
       }
       a0 = fmaf(pa, P.sa[m], a0);
       a1 = fmaf(pb, P.sb[m], a1);
     } else {
       const int4 xv = *reinterpret_cast<const int4*>(xq + c * 16);
+      const int4 yv = *reinterpret_cast<const int4*>(xq + xb_off + c * 16);
       int pa = __builtin_amdgcn_sdot4((int)va.x, xv.x, 0, false);
       pa = __builtin_amdgcn_sdot4((int)va.y, xv.y, pa, false);
       pa = __builtin_amdgcn_sdot4((int)va.z, xv.z, pa, false);
       pa = __builtin_amdgcn_sdot4((int)va.w, xv.w, pa, false);
-      int pb = __builtin_amdgcn_sdot4((int)vb.x, xv.x, 0, false);
-      pb = __builtin_amdgcn_sdot4((int)vb.y, xv.y, pb, false);
-      pb = __builtin_amdgcn_sdot4((int)vb.z, xv.z, pb, false);
-      pb = __builtin_amdgcn_sdot4((int)vb.w, xv.w, pb, false);
+      int pb = __builtin_amdgcn_sdot4((int)vb.x, yv.x, 0, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.y, yv.y, pb, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.z, yv.z, pb, false);
+      pb = __builtin_amdgcn_sdot4((int)vb.w, yv.w, pb, false);
       // Chunks 2b and 2b+1 (lanes j, j^1) form block b: exact i32 sum.
       const int ia = pa + __shfl_xor(pa, 1);
       const int ib = pb + __shfl_xor(pb, 1);
       if ((j & 1) == 0) {
         const int b = c >> 1;
         a0 += (float)ia * P.sa[m] * xs[b];
-        a1 += (float)ib * P.sb[m] * xs[b];
+        a1 += (float)ib * P.sb[m] * xs[(xb_off >> 5) + b];
       }
     }
   }
@@ -221,70 +233,69 @@ __device__ __forceinline__ void store_row(const RowStage<N>& R, float* dst, int 
   }
 }
 
-// Dots both rows with n <= NT activation rows held in LDS (row t at
-// xl + t * ld), FP32 (BF16 or INT8 weight-only kinds). a0[t] / a1[t] hold
-// this lane's partial sums; row16_sum() completes them.
+// Dots both rows with NT activation rows held in LDS (row t at xl + t * ld;
+// the b segment from element xb_off of the row, a multiple of 32), FP32
+// (BF16 or INT8 weight-only kinds). a0[t] / a1[t] hold this lane's partial
+// sums; row16_sum() completes them. Each chunk's weights are widened once
+// and dotted with every token (straight-line code: NT is exact). BF16
+// products accumulate in chunk order; INT8 chunks (inside one 32-block) sum
+// q * x per token and apply the block scale once.
 template <int KIND, int KMAX, int NT>
 __device__ __forceinline__ void dot_rows_multi(const RowPair<KIND, KMAX>& P, int K, const float* xl,
-                                               int ld, int n, float (&a0)[NT], float (&a1)[NT]) {
+                                               int xb_off, int ld, float (&a0)[NT],
+                                               float (&a1)[NT]) {
   static_assert(KIND != kW8A8, "W8A8 groups are single-row: dot_rows");
   using RP = RowPair<KIND, KMAX>;
+  constexpr int E = RP::kElems;
   const int j = threadIdx.x & (kLpr - 1);
-  const int nchunks = K / RP::kElems;
+  const int nchunks = K / E;
 #pragma unroll
   for (int m = 0; m < RP::kC; m++) {
     const int c = j + kLpr * m;
     if (c >= nchunks) break;
-    const u32x4 va = P.wa[m], vb = P.wb[m];
-    if constexpr (KIND == kBF16) {
-      float wa[8], wb[8];
+    u32x4 va = P.wa[m], vb = P.wb[m];
+    // Opaque copies keep the widening inside the caller's loops: hoisted
+    // out of them, every chunk's widened weights would be live at once.
+    asm volatile("" : "+v"(va), "+v"(vb));
+    float wa[E], wb[E];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        wa[2 * i] = bf16_lo(va[i]);
-        wa[2 * i + 1] = bf16_hi(va[i]);
-        wb[2 * i] = bf16_lo(vb[i]);
-        wb[2 * i + 1] = bf16_hi(vb[i]);
-      }
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        if (t < n) {
-          const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * 8);
-          const float4 x0 = xp[0], x1 = xp[1];
-          const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-          for (int i = 0; i < 8; i++) {
-            a0[t] = fmaf(wa[i], xv[i], a0[t]);
-            a1[t] = fmaf(wb[i], xv[i], a1[t]);
-          }
-        }
-      }
-    } else {
-      float wa[16], wb[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        // The dequantised weight, rounded once, as the reference stores it.
-        wa[i] = (float)(int8_t)((va[i >> 2] >> (8 * (i & 3))) & 0xff) * P.sa[m];
-        wb[i] = (float)(int8_t)((vb[i >> 2] >> (8 * (i & 3))) & 0xff) * P.sb[m];
-      }
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        if (t < n) {
-          const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * 16);
-#pragma unroll
-          for (int v4 = 0; v4 < 4; v4++) {
-            const float4 xv = xp[v4];
-            const float x4[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-              a0[t] = fmaf(wa[4 * v4 + b], x4[b], a0[t]);
-              a1[t] = fmaf(wb[4 * v4 + b], x4[b], a1[t]);
-            }
-          }
-        }
+    for (int i = 0; i < E; i++) {
+      if constexpr (KIND == kBF16) {
+        wa[i] = (i & 1) ? bf16_hi(va[i >> 1]) : bf16_lo(va[i >> 1]);
+        wb[i] = (i & 1) ? bf16_hi(vb[i >> 1]) : bf16_lo(vb[i >> 1]);
+      } else {
+        wa[i] = (float)(int8_t)((va[i >> 2] >> (8 * (i & 3))) & 0xff);
+        wb[i] = (float)(int8_t)((vb[i >> 2] >> (8 * (i & 3))) & 0xff);
       }
     }
-    // One chunk's dequantised weights live at a time.
-    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * E);
+      const float4* yp = reinterpret_cast<const float4*>(xl + t * ld + xb_off + c * E);
+      float pa = KIND == kBF16 ? a0[t] : 0.0f, pb = KIND == kBF16 ? a1[t] : 0.0f;
+#pragma unroll
+      for (int v4 = 0; v4 < E / 4; v4++) {
+        const float4 xv = xp[v4], yv = yp[v4];
+        pa = fmaf(wa[4 * v4 + 0], xv.x, pa);
+        pa = fmaf(wa[4 * v4 + 1], xv.y, pa);
+        pa = fmaf(wa[4 * v4 + 2], xv.z, pa);
+        pa = fmaf(wa[4 * v4 + 3], xv.w, pa);
+        pb = fmaf(wb[4 * v4 + 0], yv.x, pb);
+        pb = fmaf(wb[4 * v4 + 1], yv.y, pb);
+        pb = fmaf(wb[4 * v4 + 2], yv.z, pb);
+        pb = fmaf(wb[4 * v4 + 3], yv.w, pb);
+      }
+      if constexpr (KIND == kBF16) {
+        a0[t] = pa;
+        a1[t] = pb;
+      } else {
+        a0[t] = fmaf(pa, P.sa[m], a0[t]);
+        a1[t] = fmaf(pb, P.sb[m], a1[t]);
+      }
+      // One token's activations in registers at a time (the other waves
+      // of the SIMD cover the LDS latency).
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
