@@ -4,7 +4,7 @@
 // dots it with the tile's activation rows staged in LDS. The grid is one
 // unit per workgroup, shared-expert units first (they need nothing from
 // the dispatch), then the slices of each routed tile; workgroups are kept
-// small (36 KiB of LDS, <= 168 VGPRs) so that three of them share a CU and
+// small (36 KiB of LDS, <= 128 or 168 VGPRs) so that four or three share a CU and
 // their chains of dependent loads overlap. Used for 2 <= T <= 16, and for
 // the single-row W8A8 groups of INT8 layers at any T.
 //
@@ -31,10 +31,18 @@ constexpr int kDotTok = 4;             // tokens per register batch of the dot
 constexpr int kStage = 9216;           // FP32 activations staged per workgroup (36 KiB)
 constexpr int kWideK = 2048;           // widest reduction dimension (H, S)
 constexpr int kSegK = 1024;            // widest down-projection segment in registers
+// Shared-expert tiles take 8 rows: their units dot every weight with each
+// row, and at 16 rows they were the longest units of a launch.
+constexpr int kSharedRows = 8;
 
-// Three 256-thread workgroups per CU: at most 168 VGPRs per lane. (Four,
-// at 128, spill in the INT8 and BF16 forms and measured slower.)
-#define UOCR_BATCH_ATTR __attribute__((amdgpu_waves_per_eu(3)))
+// Workgroups of 256 threads per CU: four (at most 128 VGPRs per lane) for
+// the gate/up GEMV where INT8 rows of up to 1280 bytes fit, three (168)
+// otherwise. The down GEMV measured faster at three (its staged activation
+// rows are longer and its shared-expert units heavier).
+template <int KIND, int KMAX, bool DYN>
+constexpr int batch_waves() {
+  return !DYN && KIND == kInt8 && KMAX <= 1280 ? 4 : 3;
+}
 
 // Down-projection rows of a group of width W: full rows (32 per unit) up to
 // kSegK, otherwise two column halves of seg_of(W) per row (16 rows per unit).
@@ -49,8 +57,8 @@ struct Unit {
 };
 
 // Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
-// holds rows [ts * mchunk, ...) of the shared group), then ur slices of each
-// routed tile of the dispatch list. singles: only routed groups of a single
+// holds rows [ts * kSharedRows, ...) of the shared group), then ur slices of
+// each routed tile of the dispatch list. singles: only routed groups of a single
 // row (the W8A8 rows the MFMA engine leaves to this engine under
 // DynamicActivations).
 __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
@@ -60,10 +68,10 @@ __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S
     const int ts = b / us;
     u.g = L.E;
     u.routed = false;
-    u.r0 = ts * mchunk;
+    u.r0 = ts * kSharedRows;
     u.slice = b - ts * us;
     u.group_rows = T;
-    u.n = min(mchunk, T - u.r0);
+    u.n = min(kSharedRows, T - u.r0);
     return u.n > 0;
   }
   b -= nsh * us;
@@ -146,14 +154,14 @@ __device__ __forceinline__ const float* s2_of(const DeviceLayer& L, int g) {
 // sums (in every lane of the row's 16-lane group). K valid columns of each
 // activation row are staged at stride ld (zero beyond). A single-row tile
 // of an INT8 layer in DynamicActivations mode takes the W8A8 dot instead.
-template <int KIND, int KMAX, int XB, typename RowOf, typename Emit>
+template <int KIND, int KMAX, int XB, bool DYN, typename RowOf, typename Emit>
 __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                          const RowPair<KIND, KMAX>& P, int K, int xb, int cols,
                                          int ld, const Unit& u, RowOf row_of, Emit emit) {
   const int lane = threadIdx.x & 63;
   const int xb_off = XB ? xb : 0;
-  if constexpr (KIND == kInt8) {
-    if (L.quant_mode == 2 && u.group_rows == 1) {
+  if constexpr (KIND == kInt8 && DYN) {
+    if (u.group_rows == 1) {
       stage_tile(sm, 0, 1, cols, ld, row_of);
       // The zero columns quantise to zero blocks, so every block a segment
       // can reach is defined.
@@ -178,7 +186,7 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
         float a0[NT], a1[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
-        dot_rows_multi(P, K, sm.x + d0 * ld, xb_off, ld, a0, a1);
+        dot_rows_multi<KIND, KMAX, NT, XB != 0>(P, K, sm.x + d0 * ld, xb_off, ld, a0, a1);
 #pragma unroll
         for (int t = 0; t < NT; t++) emit(b0 + d0 + t, row16_sum(a0[t]), row16_sum(a1[t]));
       };
@@ -196,8 +204,9 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
 // Gate/up: a unit is 16 hidden values of one tile (each wave 4 gate rows
 // and the 4 matching up rows). h = silu(gate) * up (Decoder::feed_forward,
 // src/decoder/mod.rs:114-122).
-template <int KIND, int KH>
-__global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_gateup_kernel(
+template <int KIND, int KH, bool DYN>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_gateup_kernel(
     DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
   __shared__ __align__(16) BatchSmem sm;
   Unit u;
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_gateup_kernel(
   };
   float* hout = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
   const int ld = u.routed ? L.I : L.S;
-  tile_dot<KIND, KH, 0>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
+  tile_dot<KIND, KH, 0, DYN>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
     if ((lane & 15) == 0 && k < W) hout[(size_t)t * ld + k] = silu(g) * up;
   });
 }
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_gateup_kernel(
 // the down matrix), or, for widths beyond kSegK, 16 output features with
 // each row's two column halves in the lanes' two segments. Writes y
 // (routed, dispatched order) or ys.
-template <int KIND, bool HALVES>
+template <int KIND, bool HALVES, bool DYN>
 __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                           const Unit& u) {
   const int W = L.width(u.g);
@@ -238,7 +247,7 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   const float* hin = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
   auto row_of = [&](int t) { return hin + (size_t)t * W; };
   float* yout = u.routed ? S.y + (size_t)base * L.H : S.ys + (size_t)base * L.H;
-  tile_dot<KIND, kSegK, HALVES ? 1 : 0>(L, S, sm, P, seg, seg, W, HALVES ? 2 * seg : W, u, row_of,
+  tile_dot<KIND, kSegK, HALVES ? 1 : 0, DYN>(L, S, sm, P, seg, seg, W, HALVES ? 2 * seg : W, u, row_of,
                                         [&](int t, float y0, float y1) {
     if ((lane & 15) == 0) {
       if (HALVES) {
@@ -251,17 +260,18 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   });
 }
 
-template <int KIND>
-__global__ __launch_bounds__(256) UOCR_BATCH_ATTR void batch_down_kernel(
+template <int KIND, bool DYN>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(3))) void batch_down_kernel(
     DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
   __shared__ __align__(16) BatchSmem sm;
   Unit u;
   if (!load_unit(L, S, T, mchunk, nsh, down_units(L.H, L.S), down_units(L.H, L.I), singles, u))
     return;
   if (L.width(u.g) <= kSegK)
-    down_body<KIND, false>(L, S, sm, u);
+    down_body<KIND, false, DYN>(L, S, sm, u);
   else
-    down_body<KIND, true>(L, S, sm, u);
+    down_body<KIND, true, DYN>(L, S, sm, u);
 }
 
 // ------------------------------------------------------------- small router
@@ -386,12 +396,20 @@ int routed_bound(const DeviceLayer& L, int T, int tiles_bound, int mchunk) {
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, int singles, hipStream_t s) {
-  const int nsh = singles ? 0 : (T + mchunk - 1) / mchunk;
+  const int nsh = singles ? 0 : (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * ((L.S + 15) / 16) + routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16);
-  if (L.H <= 1280)
-    batch_gateup_kernel<KIND, 1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
-  else
-    batch_gateup_kernel<KIND, kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
+  const dim3 grid(units), block(256);
+  if (L.quant_mode == kQuantDynamic) {
+    if (L.H <= 1280)
+      batch_gateup_kernel<KIND, 1280, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+    else
+      batch_gateup_kernel<KIND, kWideK, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+  } else {
+    if (L.H <= 1280)
+      batch_gateup_kernel<KIND, 1280, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+    else
+      batch_gateup_kernel<KIND, kWideK, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+  }
 }
 
 }  // namespace
@@ -412,13 +430,16 @@ void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tile
 
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
                        hipStream_t s, bool singles) {
-  const int nsh = singles ? 0 : (T + mchunk - 1) / mchunk;
+  const int nsh = singles ? 0 : (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * down_units(L.H, L.S) +
                     routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I);
+  const dim3 grid(units), block(256);
   if (L.quant_mode == 0)
-    batch_down_kernel<kBF16><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
+    batch_down_kernel<kBF16, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+  else if (L.quant_mode == kQuantDynamic)
+    batch_down_kernel<kInt8, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
   else
-    batch_down_kernel<kInt8><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh, singles);
+    batch_down_kernel<kInt8, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
 }
 
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,

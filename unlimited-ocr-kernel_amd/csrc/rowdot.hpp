@@ -234,13 +234,13 @@ __device__ __forceinline__ void store_row(const RowStage<N>& R, float* dst, int 
 }
 
 // Dots both rows with NT activation rows held in LDS (row t at xl + t * ld;
-// the b segment from element xb_off of the row, a multiple of 32), FP32
+// with SEG_B the b segment from element xb_off of the row), FP32
 // (BF16 or INT8 weight-only kinds). a0[t] / a1[t] hold this lane's partial
 // sums; row16_sum() completes them. Each chunk's weights are widened once
 // and dotted with every token (straight-line code: NT is exact). BF16
 // products accumulate in chunk order; INT8 chunks (inside one 32-block) sum
 // q * x per token and apply the block scale once.
-template <int KIND, int KMAX, int NT>
+template <int KIND, int KMAX, int NT, bool SEG_B = false>
 __device__ __forceinline__ void dot_rows_multi(const RowPair<KIND, KMAX>& P, int K, const float* xl,
                                                int xb_off, int ld, float (&a0)[NT],
                                                float (&a1)[NT]) {
@@ -271,8 +271,9 @@ __device__ __forceinline__ void dot_rows_multi(const RowPair<KIND, KMAX>& P, int
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const float4* xp = reinterpret_cast<const float4*>(xl + t * ld + c * E);
-      const float4* yp = reinterpret_cast<const float4*>(xl + t * ld + xb_off + c * E);
       float pa = KIND == kBF16 ? a0[t] : 0.0f, pb = KIND == kBF16 ? a1[t] : 0.0f;
+      const float4* yp =
+          reinterpret_cast<const float4*>(xl + t * ld + (SEG_B ? xb_off : 0) + c * E);
 #pragma unroll
       for (int v4 = 0; v4 < E / 4; v4++) {
         const float4 xv = xp[v4], yv = yp[v4];
