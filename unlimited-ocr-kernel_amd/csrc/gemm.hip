@@ -463,12 +463,13 @@ constexpr int kCostSquare = 8, kCostWide = 9, kCostTiny = 8;
 
 // Which variants run the 128 x 512 shape. The FP32-class BF16 engine moves
 // as many bytes per stage in either shape (the A planes are hi + lo), so a
-// small group's last tile costs half. With one activation plane the wide
+// small group's last tile costs half (12-layer 4096-token stack 7.21 -> 6.91
+// ms; 1024 tokens 0.32 -> 0.27 ms). With one activation plane the wide
 // stage moves 1.25x the bytes and a small group's items are bound by their
-// weight stream from HBM, which the shape does not shorten: measured on the
-// 12-layer 4096-token stack, square items only are faster there (4.59 vs
-// 4.69 ms) and on the 512-token INT8 layer (0.40 vs 0.43 ms), while the
-// FP32 class gains (7.21 -> 6.91 ms; 1024 tokens 0.32 -> 0.27 ms).
+// weight stream from HBM, which the shape does not shorten: square items
+// only are faster there (4.59 vs 4.69 ms). The INT8 engine streams int8
+// rows (half the bytes of bf16) and dequantises them in registers: with
+// the 128 x 512 and 64 x 1024 shapes its 512-token layer runs in 0.29 ms.
 template <bool SPLIT, bool Q8>
 constexpr bool use_wide_items() { return SPLIT || Q8; }
 // 64 x 1024 items: the INT8 engine only (its stages are 32-deep int8 rows,
