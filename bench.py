@@ -79,7 +79,7 @@ def gate_traffic():
     try:
         with open(path) as f:
             for line in f:
-                if "mfma_group_kernel<32, 4, 4, false, true, false>" in line:
+                if "mfma_group_kernel<32, 4, 3, false, true, false, false, false>" in line:
                     cells = [c.strip().replace(",", "") for c in line.split("|")]
                     return int((float(cells[3]) + float(cells[5])) * 1e6)
     except (OSError, ValueError, IndexError):

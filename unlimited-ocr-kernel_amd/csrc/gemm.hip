@@ -467,11 +467,12 @@ constexpr int kCostSquare = 8, kCostWide = 9, kCostTiny = 8;
 // ms; 1024 tokens 0.32 -> 0.27 ms). With one activation plane the wide
 // stage moves 1.25x the bytes and a small group's items are bound by their
 // weight stream from HBM, which the shape does not shorten: square items
-// only are faster there (4.59 vs 4.69 ms). The INT8 engine streams int8
-// rows (half the bytes of bf16) and dequantises them in registers: with
-// the 128 x 512 and 64 x 1024 shapes its 512-token layer runs in 0.29 ms.
-template <bool SPLIT, bool Q8>
-constexpr bool use_wide_items() { return SPLIT || Q8; }
+// only are faster on the 4096-token stack (4.59 vs 4.69 ms), so BF16
+// activations take the wide shape only up to kWideMaxTokens tokens, where
+// small groups dominate. The INT8 engine streams int8 rows (half the bytes
+// of bf16) and dequantises them in registers: with the 128 x 512 and
+// 64 x 1024 shapes its 512-token layer runs in 0.29 ms.
+constexpr int kWideMaxTokens = 2048;
 // 64 x 1024 items: the INT8 engine only (its stages are 32-deep int8 rows,
 // so three stages of 1024 B rows still fit; a bf16 B plane of 1024 rows
 // leaves room for two).
@@ -481,12 +482,12 @@ constexpr bool use_tiny_items() { return Q8; }
 // Groups of one row are skipped when the overlay runs DynamicActivations
 // (the batch engine's W8A8 path owns them). NBUF_W: stage buffers of the
 // 128 x 512 shape.
-template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8 = false>
+template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8, bool WIDE, bool TINY>
 __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
                                                             MfmaPlanes P, int T) {
   extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
-  constexpr bool kWide = use_wide_items<SPLIT, Q8>();
-  constexpr bool kTiny = kWide && use_tiny_items<SPLIT, Q8>();
+  constexpr bool kWide = WIDE;
+  constexpr bool kTiny = WIDE && TINY;
 
   // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
   // square items (shared expert first, then routed, each in row-tile,
@@ -602,14 +603,14 @@ constexpr size_t mfma_lds_bytes() {
   const size_t m = sq > wd ? sq : wd;
   return m > ty ? m : ty;
 }
-// BF16 activations: 32-deep stages, four buffers (128 KiB). FP32-class (hi +
+// BF16 activations: 32-deep stages, four buffers (128 KiB), three for the
+// 128 x 512 items of its small-batch variant (120 KiB). FP32-class (hi +
 // lo planes): 32-deep stages, three buffers (144 KiB either shape). INT8
 // overlay (int8 rows + scales, 25 / 41 KiB per stage): 32-deep stages (one
 // scale block), four buffers with BF16 activations (100 KiB), three in the
 // FP32 class (123 KiB); three for its 128 x 512 and 64 x 1024 items (up to
-// 132 KiB). The small-shape counts apply only where use_wide_items() /
-// use_tiny_items() enable those shapes.
-constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 4, kBkSplit = 32, kBufSplit = 3;
+// 132 KiB). The small-shape counts apply only to variants with those shapes.
+constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 3, kBkSplit = 32, kBufSplit = 3;
 constexpr int kBkQ = 32, kBufQ = 4, kBufQS = 3;
 
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
@@ -635,11 +636,10 @@ static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   return (unsigned)(per_xcd * kXcds);
 }
 
-#define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, Q8) \
-  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, Q8>
-#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8)                      \
-  mfma_lds_bytes<BK, NBUF, NBUFW, AP, Q8, use_wide_items<(AP > 1), Q8>(), \
-                 use_tiny_items<(AP > 1), Q8>()>()
+#define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, Q8, WIDE) \
+  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, Q8, WIDE, use_tiny_items<SPLIT, Q8>()>
+#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8, WIDE) \
+  mfma_lds_bytes<BK, NBUF, NBUFW, AP, Q8, WIDE, WIDE && use_tiny_items<(AP > 1), Q8>()>()
 
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -647,17 +647,23 @@ static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(512);
   if (L.quant_mode != kQuantNone) {
     if (bf16_only)
-      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQS, false, GATEUP, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQS, 1, true), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQS, false, GATEUP, true, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQS, 1, true, true), s>>>(L, S, P, T);
     else
-      UOCR_MFMA_KERNEL(kBkQ, kBufQS, kBufQS, true, GATEUP, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQS, kBufQS, 2, true), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQS, kBufQS, true, GATEUP, true, true)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQS, kBufQS, 2, true, true), s>>>(L, S, P, T);
+  } else if (bf16_only && T <= kWideMaxTokens) {
+    UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false, true)
+        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false, true), s>>>(L, S,
+                                                                                         P, T);
   } else if (bf16_only) {
-    UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false)
-        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false), s>>>(L, S, P, T);
+    UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false, false)
+        <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false, false), s>>>(L, S,
+                                                                                          P, T);
   } else {
-    UOCR_MFMA_KERNEL(kBkSplit, kBufSplit, kBufSplit, true, GATEUP, false)
-        <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, false), s>>>(L, S, P, T);
+    UOCR_MFMA_KERNEL(kBkSplit, kBufSplit, kBufSplit, true, GATEUP, false, true)
+        <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, false, true), s>>>(L, S,
+                                                                                           P, T);
   }
 }
 
@@ -675,15 +681,16 @@ void mfma_init_attributes() {
   auto set = [](const void* k, size_t bytes) {
     (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   };
-#define UOCR_MFMA_ATTR(BK, NBUF, NBUFW, SPLIT, Q8, AP)                                      \
-  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, true, Q8),                    \
-      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8));                                            \
-  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, false, Q8),                   \
-      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8));
-  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1)
-  UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2)
-  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQS, false, true, 1)
-  UOCR_MFMA_ATTR(kBkQ, kBufQS, kBufQS, true, true, 2)
+#define UOCR_MFMA_ATTR(BK, NBUF, NBUFW, SPLIT, Q8, AP, WIDE)                                \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, true, Q8, WIDE),              \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8, WIDE));                                      \
+  set((const void*)UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, false, Q8, WIDE),             \
+      UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8, WIDE));
+  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, false)
+  UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, true)
+  UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2, true)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQS, false, true, 1, true)
+  UOCR_MFMA_ATTR(kBkQ, kBufQS, kBufQS, true, true, 2, true)
 #undef UOCR_MFMA_ATTR
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }
