@@ -264,6 +264,23 @@ def test_wide_experts_small_batch(ctx, T, quant):
                 flags=um.FLAG_FORCE_GEMV)
 
 
+# Expert widths beyond 2048 exceed the small-batch engine: small batches
+# take the grouped GEMM instead (and forcing the small-batch engine fails).
+WIDER = dict(hidden=256, inter=2112, experts=4, shared=1)
+
+
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY])
+def test_widths_beyond_small_batch(ctx, T, quant):
+    say(f"wider experts T={T} quant={quant}")
+    case = Case(ctx, WIDER, 2, seed=80 + T, quant=quant)
+    x = syn.activations(T, WIDER["hidden"], seed=90 + T)
+    check_layer(case, ctx, x)
+    with pytest.raises(um.UocrError) as e:
+        case.run(ctx, x, flags=um.FLAG_FORCE_GEMV)
+    assert e.value.status == um.UNSUPPORTED
+
+
 @pytest.fixture(scope="module")
 def full_bf16(ctx):
     return Case(ctx, FULL, 6, seed=0)

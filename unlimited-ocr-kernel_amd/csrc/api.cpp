@@ -286,6 +286,9 @@ Engine choose_engine(const uocr_moe_layer* layer, size_t T, uint32_t flags) {
                     (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
   if (mfma) return Engine::Mfma;
   if (T == 1 && uocr::decode_supported(L)) return Engine::Decode;
+  // Shapes beyond the small-batch engine's registers take the grouped GEMM
+  // unless the caller forces the small-batch engine.
+  if (!uocr::batch_supported(L) && !(flags & UOCR_FLAG_FORCE_GEMV)) return Engine::Mfma;
   return Engine::Batch;
 }
 
