@@ -52,25 +52,37 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(
       }
     }
   }
+  // Every load of the row is issued before the first is used (the expert
+  // rows of slots j >= K read slot 0's row again and are not used).
+  const size_t rs = Y16 ? (size_t)H / 2 : (size_t)H;  // row stride in floats
+  float4 sv[kRowChunks], rv[kRowChunks], v[kRowChunks][8];
+#pragma unroll
+  for (int it = 0; it < kRowChunks; it++) {
+    const int i = (threadIdx.x + kRowThreads * it) * 4;
+    if (i >= H) break;
+    sv[it] = load4<Y16>(ys + t * rs, i);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[it][j] = load4<Y16>(y + (j < K ? pos[j] : pos[0]) * rs, i);
+    if (residual) rv[it] = *reinterpret_cast<const float4*>(residual + (size_t)t * H + i);
+  }
   float4 row[kRowChunks];
 #pragma unroll
   for (int it = 0; it < kRowChunks; it++) {
     const int i = (threadIdx.x + kRowThreads * it) * 4;
     if (i >= H) break;
-    const size_t rs = Y16 ? (size_t)H / 2 : (size_t)H;  // row stride in floats
-    float4 acc = load4<Y16>(ys + t * rs, i);
+    float4 acc = sv[it];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       if (j < K) {
-        const float4 v = load4<Y16>(y + pos[j] * rs, i);
-        acc.x = acc.x + p[j] * v.x;
-        acc.y = acc.y + p[j] * v.y;
-        acc.z = acc.z + p[j] * v.z;
-        acc.w = acc.w + p[j] * v.w;
+        const float4 u = v[it][j];
+        acc.x = acc.x + p[j] * u.x;
+        acc.y = acc.y + p[j] * u.y;
+        acc.z = acc.z + p[j] * u.z;
+        acc.w = acc.w + p[j] * u.w;
       }
     }
     if (residual) {
-      const float4 r = *reinterpret_cast<const float4*>(residual + (size_t)t * H + i);
+      const float4 r = rv[it];
       acc.x = r.x + acc.x;
       acc.y = r.y + acc.y;
       acc.z = r.z + acc.z;
