@@ -28,12 +28,17 @@ __global__ __launch_bounds__(256) void router_rows_kernel(const float* __restric
   for (int p = lane; p < pairs; p += 64) {
     uint32_t wp = row[p];
     float w0 = bf16_lo(wp), w1 = bf16_hi(wp);
+    // Every token's pair is loaded before any is used (tokens past T read
+    // token 0 again and are not used).
+    float2 xv[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++)
+      xv[t] = reinterpret_cast<const float2*>(x + (size_t)(t < T ? t : 0) * H)[p];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
       if (t < T) {
-        float2 xv = reinterpret_cast<const float2*>(x + (size_t)t * H)[p];
-        acc[t] = fmaf(w0, xv.x, acc[t]);
-        acc[t] = fmaf(w1, xv.y, acc[t]);
+        acc[t] = fmaf(w0, xv[t].x, acc[t]);
+        acc[t] = fmaf(w1, xv[t].y, acc[t]);
       }
     }
   }
