@@ -33,6 +33,27 @@ __global__ __launch_bounds__(kRowThreads) void lm_head_kernel(const float* __res
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
+  // ---- this wave's rows [r0, r0 + kLmRowsPerWave), eight per pass: the
+  // 16-lane group g takes rows 2g and 2g + 1 of the pass. The resources
+  // start at r0, so offsets stay small whatever the matrix size. The first
+  // pass's loads are issued before the norm, which does not feed them
+  // (not for INT8 weight-only: its registers then exceed one SIMD's share
+  // for two waves, measured 40 -> 47 us).
+  const int r0 = blockIdx.x * kLmRowsPerWg + wave * kLmRowsPerWave;
+  const int nrows = min(kLmRowsPerWave, head.V - r0);
+  const int nblk = H / kQBlock;
+  const void* wbase = KIND == kBF16
+                          ? static_cast<const void*>(head.w + (size_t)r0 * H)
+                          : static_cast<const void*>(head.q + (size_t)r0 * H);
+  const float* sbase = KIND == kBF16 ? nullptr : head.s + (size_t)r0 * nblk;
+  const int grp = lane >> 4;
+  const int j = lane & 15;
+  using RP = RowPair<KIND == kBF16 ? kBF16 : kInt8, KMAX>;
+  constexpr bool kDouble = RP::kC <= 10;  // two passes in flight when registers allow
+  RP P[kDouble ? 2 : 1];
+  constexpr bool kEarly = KIND != kInt8;
+  if (kEarly && r0 < head.V) issue_rows(P[0], wbase, sbase, nrows, H, 2 * grp, 2 * grp + 1);
+
   // ---- RMSNorm of the row into LDS.
   float4 row[kRowChunks];
 #pragma unroll
@@ -47,26 +68,9 @@ __global__ __launch_bounds__(kRowThreads) void lm_head_kernel(const float* __res
     if (wave == 0) quantize_lds(xl, H, xq, xs, lane, blockIdx.x == 0 ? err : nullptr);
     __syncthreads();
   }
-
-  // ---- this wave's rows [r0, r0 + kLmRowsPerWave), eight per pass: the
-  // 16-lane group g takes rows 2g and 2g + 1 of the pass. The resources
-  // start at r0, so offsets stay small whatever the matrix size.
-  constexpr int kWChunk = KIND == kBF16 ? 2 : 1;  // bytes per weight
-  const int r0 = blockIdx.x * kLmRowsPerWg + wave * kLmRowsPerWave;
   if (r0 >= head.V) return;  // no barrier follows
-  const int nrows = min(kLmRowsPerWave, head.V - r0);
-  const int nblk = H / kQBlock;
-  const void* wbase = KIND == kBF16
-                          ? static_cast<const void*>(head.w + (size_t)r0 * H)
-                          : static_cast<const void*>(head.q + (size_t)r0 * H);
-  const float* sbase = KIND == kBF16 ? nullptr : head.s + (size_t)r0 * nblk;
-  (void)kWChunk;
-  const int grp = lane >> 4;
-  const int j = lane & 15;
-  using RP = RowPair<KIND == kBF16 ? kBF16 : kInt8, KMAX>;
-  constexpr bool kDouble = RP::kC <= 10;  // two passes in flight when registers allow
-  RP P[kDouble ? 2 : 1];
-  issue_rows(P[0], wbase, sbase, nrows, H, 2 * grp, 2 * grp + 1);
+  if (!kEarly) issue_rows(P[0], wbase, sbase, nrows, H, 2 * grp, 2 * grp + 1);
+
 #pragma unroll
   for (int pass = 0; pass < kLmPasses; pass++) {
     RP& cur = P[kDouble ? (pass & 1) : 0];
