@@ -102,8 +102,8 @@ def decode_bytes(int8: bool, unique_experts: float, T: int = 1) -> float:
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this "
-              "one-GPU build (expert-parallel sharding is described in DESIGN.md)",
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the path "
+              "runs on one GPU (expert-parallel sharding is designed, not built)",
               file=sys.stderr)
         sys.exit(2)
 
