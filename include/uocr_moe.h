@@ -111,6 +111,29 @@ typedef struct uocr_moe_int8_weights {
   const float* shared_down_scales;
 } uocr_moe_int8_weights;
 
+/* Optional trace of the W8A8 projections (DynamicActivations): the exact
+ * int32 block sums of Int8Matrix::linear_dynamic_int8
+ * (src/cpu/quantized.rs:190-198, sum over one 32-block of q_w * q_x) for
+ * every row a single-row group projects, and the FP32 hidden row
+ * (silu(gate) * up) that entered its down projection. Routed entries are
+ * indexed by dispatched position p (expert_offsets order):
+ *   gateup_sums [T*k][2*I][H/32]  rows 0..I-1 gate_proj, I..2I-1 up_proj
+ *   down_sums   [T*k][H][I/32]
+ *   hidden      [T*k][I]
+ * Positions of multi-row groups are left untouched. The shared expert is a
+ * single-row group only when T == 1:
+ *   shared_gateup_sums [2*S][H/32], shared_down_sums [H][S/32],
+ *   shared_hidden [S].
+ * Device pointers; NULL members are skipped. */
+typedef struct uocr_w8a8_trace {
+  int32_t* gateup_sums;
+  int32_t* down_sums;
+  float* hidden;
+  int32_t* shared_gateup_sums;
+  int32_t* shared_down_sums;
+  float* shared_hidden;
+} uocr_w8a8_trace;
+
 /* Optional per-forward trace, device pointers; NULL members are skipped.
  * Routing order is route()'s: probability descending, id ascending. */
 typedef struct uocr_moe_trace {
@@ -120,6 +143,7 @@ typedef struct uocr_moe_trace {
   int32_t* expert_offsets; /* [E+1] start of each expert's assignments */
   int32_t* perm_rows;      /* [T*k] token row of each assignment, expert-major */
   float* perm_weights;     /* [T*k] routing weight of each assignment */
+  const uocr_w8a8_trace* w8a8; /* W8A8 block sums (NULL: none) */
 } uocr_moe_trace;
 
 typedef struct uocr_gpu_ctx uocr_gpu_ctx;
@@ -159,6 +183,11 @@ int uocr_gpu_ctx_timings(uocr_gpu_ctx* ctx, uocr_phase_time* out, size_t cap, si
  * src/cpu/mod.rs:73-78); forwards above the context's limit fail with
  * Resource. */
 size_t uocr_moe_scratch_bytes(const uocr_moe_config* cfg, size_t T);
+/* Most tokens one forward of this configuration accepts (the device
+ * engines address activation planes with 32-bit byte offsets); more ->
+ * Resource. No counterpart in the reference, whose tensors are host
+ * vectors. */
+size_t uocr_moe_max_tokens(const uocr_moe_config* cfg);
 
 /* ------------------------------------------------------------------ layer */
 

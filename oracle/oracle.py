@@ -14,7 +14,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# UOCR_ORACLE_LIB points the binding at another build of the same source
+# (the sanitizer test loads an ASan/UBSan build that way).
+_LIB_PATH = os.environ.get("UOCR_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 OK, IO, JSON, FORMAT, SHAPE, UNSUPPORTED, RESOURCE, NUMERICAL = range(8)
 QUANT_NONE, QUANT_WEIGHTS_ONLY, QUANT_DYNAMIC = 0, 1, 2
@@ -72,6 +74,8 @@ def _load():
                                            ctypes.c_int, _SZ, ctypes.POINTER(MoeTraceStruct)]),
         "orc_moe_block": (ctypes.c_int, [ctypes.POINTER(MoeLayerStruct), _P, ctypes.c_float, _P,
                                          _SZ, _P, ctypes.c_int]),
+        "orc_moe_block_rows": (ctypes.c_int, [ctypes.POINTER(MoeLayerStruct), _P, ctypes.c_float,
+                                              _P, _SZ, _P, ctypes.c_int]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -323,15 +327,22 @@ def moe_experts(w: MoeWeights, x, threads=1, scratch_limit=0, trace=False):
     return (y, tr) if trace else y
 
 
-def moe_block(w: MoeWeights, norm_weight, eps, x, threads=1):
-    """x + experts(rms_norm(x)) — the post-attention half of Decoder::layer."""
+def moe_block(w: MoeWeights, norm_weight, eps, x, threads=1, row_threads=0):
+    """x + experts(rms_norm(x)) — the post-attention half of Decoder::layer.
+
+    row_threads > 1 splits the prefill GEMM rows over that many threads
+    (bit-identical; not a reference semantic, for CPU-baseline timing)."""
     x = _f32(x)
     T = x.shape[0]
     y = np.zeros((T, w.hidden), np.float32)
     nw = _f32(norm_weight)
     st, keep = _layer_struct(w)
-    status = lib().orc_moe_block(ctypes.byref(st), _ptr(nw), float(eps), _ptr(x), T, _ptr(y),
-                                 int(threads))
+    if row_threads > 1:
+        status = lib().orc_moe_block_rows(ctypes.byref(st), _ptr(nw), float(eps), _ptr(x), T,
+                                          _ptr(y), int(row_threads))
+    else:
+        status = lib().orc_moe_block(ctypes.byref(st), _ptr(nw), float(eps), _ptr(x), T,
+                                     _ptr(y), int(threads))
     del keep
     _check(status, "moe block")
     return y

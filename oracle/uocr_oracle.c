@@ -23,6 +23,10 @@
 typedef struct {
   int threads;
   size_t scratch; /* bytes; 0 = unlimited */
+  /* Not a reference semantic: > 1 splits the rows of the multi-row scalar
+   * GEMM over that many threads (each row's dot keeps its order, so the
+   * result is bit-identical). Only the CPU-baseline timing sets it. */
+  int row_threads;
 } orc_ctx;
 
 /* src/cpu/mod.rs:73-78: elements * 4 must fit the scratch limit. */
@@ -132,6 +136,7 @@ static int linear_ctx(const orc_ctx* cpu, const float* x, size_t m, size_t k, co
   int st = check_elements(cpu, m * n);
   if (st) return st;
   /* src/cpu/ops.rs:39-47: single-threaded scalar triple loop off macOS. */
+#pragma omp parallel for num_threads(cpu->row_threads) schedule(static) if (cpu->row_threads > 1)
   for (size_t i = 0; i < m; i++) {
     const float* xr = x + i * k;
     for (size_t j = 0; j < n; j++) {
@@ -150,7 +155,7 @@ static int linear_ctx(const orc_ctx* cpu, const float* x, size_t m, size_t k, co
 
 int orc_linear(const float* x, size_t m, size_t k, const float* w, size_t n, const float* bias,
                float* y) {
-  orc_ctx cpu = {1, 0};
+  orc_ctx cpu = {1, 0, 0};
   return linear_ctx(&cpu, x, m, k, w, n, bias, y);
 }
 
@@ -187,7 +192,7 @@ static int linear_weight_ctx(const orc_ctx* cpu, const float* x, size_t m, size_
 
 int orc_linear_weight_bf16(const float* x, size_t m, size_t k, const uint16_t* w, size_t n,
                            const float* bias, float* y, int threads) {
-  orc_ctx cpu = {threads > 0 ? threads : 1, 0};
+  orc_ctx cpu = {threads > 0 ? threads : 1, 0, 0};
   return linear_weight_ctx(&cpu, x, m, k, w, n, bias, y);
 }
 
@@ -304,7 +309,7 @@ static int int8_linear_ctx(const orc_ctx* cpu, const int8_t* q, const float* s, 
 
 int orc_int8_linear(const int8_t* q, const float* s, size_t rows, size_t cols, const float* x,
                     size_t batch, float* y, int threads) {
-  orc_ctx cpu = {threads > 0 ? threads : 1, 0};
+  orc_ctx cpu = {threads > 0 ? threads : 1, 0, 0};
   return int8_linear_ctx(&cpu, q, s, rows, cols, x, batch, y);
 }
 
@@ -351,7 +356,7 @@ static int int8_dynamic_ctx(const orc_ctx* cpu, const int8_t* q, const float* s,
 
 int orc_int8_linear_dynamic(const int8_t* q, const float* s, size_t rows, size_t cols,
                             const float* x, float* y, int32_t* block_sums, int threads) {
-  orc_ctx cpu = {threads > 0 ? threads : 1, 0};
+  orc_ctx cpu = {threads > 0 ? threads : 1, 0, 0};
   return int8_dynamic_ctx(&cpu, q, s, rows, cols, x, y, block_sums);
 }
 
@@ -518,7 +523,7 @@ static int experts_ctx(const orc_ctx* cpu, const orc_moe_layer* L, const float* 
           task_p[n] = probs[counts[e]];
           n++;
         }
-      orc_ctx worker = {1, cpu->scratch ? cpu->scratch / tasks : 0};
+      orc_ctx worker = {1, cpu->scratch ? cpu->scratch / tasks : 0, 0};
 #pragma omp parallel for num_threads(cpu->threads) schedule(dynamic, 1)
       for (size_t task = 0; task < tasks; task++) {
         matrix g, u, d;
@@ -582,22 +587,34 @@ done:
 
 int orc_moe_experts(const orc_moe_layer* layer, const float* x, size_t T, float* y, int threads,
                     size_t scratch_limit, orc_moe_trace* trace) {
-  orc_ctx cpu = {threads > 0 ? threads : 1, scratch_limit};
+  orc_ctx cpu = {threads > 0 ? threads : 1, scratch_limit, 0};
   return experts_ctx(&cpu, layer, x, T, y, trace);
 }
 
-int orc_moe_block(const orc_moe_layer* layer, const float* norm_weight, float eps, const float* x,
-                  size_t T, float* y, int threads) {
+static int moe_block_ctx(const orc_ctx* cpu, const orc_moe_layer* layer,
+                         const float* norm_weight, float eps, const float* x, size_t T, float* y) {
   if (!layer) return ORC_SHAPE;
   size_t H = layer->hidden;
   float* normalized = (float*)malloc(T * H * sizeof(float) + 1);
   if (!normalized) return ORC_RESOURCE;
   int st = orc_rms_norm(x, T, H, norm_weight, eps, normalized);
-  if (!st) st = orc_moe_experts(layer, normalized, T, y, threads, 0, NULL);
+  if (!st) st = experts_ctx(cpu, layer, normalized, T, y, NULL);
   if (!st) {
     /* src/decoder/mod.rs:361-363: residual += mlp. */
     for (size_t i = 0; i < T * H; i++) y[i] = x[i] + y[i];
   }
   free(normalized);
   return st;
+}
+
+int orc_moe_block(const orc_moe_layer* layer, const float* norm_weight, float eps, const float* x,
+                  size_t T, float* y, int threads) {
+  orc_ctx cpu = {threads > 0 ? threads : 1, 0, 0};
+  return moe_block_ctx(&cpu, layer, norm_weight, eps, x, T, y);
+}
+
+int orc_moe_block_rows(const orc_moe_layer* layer, const float* norm_weight, float eps,
+                       const float* x, size_t T, float* y, int row_threads) {
+  orc_ctx cpu = {1, 0, row_threads};
+  return moe_block_ctx(&cpu, layer, norm_weight, eps, x, T, y);
 }

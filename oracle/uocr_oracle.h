@@ -126,6 +126,12 @@ int orc_moe_experts(const orc_moe_layer* layer, const float* x, size_t T, float*
  * y = x + experts(rms_norm(x, norm_weight, eps)). */
 int orc_moe_block(const orc_moe_layer* layer, const float* norm_weight, float eps, const float* x,
                   size_t T, float* y, int threads);
+/* The same block with the rows of every multi-row scalar GEMM split over
+ * `row_threads` threads: bit-identical to orc_moe_block, and not what the
+ * reference does (its prefill GEMM is serial off macOS, src/cpu/ops.rs:
+ * 36-47). Used only to time a stronger CPU baseline. */
+int orc_moe_block_rows(const orc_moe_layer* layer, const float* norm_weight, float eps,
+                       const float* x, size_t T, float* y, int row_threads);
 
 #ifdef __cplusplus
 }

@@ -32,3 +32,29 @@ def test_scratch_budget_grows_with_tokens():
     assert 0 < small < big
     # Dominated by the routed hidden and output rows: T*k*(I + H) floats.
     assert big >= 4096 * 6 * (896 + 1280) * 4
+
+
+def test_token_cap_is_derived_from_byte_ranges():
+    """uocr_moe_max_tokens keeps every 32-bit buffer range of the MFMA engine
+    below 2^31 bytes: x planes T*H*2, routed hidden planes T*k*I*2, shared
+    hidden planes T*S*2, and T*k*H elements of expert outputs."""
+    limit = (1 << 31) - 1
+
+    def expect(H, I, E, SH, K):
+        per = max(2 * H, 2 * K * I, 2 * I * SH, K * H)
+        return limit // per
+
+    # The model shape: routed hidden planes dominate (k*I*2 = 10752 B/token).
+    cfg = um.config()
+    n = um.max_tokens(cfg)
+    assert n == expect(1280, 896, 64, 2, 6) == 199728
+    assert n * 6 * 896 * 2 < 1 << 31 and (n + 1) * 6 * 896 * 2 >= limit - 6 * 896 * 2
+    # Shapes validate_config accepts where a fixed 262,144-token cap wraps:
+    # k=8, I=1024 (T*k*I*2 = 2^32 at 262,144), a wide shared expert, a wide
+    # hidden row.
+    for H, I, E, SH, K in [(1280, 1024, 64, 2, 8), (2048, 4096, 8, 2, 2), (8192, 64, 8, 1, 1)]:
+        c = um.config(H, I, E, SH, K, normalize=True)
+        m = um.max_tokens(c)
+        assert m == expect(H, I, E, SH, K)
+        assert m < 262144
+        assert m * max(2 * H, 2 * K * I, 2 * I * SH, K * H) <= limit

@@ -50,7 +50,7 @@ def test_route_normalised_weights_closed_form():
 
 
 def test_linear_kat():
-    # tests/ops.rs:23-33
+    # tests/ops.rs:10-20
     x = np.array([[1, 2, 3], [-1, 0, 2]], np.float32)
     w = np.array([[1, 0, -1], [2, 1, 0]], np.float32)
     y = orc.linear(x, w, bias=np.array([1, -1], np.float32))
@@ -58,7 +58,7 @@ def test_linear_kat():
 
 
 def test_softmax_kats():
-    # tests/ops.rs:46-53
+    # tests/ops.rs:33-40
     assert orc.softmax([1000.0, 1000.0, -1000.0]).tolist() == [0.5, 0.5, 0.0]
     for bad in ([float("nan"), 0.0], [float("-inf")] * 2, [], [float("inf")]):
         with pytest.raises(orc.OracleError) as e:
@@ -67,7 +67,7 @@ def test_softmax_kats():
 
 
 def test_softmax_matches_f64_oracle():
-    # tests/ops.rs:114-145 (Scalar backend).
+    # tests/ops.rs:101-132 (Scalar backend).
     for n in [1, 3, 17, 196, 4096]:
         x = np.array([-np.inf if i % 7 == 3 else 1000.0 + math.sin(i * 0.37) * 30.0
                       for i in range(n)], np.float32)
@@ -79,7 +79,7 @@ def test_softmax_matches_f64_oracle():
 
 
 def test_rms_norm_kat():
-    # tests/ops.rs:55-64
+    # tests/ops.rs:42-51
     y = orc.rms_norm(np.array([[1.0, 3.0]], np.float32), np.array([1.0, 1.0], np.float32), 1e-6)
     assert abs(y[0, 0] - 0.44721355) < 1e-6
     assert abs(y[0, 1] - 1.3416406) < 1e-6
@@ -89,7 +89,7 @@ def test_rms_norm_kat():
 
 
 def test_silu_kat():
-    # tests/ops.rs:88-100
+    # tests/ops.rs:74-84
     y = orc.silu(np.array([-1.0, 0.0, 1.0], np.float32))
     for a, b in zip(y, [-0.26894143, 0.0, 0.7310586]):
         assert abs(a - b) < 1e-6

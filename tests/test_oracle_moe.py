@@ -176,3 +176,14 @@ def test_errors():
     with pytest.raises(orc.OracleError) as e:
         orc.moe_experts(Ld, x)
     assert e.value.status == orc.FORMAT
+
+
+def test_row_parallel_block_is_bit_identical():
+    """orc_moe_block_rows (the CPU-baseline timing aid that splits the
+    prefill GEMM's rows over threads) returns the serial block's bits."""
+    w = small_layer(seed=31)
+    x = syn.activations(37, w.hidden, seed=32)
+    nw = np.linspace(0.5, 1.5, w.hidden).astype(np.float32)
+    a = orc.moe_block(w, nw, 1e-6, x)
+    b = orc.moe_block(w, nw, 1e-6, x, row_threads=4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

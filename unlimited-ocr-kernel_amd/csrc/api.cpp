@@ -6,6 +6,7 @@
 // (src/cpu/mod.rs:18-79): a device, a stream and a scratch budget.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -227,6 +228,24 @@ int validate_config(const uocr_moe_config* c) {
   return UOCR_OK;
 }
 
+// Most tokens one forward may carry. The MFMA engine addresses its bf16
+// activation planes through buffer resources whose ranges and per-lane
+// offsets are 32-bit byte counts, with offset 2^31 standing for "outside
+// every resource": the x planes (T*H*2 bytes), the routed hidden planes
+// (T*K*I*2) and the shared hidden planes (T*S*2) must each stay below
+// 2^31 bytes. Expert outputs [T*K, H] are indexed with 32-bit element
+// offsets in places, so T*K*H stays below 2^31 too.
+size_t max_tokens(const uocr_moe_config& c) {
+  const uint64_t H = c.hidden_size, K = c.num_experts_per_tok, I = c.moe_intermediate_size;
+  const uint64_t S = I * c.n_shared_experts;
+  uint64_t per = 2 * H;
+  per = std::max<uint64_t>(per, 2 * K * I);
+  per = std::max<uint64_t>(per, 2 * S);
+  per = std::max<uint64_t>(per, K * H);
+  if (per == 0) return 0;
+  return (size_t)(((1ull << 31) - 1) / per);
+}
+
 hipMemcpyKind kind_of(uocr_memory where) {
   return where == UOCR_MEMORY_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
 }
@@ -317,6 +336,29 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
   hipStream_t st = ctx->stream;
+  const uocr_w8a8_trace* q8t =
+      trace && L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS ? trace->w8a8 : nullptr;
+  if (q8t) {
+    S.q8.gateup = q8t->gateup_sums;
+    S.q8.down = q8t->down_sums;
+    S.q8.hidden = q8t->hidden;
+    if (T == 1) {
+      S.q8.s_gateup = q8t->shared_gateup_sums;
+      S.q8.s_down = q8t->shared_down_sums;
+      S.q8.s_hidden = q8t->shared_hidden;
+    }
+  }
+  // The W8A8 trace's hidden rows, copied where the engine holds them (the
+  // MFMA GEMMs later reuse the small-batch engine's hidden rows' bytes).
+  auto trace_hidden = [&](const float* routed, const float* shared) -> int {
+    if (S.q8.hidden)
+      HIP_TRY(hipMemcpyAsync(S.q8.hidden, routed, T * L.K * L.I * 4, hipMemcpyDeviceToDevice, st),
+              "trace copy");
+    if (S.q8.s_hidden)
+      HIP_TRY(hipMemcpyAsync(S.q8.s_hidden, shared, (size_t)L.S * 4, hipMemcpyDeviceToDevice, st),
+              "trace copy");
+    return UOCR_OK;
+  };
   const Engine engine = choose_engine(layer, T, flags);
   const bool mfma = engine == Engine::Mfma;
   // The small-batch engine also takes the single-row W8A8 groups of the
@@ -342,6 +384,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     phase_begin(ctx, kDown);
     uocr::launch_decode_stage(2, L, S, residual, y, st);
     phase_end(ctx);
+    if (int r = trace_hidden(S.gu, S.gu + (size_t)L.K * L.I)) return r;
   } else {
     if (T <= (size_t)uocr::kGemvChunk && !mfma) {
       // Few tokens: logits with every token staged once, then one
@@ -395,6 +438,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
         phase_begin(ctx, kGateUp);
         uocr::launch_batch_gateup(L, S, Ti, tiles_bound, uocr::kGemvChunk, st, true);
         phase_end(ctx);
+        if (int r = trace_hidden(S.h, S.hs)) return r;
         phase_begin(ctx, kDown);
         uocr::launch_batch_down(L, S, Ti, tiles_bound, uocr::kGemvChunk, st, true);
         phase_end(ctx);
@@ -409,6 +453,7 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
       phase_begin(ctx, kGateUp);
       uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);
+      if (int r = trace_hidden(S.h, S.hs)) return r;
       phase_begin(ctx, kDown);
       uocr::launch_batch_down(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);
@@ -522,6 +567,11 @@ const char* uocr_last_error(const uocr_gpu_ctx* ctx) {
 size_t uocr_moe_scratch_bytes(const uocr_moe_config* cfg, size_t T) {
   if (!cfg) return 0;
   return plan_scratch(*cfg, T).total;
+}
+
+size_t uocr_moe_max_tokens(const uocr_moe_config* cfg) {
+  if (!cfg) return 0;
+  return max_tokens(*cfg);
 }
 
 int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
@@ -736,9 +786,10 @@ int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const
   if (!ctx || !layer) return fail(UOCR_ERR_SHAPE, "null handle");
   if (T == 0) return UOCR_OK;
   if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
-  // The MFMA engine addresses activation rows with 32-bit element offsets
-  // (T * k * max(I, S) < 2^32); 262,144 tokens per forward keeps that safe.
-  if (T > (size_t)262144) return fail(UOCR_ERR_RESOURCE, "token count too large");
+  if (layer->device != ctx->device) return fail(UOCR_ERR_SHAPE, "layer lives on another device");
+  if (T > max_tokens(layer->cfg))
+    return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu > %zu)", T,
+                max_tokens(layer->cfg));
   HIP_TRY(hipSetDevice(ctx->device), "set device");
   return enqueue_experts(ctx, layer, x, T, nullptr, y, flags, trace, false);
 }
@@ -756,10 +807,17 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
   if (!ctx || (!layers && n_layers)) return fail(UOCR_ERR_SHAPE, "null handle");
   if (T == 0 || n_layers == 0) return UOCR_OK;
   if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
-  if (T > (size_t)262144) return fail(UOCR_ERR_RESOURCE, "token count too large");
   HIP_TRY(hipSetDevice(ctx->device), "set device");
   for (size_t l = 0; l < n_layers; l++) {
     if (!layers[l]) return fail(UOCR_ERR_SHAPE, "null layer %zu", l);
+    // Every layer reads and writes the caller's [T, H] rows.
+    if (layers[l]->cfg.hidden_size != layers[0]->cfg.hidden_size)
+      return fail(UOCR_ERR_SHAPE, "layer %zu hidden size differs from layer 0", l);
+    if (layers[l]->device != ctx->device)
+      return fail(UOCR_ERR_SHAPE, "layer %zu lives on another device", l);
+    if (T > max_tokens(layers[l]->cfg))
+      return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu > %zu)", T,
+                  max_tokens(layers[l]->cfg));
     if (!layers[l]->dev.norm_w) return fail(UOCR_ERR_FORMAT, "layer %zu has no norm weight", l);
     if (plan_scratch(layers[l]->cfg, T).total > ctx->scratch_limit)
       return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit");

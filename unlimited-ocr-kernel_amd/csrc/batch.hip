@@ -154,10 +154,12 @@ __device__ __forceinline__ const float* s2_of(const DeviceLayer& L, int g) {
 // sums (in every lane of the row's 16-lane group). K valid columns of each
 // activation row are staged at stride ld (zero beyond). A single-row tile
 // of an INT8 layer in DynamicActivations mode takes the W8A8 dot instead.
+// `sums`: where the W8A8 dot stores its block sums (a test trace).
 template <int KIND, int KMAX, int XB, bool DYN, typename RowOf, typename Emit>
 __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                          const RowPair<KIND, KMAX>& P, int K, int xb, int cols,
-                                         int ld, const Unit& u, RowOf row_of, Emit emit) {
+                                         int ld, const Unit& u, RowOf row_of, Emit emit,
+                                         const BlockSumOut& sums = BlockSumOut()) {
   const int lane = threadIdx.x & 63;
   const int xb_off = XB ? xb : 0;
   if constexpr (KIND == kInt8 && DYN) {
@@ -168,7 +170,7 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
       if (threadIdx.x < 64) quantize_lds(sm.x, ld, sm.xq, sm.xs, lane, S.err);
       __syncthreads();
       float r0, r1;
-      dot_rows_as<kW8A8>(P, K, sm.x, sm.xq, sm.xs, r0, r1, xb_off);
+      dot_rows_as<kW8A8>(P, K, sm.x, sm.xq, sm.xs, r0, r1, xb_off, sums);
       emit(0, r0, r1);
       return;
     }
@@ -224,9 +226,21 @@ __attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_ga
   };
   float* hout = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
   const int ld = u.routed ? L.I : L.S;
+  BlockSumOut bs;
+  if (DYN && u.group_rows == 1 && k < W) {
+    // A single-row group: position `base` (routed) or the one token (shared).
+    const int nb = L.H / kQBlock;
+    int32_t* at = u.routed ? (S.q8.gateup ? S.q8.gateup + (size_t)base * 2 * L.I * nb : nullptr)
+                           : S.q8.s_gateup;
+    if (at) {
+      bs.a = at + (size_t)k * nb;
+      bs.b = at + (size_t)(W + k) * nb;
+      bs.na = bs.nb = nb;
+    }
+  }
   tile_dot<KIND, KH, 0, DYN>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
     if ((lane & 15) == 0 && k < W) hout[(size_t)t * ld + k] = silu(g) * up;
-  });
+  }, bs);
 }
 
 // Down: a unit is 32 output features of one tile (each wave 8 full rows of
@@ -247,6 +261,24 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   const float* hin = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
   auto row_of = [&](int t) { return hin + (size_t)t * W; };
   float* yout = u.routed ? S.y + (size_t)base * L.H : S.ys + (size_t)base * L.H;
+  BlockSumOut bs;
+  if (DYN && u.group_rows == 1) {
+    // Rows [H][W/32] of a single-row group's down projection: full rows ra
+    // and rb, or the two column halves of row ra.
+    const int nb = W / kQBlock;
+    int32_t* at = u.routed ? (S.q8.down ? S.q8.down + (size_t)base * L.H * nb : nullptr) : S.q8.s_down;
+    if (at && ra < L.H) {
+      bs.a = at + (size_t)ra * nb;
+      if (HALVES) {
+        bs.b = bs.a + seg / kQBlock;
+        bs.na = seg / kQBlock;
+        bs.nb = nb - seg / kQBlock;
+      } else {
+        bs.b = rb < L.H ? at + (size_t)rb * nb : nullptr;
+        bs.na = bs.nb = nb;
+      }
+    }
+  }
   tile_dot<KIND, kSegK, HALVES ? 1 : 0, DYN>(L, S, sm, P, seg, seg, W, HALVES ? 2 * seg : W, u, row_of,
                                         [&](int t, float y0, float y1) {
     if ((lane & 15) == 0) {
@@ -257,7 +289,7 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
         if (rb < L.H) yout[(size_t)t * L.H + rb] = y1;
       }
     }
-  });
+  }, bs);
 }
 
 template <int KIND, bool DYN>
@@ -318,7 +350,7 @@ __global__ __launch_bounds__(64) void small_router_kernel(const float* __restric
 }
 
 // One workgroup of 16 waves: wave t routes token t (moe::route,
-// src/decoder/moe.rs:11-31), then the dispatch of Decoder::experts
+// src/decoder/moe.rs:7-30), then the dispatch of Decoder::experts
 // (src/decoder/mod.rs:127-141): per expert, its tokens in ascending order;
 // one row tile per active expert and one for the shared expert.
 constexpr int kRouteWaves = 16;

@@ -18,8 +18,8 @@
 // the rounded product w * scale (src/cpu/quantized.rs:119-131); W8A8 for
 // DynamicActivations (one row is always a single-row group, :103-104) with
 // the row quantised per 32-block and exact i32 block sums (:155-236).
-// Routing is moe::route (src/decoder/moe.rs:11-31) on logits from
-// ops::linear (src/cpu/ops.rs:23-58); the combine follows moe.rs:85-103.
+// Routing is moe::route (src/decoder/moe.rs:7-30) on logits from
+// ops::linear (src/cpu/ops.rs:9-59); the combine follows src/decoder/mod.rs:185-194.
 #include "common.hpp"
 #include "moe_kernels.hpp"
 #include "routing.hpp"
@@ -113,8 +113,15 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
     RowPair<KIND, KH> P;
     issue_rows(P, w13_of<KIND>(L, L.E), s13_of<KIND>(L, L.E), 2 * L.S, L.H, ra, ra + 32);
     stage_x<KIND, KH>(L, S, sm, wave, lane);
+    BlockSumOut bs;
+    if (KIND == kW8A8 && S.q8.s_gateup) {
+      const int nb = L.H / kQBlock;
+      bs.a = S.q8.s_gateup + (size_t)k * nb;
+      bs.b = S.q8.s_gateup + (size_t)(L.S + k) * nb;
+      bs.na = bs.nb = nb;
+    }
     float r0, r1;
-    dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
+    dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
     if ((lane & 15) == 0) S.gu[(size_t)L.K * L.I + k] = silu(r0) * r1;
     return;
   }
@@ -175,8 +182,16 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
   const int ra = gate_row(k);
   RowPair<KIND, KH> P;
   issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
+  // One token: the dispatched position of a slot is the slot itself.
+  BlockSumOut bs;
+  if (KIND == kW8A8 && S.q8.gateup) {
+    const int nb = L.H / kQBlock;
+    bs.a = S.q8.gateup + ((size_t)slot * 2 * L.I + k) * nb;
+    bs.b = S.q8.gateup + ((size_t)slot * 2 * L.I + L.I + k) * nb;
+    bs.na = bs.nb = nb;
+  }
   float r0, r1;
-  dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1);
+  dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
   if ((lane & 15) == 0) S.gu[(size_t)slot * L.I + k] = silu(r0) * r1;
 }
 
@@ -224,8 +239,17 @@ __global__ __launch_bounds__(64 * (kMaxK + 2)) void decode_down_kernel(DeviceLay
     quantize_lds(sm.hl[wave], n, sm.hq[wave], sm.hs[wave], lane, S.err);
     __syncthreads();
   }
+  BlockSumOut bs;
+  if (KIND == kW8A8 && (routed ? S.q8.down : S.q8.s_down)) {
+    const int nb = L.width(g) / kQBlock;
+    int32_t* row = routed ? S.q8.down + ((size_t)wave * L.H + f0 + q) * nb
+                          : S.q8.s_down + (size_t)(f0 + q) * nb + (wave - L.K) * (half / kQBlock);
+    bs.a = row;
+    bs.b = row + (size_t)4 * nb;
+    bs.na = bs.nb = n / kQBlock;
+  }
   float r0, r1;
-  dot_rows(P, n, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1);
+  dot_rows(P, n, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1, bs);
   if ((lane & 15) == 0) {
     sm.yl[wave][q] = r0;
     sm.yl[wave][q + 4] = r1;

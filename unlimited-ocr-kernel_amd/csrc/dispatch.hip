@@ -245,7 +245,8 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
   // Place the chunk's tokens (lanes past the chunk idle): bit t of emask[e]
   // is set when token t of the chunk selected expert e, so a token's rank
   // among the chunk's earlier tokens of that expert is a popcount. One wave
-  // sets and reads the masks; its LDS operations complete in order.
+  // sets and reads the masks: a wavefront-scope release/acquire pair around
+  // a wave barrier orders every lane's atomicOr before any lane's read.
   const int t = c * kChunk + lane;
   const bool valid = lane < kChunk && t < T;
   int my_e[8];
@@ -254,6 +255,9 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
     my_e[j] = (valid && j < K) ? ids[(size_t)t * K + j] : -1;
     if (my_e[j] >= 0) atomicOr(&emask[my_e[j]], 1ull << lane);
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (!valid) return;
   const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll

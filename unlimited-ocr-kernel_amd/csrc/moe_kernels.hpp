@@ -40,6 +40,22 @@ struct DeviceLayer {
   __host__ __device__ size_t s2_offset(int g) const { return (size_t)g * H * (I / 32); }
 };
 
+// Optional trace of the W8A8 (DynamicActivations, single-row group)
+// projections: exact i32 block sums in checkpoint row order and the f32
+// hidden rows that entered the down projection. Routed entries are indexed
+// by dispatched position p: gate/up [p][2I][H/32] (gate rows, then up
+// rows), down [p][H][I/32], hidden [p][I]. Shared entries exist for one
+// token only: gate/up [2S][H/32], down [H][S/32], hidden [S]. Null
+// pointers are not written.
+struct Q8Trace {
+  int32_t* gateup = nullptr;
+  int32_t* down = nullptr;
+  float* hidden = nullptr;
+  int32_t* s_gateup = nullptr;
+  int32_t* s_down = nullptr;
+  float* s_hidden = nullptr;
+};
+
 // Per-forward device scratch carved from the context's reservation.
 struct Scratch {
   float* logits;    // [T,E]
@@ -60,6 +76,7 @@ struct Scratch {
   uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
   float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
   int* err;         // device error flag
+  Q8Trace q8;       // W8A8 trace (tests), all null by default
 };
 
 int max_tiles(int T, int K, int E, int bm);

@@ -121,6 +121,15 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
   issue_rows_cols(P, w, s, rows, K, 0, K, ra, rb);
 }
 
+// Where a W8A8 dot also stores its exact i32 block sums (a test trace):
+// blocks [0, na) of segment a at a[...], [0, nb) of segment b at b[...];
+// null pointers store nothing.
+struct BlockSumOut {
+  int32_t* a = nullptr;
+  int32_t* b = nullptr;
+  int na = 0, nb = 0;
+};
+
 // Dots both rows with the LDS activation row (xl, or xq/xs for a W8A8
 // dot); every lane of a 16-lane group returns that group's two row sums.
 // DOT picks the arithmetic: INT8 chunks serve both the weight-only and the
@@ -129,7 +138,8 @@ __device__ __forceinline__ void issue_rows(RowPair<KIND, KMAX>& P, const void* w
 template <int DOT, int KIND, int KMAX>
 __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K, const float* xl,
                                             const int8_t* xq, const float* xs, float& r0,
-                                            float& r1, int xb_off = 0) {
+                                            float& r1, int xb_off = 0,
+                                            const BlockSumOut& sums = BlockSumOut()) {
   using RP = RowPair<KIND, KMAX>;
   static_assert((DOT == kBF16) == (KIND == kBF16), "BF16 dots need BF16 chunks");
   const int j = threadIdx.x & (kLpr - 1);
@@ -193,6 +203,8 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
         const int b = c >> 1;
         a0 += (float)ia * P.sa[m] * xs[b];
         a1 += (float)ib * P.sb[m] * xs[(xb_off >> 5) + b];
+        if (sums.a && b < sums.na) sums.a[b] = ia;
+        if (sums.b && b < sums.nb) sums.b[b] = ib;
       }
     }
   }
@@ -203,8 +215,8 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
 template <int KIND, int KMAX>
 __device__ __forceinline__ void dot_rows(const RowPair<KIND, KMAX>& P, int K, const float* xl,
                                          const int8_t* xq, const float* xs, float& r0,
-                                         float& r1) {
-  dot_rows_as<KIND>(P, K, xl, xq, xs, r0, r1);
+                                         float& r1, const BlockSumOut& sums = BlockSumOut()) {
+  dot_rows_as<KIND>(P, K, xl, xq, xs, r0, r1, 0, sums);
 }
 
 // An FP32 row of n <= N values (n % 4 == 0) held in registers of one wave

@@ -20,7 +20,9 @@ except ImportError:  # the library itself does not need torch
     pass
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libuocr_moe.so")
+# UOCR_MOE_LIB points the binding at another build of the library (the
+# sanitizer test loads a CPU-only ASan/UBSan build of the host code).
+LIB_PATH = os.environ.get("UOCR_MOE_LIB") or os.path.join(_HERE, "libuocr_moe.so")
 
 OK, IO, JSON, FORMAT, SHAPE, UNSUPPORTED, RESOURCE, NUMERICAL = range(8)
 STATUS_NAMES = ["Ok", "Io", "Json", "Format", "Shape", "Unsupported", "Resource", "Numerical"]
@@ -36,6 +38,7 @@ PHASES = ["router", "topk", "dispatch", "split", "gateup", "down", "combine", "n
 EXPORTS = [
     "uocr_gpu_ctx_create", "uocr_gpu_ctx_destroy", "uocr_gpu_ctx_stream",
     "uocr_gpu_ctx_synchronize", "uocr_last_error", "uocr_moe_scratch_bytes",
+    "uocr_moe_max_tokens",
     "uocr_gpu_ctx_set_timing", "uocr_gpu_ctx_timings",
     "uocr_moe_layer_create", "uocr_moe_layer_attach_int8", "uocr_moe_layer_precision",
     "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
@@ -104,9 +107,18 @@ class ModelConfig(ctypes.Structure):
         ("routed_scaling_factor", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
 
 
+W8A8_TRACE_FIELDS = ("gateup_sums", "down_sums", "hidden", "shared_gateup_sums",
+                     "shared_down_sums", "shared_hidden")
+
+
+class W8A8Trace(ctypes.Structure):
+    _fields_ = [(n, _P) for n in W8A8_TRACE_FIELDS]
+
+
 class Trace(ctypes.Structure):
     _fields_ = [(n, _P) for n in ("logits", "topk_ids", "topk_weights", "expert_offsets",
-                                  "perm_rows", "perm_weights")]
+                                  "perm_rows", "perm_weights")] + [
+        ("w8a8", ctypes.POINTER(W8A8Trace))]
 
 
 def _load():
@@ -120,6 +132,7 @@ def _load():
         "uocr_gpu_ctx_synchronize": (ctypes.c_int, [_P]),
         "uocr_last_error": (ctypes.c_char_p, [_P]),
         "uocr_moe_scratch_bytes": (_SZ, [ctypes.POINTER(MoeConfig), _SZ]),
+        "uocr_moe_max_tokens": (_SZ, [ctypes.POINTER(MoeConfig)]),
         "uocr_gpu_ctx_set_timing": (ctypes.c_int, [_P, _U32]),
         "uocr_gpu_ctx_timings": (ctypes.c_int, [_P, ctypes.POINTER(PhaseTime), _SZ,
                                                 ctypes.POINTER(_SZ)]),
@@ -300,13 +313,19 @@ class MoeLayer:
 
 def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | None = None,
             sync: bool = True):
-    """Decoder::experts on device tensors x [T,H] -> y [T,H] (float32, cuda)."""
+    """Decoder::experts on device tensors x [T,H] -> y [T,H] (float32, cuda).
+
+    trace: optional dict of device tensors named as uocr_moe_trace's members;
+    a nested dict under "w8a8" names uocr_w8a8_trace's members."""
     T = x.shape[0]
     tr = None
     if trace is not None:
         tr = Trace(*[_ptr(trace.get(n)) for n in ("logits", "topk_ids", "topk_weights",
                                                   "expert_offsets", "perm_rows",
                                                   "perm_weights")])
+        if trace.get("w8a8"):
+            q8 = W8A8Trace(*[_ptr(trace["w8a8"].get(n)) for n in W8A8_TRACE_FIELDS])
+            tr.w8a8 = ctypes.pointer(q8)
     fn = lib.uocr_moe_forward if sync else lib.uocr_moe_forward_async
     _check(fn(ctx.handle, layer.handle, _ptr(x), T, _ptr(y), flags,
               ctypes.byref(tr) if tr is not None else None))
@@ -363,6 +382,10 @@ def block_forward(ctx: Context, layers, x, y, flags: int = 0, sync: bool = True)
 
 def scratch_bytes(cfg: MoeConfig, T: int) -> int:
     return lib.uocr_moe_scratch_bytes(ctypes.byref(cfg), T)
+
+
+def max_tokens(cfg: MoeConfig) -> int:
+    return lib.uocr_moe_max_tokens(ctypes.byref(cfg))
 
 
 def route(ctx: Context, logits, count: int, normalize: bool, scale: float, ids, weights):
