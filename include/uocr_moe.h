@@ -223,6 +223,24 @@ int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const
 /* The same, then synchronize: errors are reported by this call. */
 int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
                      float* y, uint32_t flags, const uocr_moe_trace* trace);
+/* Allocation-free variant of uocr_moe_forward_async. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Same engines and results as uocr_moe_forward_async, but its
+ * scratch is a static device array of UOCR_STATIC_SCRATCH_BYTES per GPU
+ * (held until the process ends) instead of a context's reservation, and it
+ * calls no allocating routine. Forwards whose uocr_moe_scratch_bytes
+ * exceeds UOCR_STATIC_SCRATCH_BYTES - 256 fail with Resource (at the model
+ * shape: up to about 126 tokens). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU race, so serialise them (one
+ * stream, or events). Enqueued on `stream` (a hipStream_t; NULL: the null
+ * stream) and returns once queued. Device-side errors (non-finite
+ * routing, normalisation or W8A8 inputs: Numerical) are written as a
+ * status code to *device_status (a device int32 the call first clears; NULL:
+ * an internal flag nobody reads). No trace, no phase timers. */
+#define UOCR_STATIC_SCRATCH_BYTES (16u << 20)
+int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t T, float* y,
+                            uint32_t flags, int32_t* device_status, void* stream);
 /* The post-attention half of Decoder::layer (src/decoder/mod.rs:351-363)
  * over a stack of MoE layers: x <- x + experts(rms_norm(x, norm_weight)),
  * layer after layer. x and y are device [T,H]; y may equal x. Synchronous. */

@@ -58,6 +58,10 @@ int uocr_moe_forward(uocr_gpu_ctx*, const uocr_moe_layer*, const float*, size_t,
                      const uocr_moe_trace*) {
   return unsupported();
 }
+int uocr_moe_forward_static(const uocr_moe_layer*, const float*, size_t, float*, uint32_t,
+                            int32_t*, void*) {
+  return unsupported();
+}
 int uocr_moe_block_forward_async(uocr_gpu_ctx*, const uocr_moe_layer* const*, size_t,
                                  const float*, size_t, float*, uint32_t) {
   return unsupported();

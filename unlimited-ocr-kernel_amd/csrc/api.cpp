@@ -20,6 +20,9 @@
 using uocr::DeviceLayer;
 using uocr::Scratch;
 
+// The static scratch of uocr_moe_forward_static (one copy per GPU).
+static __device__ __align__(256) char scratch[UOCR_STATIC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -103,14 +106,14 @@ hipEvent_t take_event(uocr_gpu_ctx* ctx) {
 
 // Brackets the launches between begin and end with events when timing.
 void phase_begin(uocr_gpu_ctx* ctx, int phase) {
-  if (!((ctx->timing_mask >> phase) & 1u)) return;
+  if (!ctx || !((ctx->timing_mask >> phase) & 1u)) return;
   ctx->open_phase = phase;
   ctx->open_start = take_event(ctx);
   (void)hipEventRecord(ctx->open_start, ctx->stream);
 }
 
 void phase_end(uocr_gpu_ctx* ctx) {
-  if (ctx->open_phase < 0) return;
+  if (!ctx || ctx->open_phase < 0) return;
   hipEvent_t stop = take_event(ctx);
   (void)hipEventRecord(stop, ctx->stream);
   ctx->pending.push_back({ctx->open_phase, ctx->open_start, stop});
@@ -188,9 +191,23 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   return p;
 }
 
-Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
+// Where a forward runs: a scratch region and its size, the stream, the
+// device error flag, and the context whose phase timers apply (null: none).
+struct Exec {
+  char* scratch;
+  size_t limit;
+  hipStream_t stream;
+  int* err;
+  uocr_gpu_ctx* timing;
+};
+
+Exec exec_of(uocr_gpu_ctx* ctx) {
+  return {ctx->scratch, ctx->scratch_limit, ctx->stream, ctx->err, ctx};
+}
+
+Scratch carve(const Exec& ex, const ScratchPlan& p) {
   Scratch s{};
-  char* b = ctx->scratch;
+  char* b = ex.scratch;
   s.logits = reinterpret_cast<float*>(b + p.logits);
   s.topk_ids = reinterpret_cast<int*>(b + p.ids);
   s.topk_w = reinterpret_cast<float*>(b + p.w);
@@ -208,7 +225,7 @@ Scratch carve(uocr_gpu_ctx* ctx, const ScratchPlan& p) {
   s.xn = reinterpret_cast<float*>(b + p.xn);
   s.xb = reinterpret_cast<uint16_t*>(b + p.xb);
   s.gu = reinterpret_cast<float*>(b + p.gu);
-  s.err = ctx->err;
+  s.err = ex.err;
   return s;
 }
 
@@ -321,21 +338,22 @@ void input_planes(const Scratch& S, const DeviceLayer& L, size_t T, uint32_t fla
 // planes_ready: the MFMA engine's input planes are already in scratch.
 // next: the following layer's RMSNorm, fused into this layer's combine (not
 // taken by the decode engine; *fused says whether it ran).
-int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
+int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x, size_t T,
                     const float* residual, float* y, uint32_t flags,
                     const uocr_moe_trace* trace, bool x_in_scratch, bool planes_ready = false,
                     const uocr::RowNorm* next = nullptr, bool* fused = nullptr) {
   if (fused) *fused = false;
+  uocr_gpu_ctx* ctx = ex.timing;  // phase timers only
   const uocr_moe_config& c = layer->cfg;
   const ScratchPlan plan = plan_scratch(c, T);
-  if (plan.total > ctx->scratch_limit)
+  if (plan.total > ex.limit)
     return fail(UOCR_ERR_RESOURCE, "operation exceeds scratch limit (%zu > %zu bytes)",
-                plan.total, ctx->scratch_limit);
-  Scratch S = carve(ctx, plan);
+                plan.total, ex.limit);
+  Scratch S = carve(ex, plan);
   if (!x_in_scratch) S.xn = const_cast<float*>(x);
   const DeviceLayer& L = layer->dev;
   const int Ti = (int)T;
-  hipStream_t st = ctx->stream;
+  hipStream_t st = ex.stream;
   const uocr_w8a8_trace* q8t =
       trace && L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS ? trace->w8a8 : nullptr;
   if (q8t) {
@@ -479,6 +497,36 @@ int enqueue_experts(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float*
     if ((r = copy(trace->perm_rows, S.perm_rows, TK * 4))) return r;
     if ((r = copy(trace->perm_weights, S.perm_w, TK * 4))) return r;
   }
+  return UOCR_OK;
+}
+
+// ------------------------------------------------ allocation-free forward
+//
+// Scratch of uocr_moe_forward_static: one array of UOCR_STATIC_SCRATCH_BYTES
+// per GPU, held until the process ends. Its first 256 bytes hold the device
+// error flag when the caller passes none; the forward's scratch follows. In
+// host code `scratch` only names the host-side stand-in: the device address
+// comes from hipGetSymbolAddress, once per device, and only that address is
+// ever passed to kernels.
+
+constexpr int kMaxStaticDevices = 64;
+constexpr size_t kStaticFlagBytes = 256;
+std::mutex g_static_mu;
+char* g_static_base[kMaxStaticDevices] = {};
+
+__global__ void clear_flag_kernel(int* flag) { *flag = 0; }
+
+// The device address of this device's array (the device must be current).
+int static_scratch_of(int device, char** out) {
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (device < 0 || device >= kMaxStaticDevices)
+    return fail(UOCR_ERR_UNSUPPORTED, "static scratch supports devices 0..%d", kMaxStaticDevices - 1);
+  if (!g_static_base[device]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address");
+    g_static_base[device] = static_cast<char*>(p);
+  }
+  *out = g_static_base[device];
   return UOCR_OK;
 }
 
@@ -791,7 +839,7 @@ int uocr_moe_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu > %zu)", T,
                 max_tokens(layer->cfg));
   HIP_TRY(hipSetDevice(ctx->device), "set device");
-  return enqueue_experts(ctx, layer, x, T, nullptr, y, flags, trace, false);
+  return enqueue_experts(exec_of(ctx), layer, x, T, nullptr, y, flags, trace, false);
 }
 
 int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float* x, size_t T,
@@ -799,6 +847,35 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
   int r = uocr_moe_forward_async(ctx, layer, x, T, y, flags, trace);
   if (r) return r;
   return read_and_clear_error(ctx);
+}
+
+int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t T, float* y,
+                            uint32_t flags, int32_t* device_status, void* stream) {
+  if (!layer) return fail(UOCR_ERR_SHAPE, "null handle");
+  if (T == 0) return UOCR_OK;
+  if (!x || !y) return fail(UOCR_ERR_SHAPE, "null activation pointer");
+  if (T > max_tokens(layer->cfg))
+    return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu > %zu)", T,
+                max_tokens(layer->cfg));
+  const size_t need = plan_scratch(layer->cfg, T).total;
+  const size_t have = (size_t)UOCR_STATIC_SCRATCH_BYTES - kStaticFlagBytes;
+  if (need > have)
+    return fail(UOCR_ERR_RESOURCE,
+                "a forward of %zu tokens needs %zu scratch bytes; the static scratch holds %zu", T,
+                need, have);
+  HIP_TRY(hipSetDevice(layer->device), "set device");
+  std::call_once(g_attr_once, [] {
+    uocr::gemv_init_attributes();
+    uocr::mfma_init_attributes();
+  });
+  char* base = nullptr;
+  if (int r = static_scratch_of(layer->device, &base)) return r;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int* err = device_status ? reinterpret_cast<int*>(device_status) : reinterpret_cast<int*>(base);
+  // A fill kernel, not a memset, so that graph capture records a kernel node.
+  hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(1), 0, st, err);
+  const Exec ex{base + kStaticFlagBytes, have, st, err, nullptr};
+  return enqueue_experts(ex, layer, x, T, nullptr, y, flags, nullptr, false);
 }
 
 int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const* layers,
@@ -841,7 +918,7 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
   for (size_t l = 0; l < n_layers; l++) {
     const uocr_moe_layer* layer = layers[l];
     const ScratchPlan plan = plan_scratch(layer->cfg, T);
-    Scratch S = carve(ctx, plan);
+    Scratch S = carve(exec_of(ctx), plan);
     const uocr::RowNorm nn = norm_of(l, S);
     if (!normed) {
       phase_begin(ctx, kNorm);
@@ -861,8 +938,8 @@ int uocr_moe_block_forward_async(uocr_gpu_ctx* ctx, const uocr_moe_layer* const*
       }
     }
     bool fused = false;
-    int r = enqueue_experts(ctx, layer, S.xn, T, cur, y, flags, nullptr, true, nn.hi != nullptr,
-                            want ? &next : nullptr, &fused);
+    int r = enqueue_experts(exec_of(ctx), layer, S.xn, T, cur, y, flags, nullptr, true,
+                            nn.hi != nullptr, want ? &next : nullptr, &fused);
     if (r) return r;
     normed = fused;
     cur = y;

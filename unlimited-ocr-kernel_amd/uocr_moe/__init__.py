@@ -42,7 +42,8 @@ EXPORTS = [
     "uocr_gpu_ctx_set_timing", "uocr_gpu_ctx_timings",
     "uocr_moe_layer_create", "uocr_moe_layer_attach_int8", "uocr_moe_layer_precision",
     "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
-    "uocr_moe_forward", "uocr_moe_block_forward", "uocr_moe_block_forward_async", "uocr_route",
+    "uocr_moe_forward", "uocr_moe_forward_static", "uocr_moe_block_forward",
+    "uocr_moe_block_forward_async", "uocr_route",
     "uocr_linear_bf16", "uocr_int8_linear", "uocr_int8_linear_dynamic", "uocr_rms_norm",
     "uocr_checkpoint_open", "uocr_checkpoint_close", "uocr_checkpoint_sha256",
     "uocr_checkpoint_count", "uocr_checkpoint_name", "uocr_checkpoint_metadata",
@@ -147,6 +148,7 @@ def _load():
         "uocr_moe_forward_async": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _U32,
                                                   ctypes.POINTER(Trace)]),
         "uocr_moe_forward": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _U32, ctypes.POINTER(Trace)]),
+        "uocr_moe_forward_static": (ctypes.c_int, [_P, _P, _SZ, _P, _U32, _P, _P]),
         "uocr_moe_block_forward": (ctypes.c_int, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ, _P,
                                                   _U32]),
         "uocr_moe_block_forward_async": (ctypes.c_int, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ,
@@ -329,6 +331,19 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
     fn = lib.uocr_moe_forward if sync else lib.uocr_moe_forward_async
     _check(fn(ctx.handle, layer.handle, _ptr(x), T, _ptr(y), flags,
               ctypes.byref(tr) if tr is not None else None))
+
+
+STATIC_SCRATCH_BYTES = 16 << 20
+
+
+def forward_static(layer: MoeLayer, x, y, flags: int = 0, status=None, stream=None):
+    """uocr_moe_forward_static: the allocation-free forward, enqueued on
+    `stream` (a torch.cuda.Stream, or None for the null stream). `status`:
+    optional device int32 tensor that receives device-side error codes."""
+    T = x.shape[0]
+    handle = stream.cuda_stream if stream is not None else None
+    _check(lib.uocr_moe_forward_static(layer.handle, _ptr(x), T, _ptr(y), flags, _ptr(status),
+                                       handle))
 
 
 class LmHead:
