@@ -49,7 +49,7 @@ GATEUP_FLOP_PER_TOKEN = 2 * H * (K * 2 * I + 2 * S)
 ROUTER_BYTES = E * H * 2
 # Host threads of one GPU's share of the box (the oracle's CPU baseline).
 CPU_THREADS = 16
-TRAFFIC_PROFILE = "profiles/gateup_fp32class_stack_T4096_counters.md"
+TRAFFIC_PROFILE = "profiles/prefill_stack_T4096_counters.md"
 TRAFFIC_KERNEL = "mfma_group_kernel<32, 3, 3, true, true, false, true, false>"
 
 
@@ -153,20 +153,17 @@ def main():
     secondary = []
     if args.layers > 0:
         log("generating the 12-layer stack (T=4096, 80% to 8 hot experts)")
-        hot = syn.route_profile(syn.hot_share(E, K, 8, 0.8), K)
         layers = []
         for l in range(args.layers):
-            w = syn.moe_weights_device(H, I, E, SH, seed=1000 + l, router_scale=hot, norm=True)
+            w = syn.hot_stack_layer_device(H, I, E, SH, K, l)
             torch.cuda.synchronize()  # the library copies on its own stream
             layers.append(um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE))
             if args.check_rows > 0 or (l == 0 and args.cpu_sample > 0):
                 host_layers.append({k: v.cpu().numpy().view(np.uint16) for k, v in w.items()})
             del w
         torch.cuda.empty_cache()
-        g = torch.Generator(device="cuda")
-        g.manual_seed(1)
         T = 4096
-        x = torch.randn((T, H), generator=g, device="cuda")
+        x = syn.hot_stack_input_device(T, H, seed=1)
         y = torch.empty_like(x)
 
         def run_stack(flags):
@@ -230,6 +227,24 @@ def main():
                               "max_normwise": err, "bar": 1e-3,
                               "ok": bool(err is not None and err <= 1e-3)}
             log(f"headline parity: {err:.3e} over {int(keep.sum())} rows")
+        # Realised routing of every layer: the share of assignments on the 8
+        # hot experts and the largest and smallest expert groups, from a
+        # traced forward of layer l on the normalised output of layers < l.
+        shares = []
+        cur = x.clone()
+        xn = torch.empty_like(x)
+        offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        ones = torch.ones(H, device="cuda")
+        for l, layer in enumerate(layers):
+            um.rms_norm(ctx, cur, ones, 1e-6, xn)
+            um.forward(ctx, layer, xn, y, trace={"expert_offsets": offs})
+            c = np.diff(offs.cpu().numpy())
+            shares.append([round(float(c[:8].sum()) / (T * K), 4), int(c.max()), int(c.min())])
+            um.block_forward(ctx, [layer], cur, cur)
+        head["routing"] = {"hot_share_per_layer": [v[0] for v in shares],
+                           "max_rows_per_layer": [v[1] for v in shares],
+                           "min_rows_per_layer": [v[2] for v in shares]}
+        log(f"realised hot shares: {[v[0] for v in shares]}")
         # BF16-rounded activations on the same stack: a labelled secondary
         # (the 2e-2 class; the reference never rounds activations).
         ms_b, gate_b, phases_b = run_stack(um.FLAG_BF16_ACTIVATIONS)
@@ -375,6 +390,12 @@ def main():
         gen.manual_seed(0)
         xp = torch.randn((1024, H), generator=gen, device="cuda")
         yp = torch.empty_like(xp)
+        offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        um.forward(ctx, layer, xp, yp, trace={"expert_offsets": offs})
+        zc = np.sort(np.diff(offs.cpu().numpy()))[::-1]
+        zipf_real = {"rows_per_expert_desc": zc.tolist(),
+                     "top1_token_share": round(float(zc[0]) / 1024, 4),
+                     "top8_assignment_share": round(float(zc[:8].sum()) / (1024 * K), 4)}
         for fl, cls in ((um.FLAG_FP32_CLASS, "fp32-class"), (um.FLAG_BF16_ACTIVATIONS, "bf16")):
             for _ in range(args.warmup):
                 um.forward(ctx, layer, xp, yp, flags=fl, sync=False)
@@ -392,7 +413,8 @@ def main():
                 "ms_per_step": round(ms, 4),
                 "hbm_frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                 "mfma_frac": round(FLOP_PER_TOKEN * 1024 / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS,
-                                   4)})
+                                   4),
+                "routing": zipf_real})
             log(f"prefill1024 {cls}: {ms:.3f} ms")
         layer.close()
 
@@ -564,6 +586,7 @@ def main():
             "layer_frac": round(head["layer_tflops"] / BF16_PEAK_TFLOPS, 4)},
         "phases_ms_per_step": head.get("phases"),
         "parity": head.get("parity"),
+        "routing": head.get("routing"),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -3,8 +3,9 @@
 
 Stack: 12 x [RMSNorm (eps 1e-6, weight ones) + MoE + residual]
 (src/decoder/mod.rs:351-363) over 4096 tokens, BF16 weights N(0, 0.02) with
-distinct per-layer streams, 80% of assignments on 8 hot experts — the
-workload bench.py times, built the same way. Rows are independent through
+distinct per-layer streams, 80% of assignments on 8 hot experts at every
+layer (router rows of the hot experts tilted toward a direction the input's
+mean follows) — the workload bench.py times, built the same way. Rows are independent through
 the stack, so a seeded sample of rows runs through the oracle's chain of
 rms_norm + experts (src/decoder/mod.rs:124-220). Two checks:
   * teacher-forced, per layer: the oracle applies layer l to the GPU's own
@@ -65,10 +66,9 @@ class Stack:
     def __init__(self, ctx):
         say(f"building the {LAYERS}-layer stack (T={T_STACK}, 80% of assignments on 8 experts)")
         cfg = um.config(H, I, E, SH, K, normalize=True)
-        hot = syn.route_profile(syn.hot_share(E, K, 8, 0.8), K)
         self.layers, self.host = [], []
         for l in range(LAYERS):
-            w = syn.moe_weights_device(H, I, E, SH, seed=1000 + l, router_scale=hot, norm=True)
+            w = syn.hot_stack_layer_device(H, I, E, SH, K, l)
             torch.cuda.synchronize()
             self.layers.append(um.MoeLayer(ctx, cfg, w, um.MEMORY_DEVICE))
             hw = {k: v.cpu().numpy().view(np.uint16) for k, v in w.items()}
@@ -79,9 +79,7 @@ class Stack:
                 shared_down=hw["shared_down"]))
             del w
         torch.cuda.empty_cache()
-        g = torch.Generator(device="cuda")
-        g.manual_seed(1)
-        self.x = torch.randn((T_STACK, H), generator=g, device="cuda")
+        self.x = syn.hot_stack_input_device(T_STACK, H, seed=1)
         self.rows = np.sort(np.random.default_rng(2024).choice(T_STACK, ROWS, replace=False))
         self.norm = np.ones(H, np.float32)
 
@@ -108,18 +106,26 @@ def stack(ctx):
 
 
 def test_headline_stack_shapes(ctx, stack):
-    """The workload reaches the GEMM shapes it is meant to: hot experts span
-    several 256-row tiles (and more than 2048 rows in total), cold experts
-    fill one small tile."""
-    xd = stack.x.clone()
-    yd = torch.empty_like(xd)
+    """The workload is what it claims at every layer: 80% (within 0.06) of
+    the assignments on the 8 hot experts, which span several 256-row tiles
+    (more than 2048 rows each), while each of the 56 cold experts fits one
+    256-row tile."""
+    cur = stack.x.clone()
+    xn = torch.empty_like(cur)
+    yd = torch.empty_like(cur)
     offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
-    um.forward(ctx, stack.layers[0], xd, yd, trace={"expert_offsets": offs})
-    counts = np.diff(offs.cpu().numpy())
-    say(f"  layer-0 expert rows: max {counts.max()} min {counts.min()}, "
-        f"hot share {np.sort(counts)[::-1][:8].sum() / counts.sum():.3f}")
-    assert counts.sum() == T_STACK * K
-    assert (counts > 2048).sum() >= 4 and (counts <= 128).sum() >= 32
+    ones = torch.ones(H, device="cuda")
+    for l, layer in enumerate(stack.layers):
+        um.rms_norm(ctx, cur, ones, EPS, xn)
+        um.forward(ctx, layer, xn, yd, trace={"expert_offsets": offs})
+        counts = np.diff(offs.cpu().numpy())
+        share = counts[:8].sum() / counts.sum()
+        say(f"  layer {l}: hot share {share:.3f}, hot rows {counts[:8].min()}..{counts[:8].max()}, "
+            f"cold rows {counts[8:].min()}..{counts[8:].max()}")
+        assert counts.sum() == T_STACK * K
+        assert abs(share - 0.8) <= 0.06, (l, share)
+        assert (counts[:8] > 2048).all() and (counts[8:] <= 256).all(), (l, counts)
+        um.block_forward(ctx, [layer], cur, cur)
 
 
 @pytest.mark.parametrize("flags,tol", [(um.FLAG_FP32_CLASS, FP32_TOL),
@@ -203,7 +209,8 @@ def test_zipf_prefill_1024(ctx, zipf_case, flags, tol):
     g = {k: v.cpu().numpy() for k, v in tr.items()}
     counts = np.diff(rtr.expert_offsets)
     say(f"  Zipf rows per expert: max {counts.max()} min {counts.min()}")
-    assert counts.max() > 256 and counts.min() < 64
+    # The capped Zipf(1.1) head (at most 45% of tokens per expert), a long tail.
+    assert 300 < counts.max() < 0.5 * T and counts.min() < 64
     # Routing: identical sets except for logit ties within 1e-6.
     ties = []
     for t in range(T):

@@ -3,10 +3,20 @@
 Weights follow the benchmark definitions: BF16 N(0, 0.02) rounded to nearest
 even; INT8 overlay int8 uniform in [-127, 127] with per-32-block scales
 |N(0.002, 0.0005)|; activations N(0, 1). The router has no bias
-(src/decoder/mod.rs:126 passes bias None), so expert popularity is shaped by
-scaling router rows: a larger row norm gives an expert larger logits more
-often. `route_profile` calibrates those scales by Monte Carlo so that the
-share of tokens routing to each expert matches a target.
+(src/decoder/mod.rs:126 passes bias None), so expert popularity is shaped
+through the router rows:
+
+* `route_profile` scales router rows (a larger row norm gives an expert
+  larger logits more often), calibrated by Monte Carlo to target shares.
+  With zero-mean inputs every logit is symmetric, so an expert is chosen by
+  at most half of the tokens: targets are capped below that (`zipf_share`'s
+  cap). Scaling past it only makes the other experts' softmax probabilities
+  underflow to exact zeros, which moe::route then breaks by lowest id.
+* `hot_tilt` reaches shares above one half: the hot experts' router rows
+  are tilted toward a unit direction d and the input carries a small mean
+  mu * d (|mu d| = 4 against |z| = sqrt(H) for z ~ N(0, 1)), so the hot
+  logits have a positive mean. The tilts are calibrated for the effective
+  mean a layer of the residual stack sees after RMSNorm.
 """
 from __future__ import annotations
 
@@ -28,21 +38,27 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
 
 # ------------------------------------------------------------ route shaping
 
-def zipf_share(n_experts: int, top_k: int, s: float = 1.1) -> np.ndarray:
-    """Capped Zipf(s) share q_e = min(1, c * rank^-s) with sum q_e = top_k.
+ZIPF_CAP = 0.45
 
-    A token picks top_k distinct experts, so no expert can be chosen by more
-    than every token; c is found by bisection.
+
+def zipf_share(n_experts: int, top_k: int, s: float = 1.1, cap: float = ZIPF_CAP) -> np.ndarray:
+    """Capped Zipf(s) share q_e = min(cap, c * rank^-s) with sum q_e = top_k.
+
+    q_e is the fraction of tokens that choose expert e. A token picks top_k
+    distinct experts, and with zero-mean N(0, 1) inputs (as the 1024-token
+    prefill specifies) a router row can win at most half of the tokens, so
+    the head of the distribution is capped just below that; c is found by
+    bisection.
     """
     ranks = np.arange(1, n_experts + 1, dtype=np.float64)
     lo, hi = 0.0, float(top_k) * 10
     for _ in range(200):
         c = 0.5 * (lo + hi)
-        if np.minimum(1.0, c * ranks ** -s).sum() > top_k:
+        if np.minimum(cap, c * ranks ** -s).sum() > top_k:
             hi = c
         else:
             lo = c
-    return np.minimum(1.0, lo * ranks ** -s)
+    return np.minimum(cap, lo * ranks ** -s)
 
 
 def hot_share(n_experts: int, top_k: int, hot: int = 8, fraction: float = 0.8) -> np.ndarray:
@@ -54,8 +70,11 @@ def hot_share(n_experts: int, top_k: int, hot: int = 8, fraction: float = 0.8) -
 
 
 def route_profile(target: np.ndarray, top_k: int, samples: int = 16384, iters: int = 60,
-                  seed: int = 12345) -> np.ndarray:
-    """Row-norm multipliers whose Gaussian logits reproduce `target` shares."""
+                  seed: int = 12345, max_ratio: float = 30.0) -> np.ndarray:
+    """Row-norm multipliers whose Gaussian logits reproduce `target` shares
+    (each at most one half). The multipliers stay within a factor
+    `max_ratio` of their geometric mean, so softmax probabilities never
+    underflow to ties."""
     rng = np.random.default_rng(seed)
     E = target.size
     z = rng.standard_normal((samples, E)).astype(np.float32)
@@ -66,20 +85,66 @@ def route_profile(target: np.ndarray, top_k: int, samples: int = 16384, iters: i
         share = np.bincount(top.ravel(), minlength=E) / samples
         f *= np.clip((np.maximum(target, 1e-4) / np.maximum(share, 1e-4)) ** 0.35, 0.8, 1.25)
         f /= np.exp(np.mean(np.log(f)))
+        f = np.clip(f, 1.0 / max_ratio, max_ratio)
     return f
+
+
+# Input mean of the hot-expert workload along the tilt direction, and the
+# growth of the residual stream's mean square per layer of the 12-layer
+# stack (each layer adds a nearly independent output of rms 0.256 to rows of
+# rms 1), which dilutes the normalised mean the deeper layers see.
+HOT_MEAN = 4.0
+STACK_GROWTH = 0.0655
+
+
+def tilt_direction(hidden: int, seed: int = 4242) -> np.ndarray:
+    """The unit direction d of the hot-expert tilt (float32)."""
+    d = np.random.default_rng(seed).standard_normal(hidden)
+    return (d / np.linalg.norm(d)).astype(np.float32)
+
+
+def hot_tilt(target: np.ndarray, top_k: int, hidden: int, layer: int = 0,
+             mean: float = HOT_MEAN, samples: int = 16384, iters: int = 80,
+             seed: int = 7) -> np.ndarray:
+    """Tilts beta_e (router row e gets beta_e * d added before the 0.02
+    scale) so that layer `layer` of the stack routes `target` shares.
+
+    Model: after RMSNorm a row is z + m d with z ~ N(0, 1) and
+    m = mean / sqrt(1 + layer * STACK_GROWTH); logit_e / 0.02 =
+    g_e . z + beta_e (m + d . z), with g_e . z ~ N(0, hidden) independent
+    per expert and d . z ~ N(0, 1) shared. Monte Carlo, additive updates."""
+    rng = np.random.default_rng(seed)
+    E = target.size
+    m = mean / np.sqrt(1.0 + layer * STACK_GROWTH)
+    n = rng.standard_normal((samples, E)) * np.sqrt(hidden)
+    w = rng.standard_normal((samples, 1))
+    beta = np.zeros(E)
+    for _ in range(iters):
+        logits = n + beta[None, :] * (m + w)
+        top = np.argpartition(-logits, top_k - 1, axis=1)[:, :top_k]
+        share = np.bincount(top.ravel(), minlength=E) / samples
+        beta += 8.0 * (target - share)
+    return beta
 
 
 # --------------------------------------------------------------- host (numpy)
 
-def moe_weights(hidden, inter, experts, shared, seed, router_scale=None, norm=False):
-    """BF16 bits of one MoE layer in checkpoint layout, from a numpy stream."""
+def moe_weights(hidden, inter, experts, shared, seed, router_scale=None, norm=False,
+                router_tilt=None):
+    """BF16 bits of one MoE layer in checkpoint layout, from a numpy stream.
+    router_tilt: (beta [E], d [hidden]) adds beta_e * d to router row e
+    before the 0.02 scale."""
     rng = np.random.default_rng(seed)
     S = inter * shared
 
     def normal(shape):
         return f32_to_bf16_bits(rng.standard_normal(shape, dtype=np.float32) * BF16_STD)
 
-    router = rng.standard_normal((experts, hidden), dtype=np.float32) * BF16_STD
+    router = rng.standard_normal((experts, hidden), dtype=np.float32)
+    if router_tilt is not None:
+        beta, d = router_tilt
+        router += np.asarray(beta, np.float32)[:, None] * np.asarray(d, np.float32)[None, :]
+    router *= BF16_STD
     if router_scale is not None:
         router *= np.asarray(router_scale, np.float32)[:, None]
     w = {
@@ -123,7 +188,7 @@ def activations(T, hidden, seed):
 # ------------------------------------------------------------ device (torch)
 
 def moe_weights_device(hidden, inter, experts, shared, seed, router_scale=None, norm=False,
-                       device="cuda"):
+                       device="cuda", router_tilt=None):
     """Same distributions generated on the GPU with torch (bench plumbing)."""
     import torch
 
@@ -135,7 +200,12 @@ def moe_weights_device(hidden, inter, experts, shared, seed, router_scale=None, 
         t = torch.randn(shape, generator=g, device=device, dtype=torch.float32) * BF16_STD
         return t.to(torch.bfloat16).view(torch.int16)
 
-    router = torch.randn((experts, hidden), generator=g, device=device) * BF16_STD
+    router = torch.randn((experts, hidden), generator=g, device=device)
+    if router_tilt is not None:
+        beta, d = router_tilt
+        router += (torch.as_tensor(np.asarray(beta, np.float32), device=device)[:, None]
+                   * torch.as_tensor(np.asarray(d, np.float32), device=device)[None, :])
+    router *= BF16_STD
     if router_scale is not None:
         router *= torch.as_tensor(np.asarray(router_scale, np.float32), device=device)[:, None]
     w = {
@@ -173,3 +243,25 @@ def int8_overlay_device(hidden, inter, experts, shared, seed, device="cuda"):
         "shared_up": mat((S, hidden)),
         "shared_down": mat((hidden, S)),
     }
+
+
+def hot_stack_layer_device(hidden, inter, experts, shared, top_k, layer, hot=8, fraction=0.8,
+                           seed_base=1000, device="cuda"):
+    """Layer `layer` of the hot-expert stack: BF16 weights from the seeded
+    stream seed_base + layer, the router tilted so that `fraction` of the
+    assignments reach the first `hot` experts at that depth, norm weight
+    ones."""
+    beta = hot_tilt(hot_share(experts, top_k, hot, fraction), top_k, hidden, layer)
+    return moe_weights_device(hidden, inter, experts, shared, seed=seed_base + layer, norm=True,
+                              device=device, router_tilt=(beta, tilt_direction(hidden)))
+
+
+def hot_stack_input_device(T, hidden, seed=1, device="cuda"):
+    """The hot-expert stack's input: N(0, 1) rows plus HOT_MEAN * d."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    x = torch.randn((T, hidden), generator=g, device=device)
+    d = torch.as_tensor(tilt_direction(hidden), device=device)
+    return x + HOT_MEAN * d[None, :]
