@@ -64,8 +64,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--secondary",
                     default="decode_int8,decode_bf16,decode_int8_t16,prefill1024,"
-                            "prefill_w8a8_t512,prefill_int8_t512,lm_head_bf16,lm_head_int8,"
-                            "lm_head_w8a8",
+                            "prefill_w8a8_t512,prefill_int8_t512,prefill_w8a8_int8mfma_t512,"
+                            "lm_head_bf16,lm_head_int8,lm_head_w8a8",
                     help="comma list of secondary workloads, or 'none'")
     ap.add_argument("--cpu-sample", type=int, default=512,
                     help="tokens of the headline workload timed on the CPU oracle at 1 thread "
@@ -419,12 +419,16 @@ def main():
         layer.close()
 
     # ------------------------------------- INT8 prefill (weight-only, W8A8)
-    def prefill_int8(quant: int):
+    def prefill_int8(quant: int, flags: int = 0):
         """The INT8-overlay layer at T=512 with uniform-random routing
         (random router rows, no popularity bias): multi-row groups run the
         weight-only dequant (FP32 math), single-row groups W8A8 under
-        DynamicActivations (src/decoder/mod.rs:103-104)."""
+        DynamicActivations (src/decoder/mod.rs:103-104). With
+        FLAG_INT8_MFMA (an opt-in extension) every group runs W8A8 on the
+        int8 MFMA."""
         kind = "w8a8" if quant == um.QUANT_DYNAMIC else "int8"
+        if flags & um.FLAG_INT8_MFMA:
+            kind = "w8a8-all-groups-int8-mfma"
         T = 512
         log(f"prefill {kind} T={T}, uniform routing")
         w = syn.moe_weights_device(H, I, E, SH, seed=3)
@@ -441,11 +445,11 @@ def main():
         xp = torch.randn((T, H), generator=gen, device="cuda")
         yp = torch.empty_like(xp)
         for _ in range(args.warmup):
-            um.forward(ctx, layer, xp, yp, sync=False)
+            um.forward(ctx, layer, xp, yp, flags=flags, sync=False)
         sync()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            um.forward(ctx, layer, xp, yp, sync=False)
+            um.forward(ctx, layer, xp, yp, flags=flags, sync=False)
         sync()
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         layer.close()
@@ -459,10 +463,11 @@ def main():
                 "hbm_frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                 "mfma_frac": round(FLOP_PER_TOKEN * T / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
 
-    for key, quant in (("prefill_w8a8_t512", um.QUANT_DYNAMIC),
-                       ("prefill_int8_t512", um.QUANT_WEIGHTS_ONLY)):
+    for key, quant, fl in (("prefill_w8a8_t512", um.QUANT_DYNAMIC, 0),
+                           ("prefill_int8_t512", um.QUANT_WEIGHTS_ONLY, 0),
+                           ("prefill_w8a8_int8mfma_t512", um.QUANT_DYNAMIC, um.FLAG_INT8_MFMA)):
         if key in wanted:
-            secondary.append(prefill_int8(quant))
+            secondary.append(prefill_int8(quant, fl))
 
     # ------------------------------------------------ vocabulary projection
     def lm_head(kind: str):

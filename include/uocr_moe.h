@@ -64,6 +64,14 @@ typedef enum uocr_memory {
 /* Force one expert engine, for tests: 0 = choose by token count. */
 #define UOCR_FLAG_FORCE_GEMV 2u
 #define UOCR_FLAG_FORCE_MFMA 4u
+/* Opt-in extension for DynamicActivations layers (else Unsupported): every
+ * expert group, whatever its row count, computes as
+ * Int8Matrix::linear_dynamic_int8 row by row (activations quantised per
+ * 32-block, int8 x int8 products with exact int32 block sums on the int8
+ * MFMA). The reference does this for single-row groups only
+ * (src/decoder/mod.rs:103-104), so for multi-row groups the results differ
+ * from it by the activation rounding (the W8A8 tolerance class). */
+#define UOCR_FLAG_INT8_MFMA 8u
 
 /* The MoE fields of ModelConfig (src/model/config.rs:35-54). */
 typedef struct uocr_moe_config {

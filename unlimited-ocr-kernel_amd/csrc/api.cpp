@@ -156,7 +156,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
-      h, hs, y, ys, xn, xb, gu, total;
+      h, hs, y, ys, xn, xb, gu, q8x, q8s, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -187,6 +187,11 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   p.xn = take(T * H * 4);
   p.xb = take(T * H * 4);
   p.gu = take((T * K * 2 * I + T * 2 * S) * 4);
+  // Int8 mode: the quantised input [T, H] and hidden rows [T*K*I + T*S],
+  // and their block scales.
+  const size_t q8_elems = T * H + T * K * I + T * S;
+  p.q8x = take(q8_elems);
+  p.q8s = take(q8_elems / 32 * 4);
   p.total = at;
   return p;
 }
@@ -225,6 +230,8 @@ Scratch carve(const Exec& ex, const ScratchPlan& p) {
   s.xn = reinterpret_cast<float*>(b + p.xn);
   s.xb = reinterpret_cast<uint16_t*>(b + p.xb);
   s.gu = reinterpret_cast<float*>(b + p.gu);
+  s.q8x = reinterpret_cast<int8_t*>(b + p.q8x);
+  s.q8s = reinterpret_cast<float*>(b + p.q8s);
   s.err = ex.err;
   return s;
 }
@@ -314,10 +321,14 @@ int read_and_clear_error(uocr_gpu_ctx* ctx) {
 // grouped GEMM for larger batches (INT8 overlays streamed as int8 rows and
 // dequantised in registers; under DynamicActivations the single-row groups
 // still take the small-batch engine's W8A8 path).
-enum class Engine { Decode, Batch, Mfma };
+enum class Engine { Decode, Batch, Mfma, Int8 };
 
 Engine choose_engine(const uocr_moe_layer* layer, size_t T, uint32_t flags) {
   const DeviceLayer& L = layer->dev;
+  // The opt-in int8 mode: every group W8A8; one token already is on the
+  // decode engine.
+  if (flags & UOCR_FLAG_INT8_MFMA)
+    return T == 1 && uocr::decode_supported(L) ? Engine::Decode : Engine::Int8;
   const bool mfma = (flags & UOCR_FLAG_FORCE_MFMA) ||
                     (!(flags & UOCR_FLAG_FORCE_GEMV) && T > (size_t)uocr::kGemvChunk);
   if (mfma) return Engine::Mfma;
@@ -377,8 +388,14 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
               "trace copy");
     return UOCR_OK;
   };
+  if ((flags & UOCR_FLAG_INT8_MFMA) && L.quant_mode != UOCR_QUANT_DYNAMIC_ACTIVATIONS)
+    return fail(UOCR_ERR_UNSUPPORTED,
+                "int8 activations need an INT8 overlay in DynamicActivations mode");
   const Engine engine = choose_engine(layer, T, flags);
+  if (engine == Engine::Int8 && !uocr::i8_supported(L))
+    return fail(UOCR_ERR_UNSUPPORTED, "int8 engine needs widths that are multiples of 64");
   const bool mfma = engine == Engine::Mfma;
+  const bool int8 = engine == Engine::Int8;
   // The small-batch engine also takes the single-row W8A8 groups of the
   // MFMA engine.
   if ((!mfma || L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS) && !uocr::batch_supported(L))
@@ -386,7 +403,7 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
                 "small-batch engine needs widths <= 2048, expert and shared widths that are "
                 "multiples of 16 and a hidden width that is a multiple of 32");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
-  const int bm = mfma ? uocr::kMfmaBM : uocr::kGemvChunk;
+  const int bm = mfma ? uocr::kMfmaBM : int8 ? uocr::kI8BM : uocr::kGemvChunk;
   // The MFMA engine may run an expert's last tile of <= 128 rows as 128 x 512
   // items and one of <= 64 rows as 64 x 1024 items.
   const int narrow = mfma ? uocr::kMfmaBM / 2 : 0;
@@ -404,7 +421,7 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
     phase_end(ctx);
     if (int r = trace_hidden(S.gu, S.gu + (size_t)L.K * L.I)) return r;
   } else {
-    if (T <= (size_t)uocr::kGemvChunk && !mfma) {
+    if (T <= (size_t)uocr::kGemvChunk && !mfma && !int8) {
       // Few tokens: logits with every token staged once, then one
       // workgroup routes them and builds the dispatch.
       phase_begin(ctx, kRouter);
@@ -436,7 +453,34 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
                             S.perm_w, S.inv_pos, S.tiles, S.counters, st);
       phase_end(ctx);
     }
-    if (mfma) {
+    if (int8) {
+      // Quantise the input rows, gate/up into FP32 hidden rows, quantise
+      // those, down.
+      uocr::I8Planes P;
+      const size_t routed_rows = T * L.K;
+      P.xq = S.q8x;
+      P.xs = S.q8s;
+      P.hid = S.h;
+      P.hid_shared = S.hs;
+      P.hid_q = S.q8x + T * L.H;
+      P.hid_s = S.q8s + T * L.H / 32;
+      phase_begin(ctx, kSplit);
+      uocr::launch_quantize_rows(S.xn, Ti, L.H, S.q8x, S.q8s, nullptr, 0, 32, nullptr, nullptr,
+                                 S.err, st);
+      phase_end(ctx);
+      phase_begin(ctx, kGateUp);
+      uocr::launch_i8_gateup(L, S, P, Ti, tiles_bound, st);
+      phase_end(ctx);
+      if (int r = trace_hidden(S.h, S.hs)) return r;
+      phase_begin(ctx, kSplit);
+      uocr::launch_quantize_rows(S.h, (int)routed_rows, L.I, P.hid_q, P.hid_s, S.hs, Ti, L.S,
+                                 P.hid_q + routed_rows * L.I, P.hid_s + routed_rows * L.I / 32,
+                                 S.err, st);
+      phase_end(ctx);
+      phase_begin(ctx, kDown);
+      uocr::launch_i8_down(L, S, P, Ti, tiles_bound, st);
+      phase_end(ctx);
+    } else if (mfma) {
       uocr::MfmaPlanes P;
       P.x_hi = S.xb;
       P.x_lo = S.xb + T * L.H;

@@ -75,6 +75,8 @@ struct Scratch {
   float* xn;        // [T, H] normalised block input
   uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
   float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
+  int8_t* q8x;      // int8 mode: quantised input [T, H] and hidden rows [T*K*I + T*S]
+  float* q8s;       // int8 mode: their block scales [T*H/32 + (T*K*I + T*S)/32]
   int* err;         // device error flag
   Q8Trace q8;       // W8A8 trace (tests), all null by default
 };
@@ -143,6 +145,26 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
                       int tiles_bound, bool bf16_only, hipStream_t s);
 constexpr int kMfmaBM = 256;
 void mfma_init_attributes();
+
+// gemm_i8.hip: int8 x int8 grouped GEMM with int32 block accumulation (the
+// opt-in UOCR_FLAG_INT8_MFMA mode). Activations enter quantised per 32-block.
+struct I8Planes {
+  const int8_t* xq;     // [T, H] quantised layer input
+  const float* xs;      // [T, H/32] its block scales
+  float* hid;           // [T*K, I] routed hidden rows (dispatched order), FP32
+  float* hid_shared;    // [T, S] shared-expert hidden rows, FP32
+  int8_t* hid_q;        // the hidden rows quantised: [T*K, I] then [T, S]
+  float* hid_s;         // their block scales: [T*K, I/32] then [T, S/32]
+};
+constexpr int kI8BM = 64;  // token rows per row tile
+bool i8_supported(const DeviceLayer& L);
+void launch_quantize_rows(const float* src, int rows, int K, int8_t* dst, float* sc,
+                          const float* src2, int rows2, int K2, int8_t* dst2, float* sc2,
+                          int* err, hipStream_t s);
+void launch_i8_gateup(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
+                      int tiles_bound, hipStream_t s);
+void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
+                    int tiles_bound, hipStream_t s);
 constexpr int kGemvChunk = 16;
 
 // decode.hip: one-token expert engine, two launches (stage 1: gate/up of

@@ -32,6 +32,7 @@ FLAG_FP32_CLASS = 0
 FLAG_BF16_ACTIVATIONS = 1
 FLAG_FORCE_GEMV = 2
 FLAG_FORCE_MFMA = 4
+FLAG_INT8_MFMA = 8
 PHASES = ["router", "topk", "dispatch", "split", "gateup", "down", "combine", "norm"]
 
 # Every symbol include/uocr_moe.h declares.
