@@ -50,7 +50,7 @@ ROUTER_BYTES = E * H * 2
 # Host threads of one GPU's share of the box (the oracle's CPU baseline).
 CPU_THREADS = 16
 TRAFFIC_PROFILE = "profiles/prefill_stack_T4096_counters.md"
-TRAFFIC_KERNEL = "mfma_group_kernel<32, 3, 3, true, true, false, true, false>"
+TRAFFIC_KERNEL = "mfma_group_kernel<32, 3, 3, true, true, false, true>"
 
 
 def log(msg):

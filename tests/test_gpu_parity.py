@@ -489,13 +489,14 @@ def test_full_bf16_mfma(ctx, full_bf16, T):
 
 @pytest.mark.parametrize("T", [17, 64, 512])
 def test_int8_mfma(ctx, full_int8, full_dynamic, T):
-    """INT8 overlays on the MFMA engine: int8 rows and block scales are
-    streamed and dequantised in registers (q * s, f32) into bf16 hi + lo
-    operands with three product terms (FP32 class), or two with BF16
-    activations; small groups run as 128 x 512 and 64 x 1024 items (T = 512
-    puts ~48 rows in each expert). Under DynamicActivations the groups of one
-    row take the W8A8 path (src/decoder/mod.rs:103-104); T = 17 and 64 leave
-    several such groups among 64 experts."""
+    """INT8 overlays on the MFMA engine: int8 rows (exact in bf16) and block
+    scales are streamed; each 32-deep block's partial product with the
+    activation planes (hi + lo for the FP32 class, hi for BF16 activations)
+    is scaled by its block scale into the f32 accumulator. 64-row tiles run
+    as 64 x 512 items (T = 512 puts ~48 rows in each expert). Under
+    DynamicActivations the groups of one row take the W8A8 path
+    (src/decoder/mod.rs:103-104); T = 17 and 64 leave several such groups
+    among 64 experts."""
     x = syn.activations(T, 1280, seed=700 + T)
     for case, name in ((full_int8, "weight-only"), (full_dynamic, "dynamic")):
         say(f"INT8 MFMA {name} T={T}")

@@ -403,10 +403,14 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
                 "small-batch engine needs widths <= 2048, expert and shared widths that are "
                 "multiples of 16 and a hidden width that is a multiple of 32");
   const bool bf16_only = (flags & UOCR_FLAG_BF16_ACTIVATIONS) != 0;
-  const int bm = mfma ? uocr::kMfmaBM : int8 ? uocr::kI8BM : uocr::kGemvChunk;
-  // The MFMA engine may run an expert's last tile of <= 128 rows as 128 x 512
-  // items and one of <= 64 rows as 64 x 1024 items.
-  const int narrow = mfma ? uocr::kMfmaBM / 2 : 0;
+  // Row tiles: 256 rows on the MFMA engine with BF16 weights (an expert's
+  // last tile of <= 128 rows runs as 128 x 512 items), 64 rows with INT8
+  // weights (64 x 512 items) and in the int8 mode, 16 on the small-batch
+  // engine.
+  const bool q8 = L.quant_mode != UOCR_QUANT_NONE;
+  const int bm = mfma ? (q8 ? uocr::kMfmaQ8BM : uocr::kMfmaBM)
+                      : int8 ? uocr::kI8BM : uocr::kGemvChunk;
+  const int narrow = mfma && !q8 ? uocr::kMfmaBM / 2 : 0;
   const int tiles_bound = uocr::max_tiles(Ti, L.K, L.E, bm);
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);

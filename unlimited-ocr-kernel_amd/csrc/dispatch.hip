@@ -24,18 +24,16 @@ constexpr int kDispatchWaves = kDispatchThreads / 64;
 // Row tiles, written by one wave: lane e holds expert e's row count c (0
 // past E). Routed tiles of bm rows go expert-major into a first list; when
 // narrow > 0, an expert's last tile of at most `narrow` rows goes instead to
-// a second list placed after the first, and (tiny > 0) one of at most `tiny`
-// rows to a third list after that (the MFMA engine runs those as 128 x 512
-// and 64 x 1024 items); the shared expert's tiles follow. counters: [0] all
-// tiles, [1] routed tiles, [2] end of the first list, [3] end of the second.
-__device__ void write_tiles(int lane, int c, int T, int bm, int narrow, int tiny,
+// a second list placed after the first (the MFMA engine runs those as
+// 128 x 512 items); the shared expert's tiles follow. counters: [0] all
+// tiles, [1] routed tiles, [2] end of the first list.
+__device__ void write_tiles(int lane, int c, int T, int bm, int narrow,
                             int* __restrict__ tiles, int* __restrict__ counters, int shared_group) {
   const int full = c / bm, rem = c - full * bm;
-  const bool ty = tiny > 0 && rem > 0 && rem <= tiny;
-  const bool nar = !ty && narrow > 0 && rem > 0 && rem <= narrow;
-  const int nsq = full + ((rem > 0 && !nar && !ty) ? 1 : 0);
-  // Three counts in one scan: square tiles < 2^16, the others <= 64 each.
-  const int packed = nsq | ((nar ? 1 : 0) << 16) | ((ty ? 1 : 0) << 24);
+  const bool nar = narrow > 0 && rem > 0 && rem <= narrow;
+  const int nsq = full + ((rem > 0 && !nar) ? 1 : 0);
+  // Two counts in one scan: square tiles < 2^16, narrow ones <= 64.
+  const int packed = nsq | ((nar ? 1 : 0) << 16);
   int incl = packed;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -44,9 +42,9 @@ __device__ void write_tiles(int lane, int c, int T, int bm, int narrow, int tiny
   }
   const int excl = incl - packed;
   const int total = __shfl(incl, 63);
-  const int routed_sq = total & 0xffff, routed_nr = (total >> 16) & 0xff, routed_ty = total >> 24;
-  const int routed_tiles = routed_sq + routed_nr + routed_ty;
-  const int sq0 = excl & 0xffff, nr0 = (excl >> 16) & 0xff, ty0 = excl >> 24;
+  const int routed_sq = total & 0xffff, routed_nr = total >> 16;
+  const int routed_tiles = routed_sq + routed_nr;
+  const int sq0 = excl & 0xffff, nr0 = excl >> 16;
   for (int i = 0; i < nsq; i++) {
     tiles[2 * (sq0 + i)] = lane;
     tiles[2 * (sq0 + i) + 1] = i * bm;
@@ -54,10 +52,6 @@ __device__ void write_tiles(int lane, int c, int T, int bm, int narrow, int tiny
   if (nar) {
     tiles[2 * (routed_sq + nr0)] = lane;
     tiles[2 * (routed_sq + nr0) + 1] = full * bm;
-  }
-  if (ty) {
-    tiles[2 * (routed_sq + routed_nr + ty0)] = lane;
-    tiles[2 * (routed_sq + routed_nr + ty0) + 1] = full * bm;
   }
   const int shared_tiles = (T + bm - 1) / bm;
   for (int i = lane; i < shared_tiles; i += 64) {
@@ -68,7 +62,6 @@ __device__ void write_tiles(int lane, int c, int T, int bm, int narrow, int tiny
     counters[0] = routed_tiles + shared_tiles;
     counters[1] = routed_tiles;
     counters[2] = routed_sq;
-    counters[3] = routed_sq + routed_nr;
   }
 }
 
@@ -110,7 +103,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       offsets[lane] = excl;
     }
     if (lane == 0) offsets[E] = T * K;
-    write_tiles(lane, c, T, bm, narrow, narrow / 2, tiles, counters, E);
+    write_tiles(lane, c, T, bm, narrow, tiles, counters, E);
   }
   __syncthreads();
   for (int c0 = 0; c0 < T; c0 += kDispatchThreads) {
@@ -236,7 +229,7 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
     if (c == 0) {
       if (lane < E) offsets[lane] = excl;
       if (lane == 0) offsets[E] = T * K;
-      write_tiles(lane, total, T, bm, narrow, narrow / 2, tiles, counters, E);
+      write_tiles(lane, total, T, bm, narrow, tiles, counters, E);
     }
   }
   if (tid < 64) emask[tid] = 0ull;

@@ -102,28 +102,32 @@ constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // One work item: a TM x TN output tile of group g, rows r0.. of the group,
-// columns n0... Three shapes share the code: 256 x 256 (waves 2 x 4) for
-// groups with more than 128 rows left, 128 x 512 (waves 1 x 8) for the last
-// tile of a group when at most 128 rows remain, and 64 x 1024 (waves 1 x 8)
-// when at most 64 remain — a small group then streams its weights in fewer
-// items without computing a mostly empty 256-row tile. A wave owns 128 rows
-// x 64 columns (4 x 2 MFMA tiles) or 64 x 128 (2 x 4): the same number of
-// accumulators and fragment reads per wave.
+// columns n0... BF16 weights use two shapes: 256 x 256 (waves 2 x 4) for
+// groups with more than 128 rows left, and 128 x 512 (waves 1 x 8) for the
+// last tile of a group when at most 128 rows remain — a small group then
+// streams its weights in fewer items without computing a mostly empty
+// 256-row tile. A wave owns 128 rows x 64 columns (4 x 2 MFMA tiles).
 //
-// Q8: INT8-overlay weights, streamed as int8 with their block scales and
-// dequantised in registers into bf16 hi + lo fragments (a third product
-// term), y always f32.
+// Q8: INT8-overlay weights, streamed as int8 rows with their block scales.
+// Items are 64 x 512 (waves 1 x 8, each 64 x 64 as 2 x 2 MFMA tiles, the
+// activations the first operand): an int8 weight is exact in bf16, so each
+// 32-deep stage (one scale block) multiplies the activation planes by the
+// int8 rows into a partial tile, and the block scale of each output row
+// (lane-uniform in this layout) is applied to that partial with one FMA
+// per element: the FP32 class needs the two activation terms only, BF16
+// activations one. y is f32.
 template <int TM, int BK, int NBUF, bool SPLIT, bool GATEUP, bool Q8>
 __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S,
                                           const MfmaPlanes& P, int T, int g, int r0, int n0,
                                           uint16_t* lds) {
   constexpr int WAVES = 8;
-  constexpr int TN = 256 * 256 / TM;      // 256, 512 or 1024
+  static_assert(Q8 ? TM == 64 : (TM == 256 || TM == 128), "item shapes");
+  constexpr int TN = Q8 ? 512 : 256 * 256 / TM;  // 256 or 512 (BF16); 512 (INT8)
   constexpr int kMi = TM >= 128 ? 4 : TM / 32;  // 32-row MFMA tiles per wave
-  constexpr int kWr = 32 * kMi;            // rows per wave: 128, or 64
+  constexpr int kWr = 32 * kMi;            // rows per wave: 128, or 64 (INT8)
   constexpr int kWm = TM / kWr;            // wave rows
   constexpr int kWn = WAVES / kWm;         // wave columns
-  constexpr int kWc = TN / kWn;            // 64 columns per wave (128 for TM = 64)
+  constexpr int kWc = TN / kWn;            // 64 columns per wave
   constexpr int kNi = kWc / 32;
   const bool routed = g < L.E;
   const int W = L.width(g);
@@ -148,8 +152,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
 
   // ---- LDS tiles. A stage holds the A plane(s) ([TM rows][BK] bf16) and
   // B: BF16 weights as a [TN rows][BK] bf16 plane; INT8 overlays (Q8) as
-  // their int8 rows ([TN][BK] bytes, BK = 32: one scale block) and the f32
-  // block scale of each row. No padding: 16-byte chunk c of a bf16 row r
+  // their int8 rows ([TN][BK] bytes, BK = 32: one scale block). Q8 block
+  // scales arrive in groups of 8 blocks ([TN rows][8] f32, three group
+  // buffers after the stage ring; see issue_scales). No padding: 16-byte chunk c of a bf16 row r
   // sits at position c ^ swz(r), which spreads the 16-byte fragment reads
   // of 16 consecutive rows over all LDS banks (int8 rows: c ^ ((r >> 3) & 1)
   // over their two chunks). Loads arrive as 1 KB wave segments (lane l ->
@@ -169,18 +174,23 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   static_assert(kSegTotA % WAVES == 0 || WAVES % kSegTotA == 0, "A segments");
   static_assert(kSegTotB % WAVES == 0 || WAVES % kSegTotB == 0, "B segments");
   const int segA0 = kSegTotA >= WAVES ? wave * kSegA : wave % kSegTotA;
+  // Two A planes of WAVES / 2 segments each (64-row tiles, FP32 class):
+  // waves 0..3 load the hi plane, waves 4..7 the lo plane, once each.
+  constexpr bool kSplitA = SPLIT && 2 * kSegTotA == WAVES;
   const int segB0 = kSegTotB >= WAVES ? wave * kSegB : wave % kSegTotB;
   constexpr int kRowDiv = 16 / kCpr;
   auto swz = [](int r) { return (r / kRowDiv) % kCpr; };
   auto swzb = [&](int r) { return Q8 ? (r >> 3) & 1 : swz(r); };
   constexpr uint32_t a_plane = (uint32_t)TM * BK * 2;
   constexpr uint32_t b_plane = (uint32_t)TN * BK * (Q8 ? 1 : 2);
-  constexpr uint32_t s_plane = Q8 ? (uint32_t)TN * 4 : 0;
   constexpr int kAPlanes = SPLIT ? 2 : 1;
-  constexpr uint32_t stage_bytes = kAPlanes * a_plane + b_plane + s_plane;
-  // Plane order in a stage: A hi, B, [A lo], [B scales].
-  constexpr uint32_t b_at = a_plane, alo_at = a_plane + b_plane,
-                     s_at = a_plane + b_plane + (SPLIT ? a_plane : 0);
+  constexpr uint32_t stage_bytes = kAPlanes * a_plane + b_plane;
+  // Plane order in a stage: A hi, B, [A lo].
+  constexpr uint32_t b_at = a_plane, alo_at = a_plane + b_plane;
+  // Q8 scale groups: group q (blocks 8q .. 8q+7) in buffer q % 3.
+  constexpr int kSGroup = 8;
+  constexpr uint32_t sg_bytes = (uint32_t)TN * kSGroup * 4;
+  constexpr uint32_t sg_at = (uint32_t)NBUF * stage_bytes;
 
   // Per-lane source offsets of this wave's segments (k = 0).
   const uint32_t row_bytes = (uint32_t)K * 2;
@@ -201,19 +211,8 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     const int c = (lane % kCprB) ^ swzb(r);
     b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes_b + 16u * c : kDmaOut;
   }
-  // Q8 block scales: dword loads of 64 rows each, kSegSW per wave per stage
-  // (when there are fewer 64-row segments than waves, waves past them
-  // repeat segment wave % count).
-  constexpr int kSegS = TN / 64;
-  constexpr int kSegSW = kSegS >= WAVES ? kSegS / WAVES : 1;
-  const int segS = kSegS >= WAVES ? wave * kSegSW : wave % kSegS;
   const int nblk = K / kQBlock;
-  uint32_t s_off[kSegSW];
-#pragma unroll
-  for (int i = 0; i < kSegSW; i++) {
-    const int r = (segS + i) * 64 + lane;
-    s_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * nblk * 4u : kDmaOut;
-  }
+  static_assert(!Q8 || TN == WAVES * 64, "a scale group is one dword load per wave and stage");
   const uint16_t* a_hi_src;
   const uint16_t* a_lo_src;
   uint32_t a_rows;
@@ -239,27 +238,49 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
   const i32x4 rs_b = buffer_rsrc(wmat, (uint32_t)N * row_bytes_b);
   const i32x4 rs_s = buffer_rsrc(Q8 ? (const void*)wscale : wmat, Q8 ? (uint32_t)N * nblk * 4u : 0u);
+  const bool lo_wave = kSplitA && __builtin_amdgcn_readfirstlane(wave) >= WAVES / 2;
+  const i32x4 rs_a1 = lo_wave ? rs_l : rs_a;
   // LDS byte addresses of this wave's first A and B segments of stage buffer 0.
   const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds);
   const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_base + (uint32_t)segA0 * 1024u);
   const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_base + b_at + (uint32_t)segB0 * 1024u);
-  const uint32_t lds_s = __builtin_amdgcn_readfirstlane(lds_base + s_at + (uint32_t)segS * 256u);
+  const uint32_t lds_a1 = lds_a + (lo_wave ? alo_at : 0u);
+  // Q8 scales: part p (0..7) of group q is one dword load per wave, rows
+  // 8 (8 p + wave) .. +7 with their 8 blocks (lane l: row + l / 8, the 32
+  // contiguous bytes of blocks 8 q ..). Position j of row r holds block
+  // 8 q + (j ^ sws(r)), so the 32 rows a half-wave reads for one block sit
+  // in 32 distinct banks. Group q + 1 travels with the loads of stages
+  // 8 q .. 8 q + 7 (part = stage % 8); group 0 before the first stage.
+  // Group q + 1 overwrites group q - 2, whose last stage (8 q - 9) was read
+  // before the loads of stage 8 q - kDepth are issued.
+  auto sws = [](int r) { return (r >> 3) & 7; };
+  auto issue_scales = [&](int q, int part) {
+    const int r = (part * WAVES + wave) * 8 + lane / 8;
+    const int blk = q * kSGroup + ((lane % 8) ^ sws(r));
+    const uint32_t off = n0 + r < N && blk < nblk ? ((uint32_t)(n0 + r) * nblk + blk) * 4u : kDmaOut;
+    const uint32_t dst = lds_base + sg_at + (uint32_t)(q % 3) * sg_bytes +
+                         (uint32_t)(part * WAVES + wave) * 256u;
+    buffer_load_lds4(rs_s, __builtin_amdgcn_readfirstlane(dst), off);
+  };
   auto issue = [&](int buf, int k0) {
     const uint32_t st = (uint32_t)buf * stage_bytes;
     const uint32_t kb = (uint32_t)k0 * 2u;
     const uint32_t ka = GATEUP ? kb : (uint32_t)(k0 / 32) * a_rows * 64u;
+    if constexpr (kSplitA) {
+      buffer_load_lds16(rs_a1, lds_a1 + st, a_off[0] + ka);
+    } else {
 #pragma unroll
-    for (int i = 0; i < kSegA; i++) {
-      buffer_load_lds16(rs_a, lds_a + st + i * 1024u, a_off[i] + ka);
-      if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + ka);
+      for (int i = 0; i < kSegA; i++) {
+        buffer_load_lds16(rs_a, lds_a + st + i * 1024u, a_off[i] + ka);
+        if constexpr (SPLIT) buffer_load_lds16(rs_l, lds_a + st + alo_at + i * 1024u, a_off[i] + ka);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kSegB; i++)
       buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + (Q8 ? (uint32_t)k0 : kb));
     if constexpr (Q8) {
-#pragma unroll
-      for (int i = 0; i < kSegSW; i++)
-        buffer_load_lds4(rs_s, lds_s + st + i * 256u, s_off[i] + (uint32_t)(k0 / kQBlock) * 4u);
+      const int stage = k0 / BK;
+      issue_scales(stage / kSGroup + 1, stage % kSGroup);
     }
   };
 
@@ -275,6 +296,23 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   const int fc = lane >> 5;   // fragment chunk inside a 16-wide k step
   const int nk = K / BK;
 
+  // Q8: partial tiles of the current stage; the last one is folded with
+  // last_scale during the next stage (zeros before the first).
+  floatx16 part[Q8 ? kMi : 1][Q8 ? kNi : 1];
+#pragma unroll
+  for (int mi = 0; mi < (Q8 ? kMi : 1); mi++)
+#pragma unroll
+    for (int ni = 0; ni < (Q8 ? kNi : 1); ni++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) part[mi][ni][r] = 0.0f;
+  float last_scale = 0.0f;
+
+  // Q8 k order inside a 32-block: MFMA step s takes k = 16 fc + 8 s .. +7
+  // from lane (fr, fc), so a lane's two steps are one 16-byte int8 chunk
+  // (chunk fc of its row) and the activation fragments follow the same
+  // order (bf16 chunk 2 fc + s). A block's partial is a sum over its 32 k
+  // in any order.
+  //
   // Ping-pong schedule. The two waves sharing a SIMD (w and w + 4) are in
   // opposite groups, one phase apart: while one group multiplies stage ks
   // from registers, the other reads its stage-ks fragments from LDS and
@@ -291,9 +329,11 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   // vmcnt <= (kDepth - 1) * kLps; the barrier then publishes them to both
   // groups before either reads stage ks + 1.
   constexpr int kDepth = NBUF - 1;
-  constexpr int kLps = kSegA * kAPlanes + kSegB + (Q8 ? kSegSW : 0);
+  constexpr int kLps = (kSplitA ? 1 : kSegA * kAPlanes) + kSegB + (Q8 ? 1 : 0);
   constexpr int kSub = BK / 16;
   const int grp = wave >> 2;
+  if constexpr (Q8)
+    for (int part = 0; part < kSGroup; part++) issue_scales(0, part);
   for (int i = 0; i < kDepth; i++)
     if (i < nk) issue(i, i * BK);
   if (nk >= kDepth)
@@ -307,45 +347,43 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     const bool steady = ks + kDepth < nk;
     if (steady) issue((ks + kDepth) % NBUF, (ks + kDepth) * BK);
     const char* cur = reinterpret_cast<const char*>(lds) + (ks % NBUF) * stage_bytes;
-    bf16x8 fa[kSub][kMi], fl[kSub][SPLIT ? kMi : 1], fb[kSub][kNi], fbl[kSub][Q8 ? kNi : 1];
+    bf16x8 fa[kSub][kMi], fl[kSub][SPLIT ? kMi : 1], fb[kSub][kNi];
     auto frag = [&](const char* plane, int row, int c) {
       return as_bf16x8(*reinterpret_cast<const uint4*>(plane + row * (BK * 2) + 16 * (c ^ swz(row))));
     };
     float bscale[kNi];
+    uint4 qraw[kNi];
     if constexpr (Q8) {
 #pragma unroll
-      for (int ni = 0; ni < kNi; ni++)
-        bscale[ni] = *reinterpret_cast<const float*>(cur + s_at + (wn * kWc + ni * 32 + fr) * 4);
+      for (int ni = 0; ni < kNi; ni++) {
+        const int row = wn * kWc + ni * 32 + fr;
+        bscale[ni] = *reinterpret_cast<const float*>(
+            reinterpret_cast<const char*>(lds) + sg_at + (ks / kSGroup) % 3 * sg_bytes +
+            row * (kSGroup * 4) + ((ks % kSGroup) ^ sws(row)) * 4);
+        qraw[ni] = *reinterpret_cast<const uint4*>(cur + b_at + row * BK + 16 * (fc ^ swzb(row)));
+      }
     }
 #pragma unroll
     for (int sub = 0; sub < kSub; sub++) {
-      const int c = 2 * sub + fc;
+      const int c = Q8 ? 2 * fc + sub : 2 * sub + fc;
 #pragma unroll
       for (int ni = 0; ni < kNi; ni++) {
         if constexpr (Q8) {
-          // Eight int8 weights of row (column) wn*64 + 32 ni + fr, k = 16 sub
-          // + 8 fc ..; w = q * s rounded to f32 as Int8Matrix::linear
-          // dequantises (src/cpu/quantized.rs:119-131), then hi = bf16(w),
-          // lo = bf16(w - hi): the same B operand bits as the FP32 reference
-          // would multiply, to 2^-16 relative.
-          const int row = wn * kWc + ni * 32 + fr;
-          const uint2 raw = *reinterpret_cast<const uint2*>(
-              cur + b_at + row * BK + 16 * (sub ^ swzb(row)) + 8 * fc);
-          uint32_t hp[4], lp[4];
+          // Eight int8 weights of row (output feature) wn*64 + 32 ni + fr,
+          // k = 16 fc + 8 sub ..: |q| <= 127 is exact in bf16 (the f32 of a
+          // small integer has zero low half), so the bf16 is its high half.
+          const uint32_t lo = sub ? qraw[ni].z : qraw[ni].x;
+          const uint32_t hi = sub ? qraw[ni].w : qraw[ni].y;
+          uint32_t hp[4];
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            const uint32_t word = j < 4 ? raw.x : raw.y;
+            const uint32_t word = j < 4 ? lo : hi;
             const int s0 = 8 * (j & 3), s1 = s0 + 8;
-            const float w0 = (float)(int8_t)((word >> s0) & 0xffu) * bscale[ni];
-            const float w1 = (float)(int8_t)((word >> s1) & 0xffu) * bscale[ni];
-            const uint32_t h0 = bf16_bits(w0), h1 = bf16_bits(w1);
-            const uint32_t l0 = bf16_bits(w0 - __uint_as_float(h0 << 16));
-            const uint32_t l1 = bf16_bits(w1 - __uint_as_float(h1 << 16));
-            hp[j / 2] = h0 | (h1 << 16);
-            lp[j / 2] = l0 | (l1 << 16);
+            const float w0 = (float)(int8_t)((word >> s0) & 0xffu);
+            const float w1 = (float)(int8_t)((word >> s1) & 0xffu);
+            hp[j / 2] = __builtin_amdgcn_perm(__float_as_uint(w1), __float_as_uint(w0), 0x07060302u);
           }
           fb[sub][ni] = as_bf16x8(make_uint4(hp[0], hp[1], hp[2], hp[3]));
-          fbl[sub][ni] = as_bf16x8(make_uint4(lp[0], lp[1], lp[2], lp[3]));
         } else {
           fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
         }
@@ -369,28 +407,88 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     // 8-byte stores). Down keeps [32 tokens x 32 features] (lane l owns
     // feature l % 32: a half-wave writes 32 adjacent outputs of one row).
     auto mma = [&](const bf16x8& a, const bf16x8& b, floatx16& c) {
-      c = GATEUP ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0)
-                 : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+      c = GATEUP && !Q8 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     };
+    if constexpr (Q8) {
+      // Tile by tile: the stage's partial (one 32-block of K) of tile t,
+      // while the block scales fold the partial of tile t - 1 into acc (one
+      // FMA per element, the scale of this lane's output feature); tile 0
+      // folds the previous stage's last tile, so only the last fold of the
+      // item waits for its MFMAs.
+      constexpr int kT = kMi * kNi;
 #pragma unroll
-    for (int sub = 0; sub < kSub; sub++)
+      for (int t = 0; t < kT; t++) {
+        const int mi = t / kNi, ni = t % kNi;
+        floatx16 z = {};
+        part[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][mi], fb[0][ni], z, 0, 0, 0);
+        if constexpr (SPLIT) mma(fl[0][mi], fb[0][ni], part[mi][ni]);
 #pragma unroll
-      for (int mi = 0; mi < kMi; mi++)
-#pragma unroll
-        for (int ni = 0; ni < kNi; ni++) {
-          mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
-          if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
-          if constexpr (Q8) mma(fa[sub][mi], fbl[sub][ni], acc[mi][ni]);
+        for (int sub = 1; sub < kSub; sub++) {
+          mma(fa[sub][mi], fb[sub][ni], part[mi][ni]);
+          if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], part[mi][ni]);
         }
+        const int pt = (t + kT - 1) % kT, pmi = pt / kNi, pni = pt % kNi;
+        const float sc = t == 0 ? last_scale : bscale[pni];
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          acc[pmi][pni][r] = __builtin_fmaf(part[pmi][pni][r], sc, acc[pmi][pni][r]);
+      }
+      last_scale = bscale[kNi - 1];
+      // One MFMA, then its share of the fold's FMAs (16 per tile), in turn.
+#pragma unroll
+      for (int i = 0; i < kT * kSub * kAPlanes; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 16 / (kSub * kAPlanes), 0);
+      }
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < kSub; sub++)
+#pragma unroll
+        for (int mi = 0; mi < kMi; mi++)
+#pragma unroll
+          for (int ni = 0; ni < kNi; ni++) {
+            mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
+            if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
+          }
+    }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   }
   if (!grp) __syncthreads();
+  if constexpr (Q8) {
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+      acc[kMi - 1][kNi - 1][r] =
+          __builtin_fmaf(part[kMi - 1][kNi - 1][r], last_scale, acc[kMi - 1][kNi - 1][r]);
+  }
 
   const int wcol0 = n0 + wn * kWc;
   if (wcol0 >= N) return;
-  if (GATEUP) {
+  if (GATEUP && Q8) {
+    // Activations first: element (mi, ni, r) is token row 32 mi + 8 (r/4) +
+    // 4 (lane/32) + r%4 and feature column wcol0 + 32 ni + lane%32; the
+    // wave's 64 columns are one (gate, up) block pair, so ni = 0 holds the
+    // gate values and ni = 1 the up values of hidden column wcol0/2 + lane%32.
+    uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
+    uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
+    const size_t hrows = routed ? (size_t)T * L.K : (size_t)T;
+    const int hcol = wcol0 / 2 + fr;
+#pragma unroll
+    for (int mi = 0; mi < kMi; mi++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mi * 32 + 8 * (r >> 2) + 4 * fc + (r & 3);
+        if (row >= mrows) continue;
+        const float gv = acc[mi][0][r];
+        const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][1][r];
+        const size_t at = ((size_t)(hcol / 32) * hrows + (base + r0 + row)) * 32 + hcol % 32;
+        const uint16_t hb = bf16_bits(h);
+        h_hi[at] = hb;
+        if constexpr (SPLIT) h_lo[at] = bf16_bits(h - __uint_as_float((uint32_t)hb << 16));
+      }
+  } else if (GATEUP) {
     // Output element (mi, ni, r) of this lane: token row 128 wm + 32 mi +
     // lane%32, feature column kWc wn + 32 ni + 8 (r/4) + 4 (lane/32) + r%4;
     // registers 4j .. 4j+3 are four consecutive features of one token.
@@ -457,9 +555,8 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
 
 // Item costs for the XCD split, in units of one 32-deep k step of a 256 x
 // 256 tile (8) — a 128 x 512 item moves 1.25x the bytes of a square one for
-// the same MFMA work, so it counts 9; a 64 x 1024 item (INT8 rows: about
-// the bytes of a square one) counts 8.
-constexpr int kCostSquare = 8, kCostWide = 9, kCostTiny = 8;
+// the same MFMA work, so it counts 9. INT8 items all have one shape.
+constexpr int kCostSquare = 8, kCostWide = 9;
 
 // Which variants run the 128 x 512 shape. The FP32-class BF16 engine moves
 // as many bytes per stage in either shape (the A planes are hi + lo), so a
@@ -469,60 +566,53 @@ constexpr int kCostSquare = 8, kCostWide = 9, kCostTiny = 8;
 // weight stream from HBM, which the shape does not shorten: square items
 // only are faster on the 4096-token stack (4.59 vs 4.69 ms), so BF16
 // activations take the wide shape only up to kWideMaxTokens tokens, where
-// small groups dominate. The INT8 engine streams int8 rows (half the bytes
-// of bf16) and dequantises them in registers: with the 128 x 512 and
-// 64 x 1024 shapes its 512-token layer runs in 0.29 ms.
+// small groups dominate. INT8 layers run 64-row tiles as 64 x 512 items
+// only (512-token layer, FP32 class: 0.29 ms with 128 x 512 and 64 x 1024
+// items of three product terms, 0.19 ms with these of two).
 constexpr int kWideMaxTokens = 2048;
-// 64 x 1024 items: the INT8 engine only (its stages are 32-deep int8 rows,
-// so three stages of 1024 B rows still fit; a bf16 B plane of 1024 rows
-// leaves room for two).
-template <bool SPLIT, bool Q8>
-constexpr bool use_tiny_items() { return Q8; }
 
 // Groups of one row are skipped when the overlay runs DynamicActivations
 // (the batch engine's W8A8 path owns them). NBUF_W: stage buffers of the
 // 128 x 512 shape.
-template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8, bool WIDE, bool TINY>
+template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8, bool WIDE>
 __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
                                                             MfmaPlanes P, int T) {
-  extern __shared__ __align__(16) uint16_t lds[];  // [stage][A hi | B | A lo | B lo]
+  extern __shared__ __align__(16) uint16_t lds[];  // [stage ring][INT8 scale groups]
+  static_assert(!Q8 || !WIDE, "INT8 items are 64 x 512 only");
   constexpr bool kWide = WIDE;
-  constexpr bool kTiny = WIDE && TINY;
 
   // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
   // square items (shared expert first, then routed, each in row-tile,
   // column-tile order) are cut into 8 contiguous ranges of equal cost, one
-  // per XCD, and so are the small-group items (128 x 512, then 64 x 1024);
-  // an XCD interleaves its two ranges. An item costs its K depth times its
+  // per XCD, and so are the small-group items (128 x 512); an XCD
+  // interleaves its two ranges. An item costs its K depth times its
   // shape's cost, so the deeper shared items of the down GEMM do not pile
   // up on one XCD, neighbouring square items (same expert, same rows) meet
   // in one L2, an XCD's deeper items start first, and the weight streams of
   // the small groups (little reuse) spread over every XCD's path to HBM.
-  // Tile lists (dispatch): routed [0, c2) square, [c2, c3) last tiles of
-  // <= 128 rows, [c3, c1) last tiles of <= 64 rows, then the shared tiles;
-  // a variant without a shape runs those tiles with the next larger one.
+  // Tile lists (dispatch): routed [0, c2) square, [c2, c1) last tiles of
+  // <= 128 rows (in two lists, <= 128 and <= 64, both run as 128 x 512),
+  // then the shared tiles; a variant without the wide shape runs them all
+  // as square items.
   const int all_tiles = S.counters[0];
   const int routed_tiles = S.counters[1];
   const int square_tiles = kWide ? S.counters[2] : routed_tiles;
-  const int wide_end = kTiny ? S.counters[3] : routed_tiles;
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
-  const int nt_routed = (n_routed + kTileN - 1) / kTileN;
+  // INT8 layers: every tile is 64 rows, every item 64 x 512.
+  constexpr int kItemN = Q8 ? 2 * kTileN : kTileN;
+  const int nt_routed = (n_routed + kItemN - 1) / kItemN;
   const int nt_wide = (n_routed + 2 * kTileN - 1) / (2 * kTileN);
-  const int nt_tiny = (n_routed + 4 * kTileN - 1) / (4 * kTileN);
-  const int nt_shared = (n_shared + kTileN - 1) / kTileN;
+  const int nt_shared = (n_shared + kItemN - 1) / kItemN;
   const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
   const long long square_items = (long long)square_tiles * nt_routed;
-  const long long wide_items = (long long)(wide_end - square_tiles) * nt_wide;
-  const long long tiny_items = (long long)(routed_tiles - wide_end) * nt_tiny;
+  const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
   const long long c_shared = (GATEUP ? L.H : L.S) * kCostSquare;
   const long long c_square = (GATEUP ? L.H : L.I) * kCostSquare;
   const long long c_wide = (GATEUP ? L.H : L.I) * kCostWide;
-  const long long c_tiny = (GATEUP ? L.H : L.I) * kCostTiny;
   const long long cost1 = shared_items * c_shared;
   const long long cost_sq = cost1 + square_items * c_square;
-  const long long cost_wd = wide_items * c_wide;
-  const long long cost_sm = cost_wd + tiny_items * c_tiny;
+  const long long cost_sm = wide_items * c_wide;
   // First square item of XCD x: the first whose cost prefix reaches x / 8 of
   // the square cost; likewise the first small-group item.
   auto first_sq = [&](int x) -> long long {
@@ -531,9 +621,7 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
     return shared_items + (b - cost1 + c_square - 1) / c_square;
   };
   auto first_sm = [&](int x) -> long long {
-    const long long b = cost_sm * x / kXcds;
-    if (b <= cost_wd) return (b + c_wide - 1) / c_wide;
-    return wide_items + (b - cost_wd + c_tiny - 1) / c_tiny;
+    return (cost_sm * x / kXcds + c_wide - 1) / c_wide;
   };
   const int xcd = blockIdx.x % kXcds;
   const long long j = blockIdx.x / kXcds;
@@ -547,18 +635,11 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   // the L2-resident square work instead of all at once.
   const long long sm_before = j * n_sm / n_xcd;
   const bool take_small = (j + 1) * n_sm / n_xcd > sm_before;
-  int tile, ntile, shape = 0;  // 0: 256 x 256, 1: 128 x 512, 2: 64 x 1024
+  int tile, ntile;
   if (take_small) {
     const long long i = sm0 + sm_before;
-    if (i < wide_items) {
-      tile = square_tiles + (int)(i / nt_wide);
-      ntile = (int)(i % nt_wide);
-      shape = 1;
-    } else {
-      tile = wide_end + (int)((i - wide_items) / nt_tiny);
-      ntile = (int)((i - wide_items) % nt_tiny);
-      shape = 2;
-    }
+    tile = square_tiles + (int)(i / nt_wide);
+    ntile = (int)(i % nt_wide);
   } else {
     const long long item = sq0 + (j - sm_before);
     if (item < shared_items) {
@@ -574,44 +655,37 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   if (Q8 && g < L.E && L.quant_mode == kQuantDynamic &&
       S.offsets[g + 1] - S.offsets[g] == 1)
     return;
-  if constexpr (kTiny) {
-    if (shape == 2) {
-      mfma_item<64, BK, NBUF_W, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * 4 * kTileN, lds);
-      return;
-    }
-  }
   if constexpr (kWide) {
-    if (shape == 1) {
-      mfma_item<128, BK, NBUF_W, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * 2 * kTileN, lds);
+    if (take_small) {
+      mfma_item<128, BK, NBUF_W, SPLIT, GATEUP, false>(L, S, P, T, g, r0, ntile * 2 * kTileN,
+                                                       lds);
       return;
     }
   }
-  mfma_item<256, BK, NBUF, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * kTileN, lds);
+  mfma_item<Q8 ? 64 : 256, BK, NBUF, SPLIT, GATEUP, Q8>(L, S, P, T, g, r0, ntile * kItemN, lds);
 }
 
 // Dynamic LDS of one shape: NBUF stages of the A planes (TM rows, bf16) and
-// B (256 * 256 / TM rows: bf16, or int8 plus one f32 scale per row), BK deep.
+// B (256 * 256 / TM rows of bf16, or 512 of int8), BK deep; INT8 also holds
+// three scale groups (512 rows x 8 blocks, f32).
 constexpr size_t stage_lds(int TM, int BK, int NBUF, int a_planes, bool q8) {
-  const size_t tn = (size_t)kTileM * kTileN / TM;
-  return (size_t)NBUF * ((size_t)a_planes * TM * BK * 2 + (q8 ? tn * BK + tn * 4 : tn * BK * 2));
+  const size_t tn = q8 ? 2 * (size_t)kTileN : (size_t)kTileM * kTileN / TM;
+  return (size_t)NBUF * ((size_t)a_planes * TM * BK * 2 + tn * BK * (q8 ? 1 : 2)) +
+         (q8 ? 3 * tn * 8 * 4 : 0);  // Q8: three scale groups of 8 blocks
 }
-template <int BK, int NBUF, int NBUF_W, int AP, bool Q8, bool WIDE, bool TINY>
+template <int BK, int NBUF, int NBUF_W, int AP, bool Q8, bool WIDE>
 constexpr size_t mfma_lds_bytes() {
-  const size_t sq = stage_lds(256, BK, NBUF, AP, Q8);
+  const size_t sq = stage_lds(Q8 ? 64 : 256, BK, NBUF, AP, Q8);
   const size_t wd = WIDE ? stage_lds(128, BK, NBUF_W, AP, Q8) : 0;
-  const size_t ty = TINY ? stage_lds(64, BK, NBUF_W, AP, Q8) : 0;
-  const size_t m = sq > wd ? sq : wd;
-  return m > ty ? m : ty;
+  return sq > wd ? sq : wd;
 }
 // BF16 activations: 32-deep stages, four buffers (128 KiB), three for the
 // 128 x 512 items of its small-batch variant (120 KiB). FP32-class (hi +
 // lo planes): 32-deep stages, three buffers (144 KiB either shape). INT8
-// overlay (int8 rows + scales, 25 / 41 KiB per stage): 32-deep stages (one
-// scale block), four buffers with BF16 activations (100 KiB), three in the
-// FP32 class (123 KiB); three for its 128 x 512 and 64 x 1024 items (up to
-// 132 KiB). The small-shape counts apply only to variants with those shapes.
+// overlay, 64 x 512 items (20 / 24 KiB per stage): 32-deep stages (one
+// scale block), four buffers, plus 48 KiB of scale groups (128 / 144 KiB).
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 3, kBkSplit = 32, kBufSplit = 3;
-constexpr int kBkQ = 32, kBufQ = 4, kBufQS = 3;
+constexpr int kBkQ = 32, kBufQ = 4;
 
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
   if (n == 0) return;
@@ -621,13 +695,14 @@ void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, h
 }
 
 // Workgroups: 8 XCDs times the most items one XCD can take. Items are
-// bounded by every row tile times the widest column count of square items
-// (a 128 x 512 item replaces two square ones); an XCD's two ranges hold an
+// bounded by every row tile times the widest column count of its items
+// (a 128 x 512 item replaces two square ones; INT8 layers: 512 columns); an XCD's two ranges hold an
 // eighth of their cost each, so at most (bound / 8) * (dearest / cheapest
 // item) + 4 items.
 static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   const int n = gateup ? std::max(2 * L.S, 2 * L.I) : L.H;
-  const long long items = (long long)tiles_bound * ((n + kTileN - 1) / kTileN);
+  const int item_n = L.quant_mode != kQuantNone ? 2 * kTileN : kTileN;  // INT8: 64 x 512
+  const long long items = (long long)tiles_bound * ((n + item_n - 1) / item_n);
   const long long k_routed = gateup ? L.H : L.I, k_shared = gateup ? L.H : L.S;
   const long long dear = std::max(k_shared * kCostSquare, k_routed * kCostWide);
   const long long cheap = std::min(k_shared, k_routed) * kCostSquare;
@@ -637,9 +712,8 @@ static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
 }
 
 #define UOCR_MFMA_KERNEL(BK, NBUF, NBUFW, SPLIT, GATEUP, Q8, WIDE) \
-  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, Q8, WIDE, use_tiny_items<SPLIT, Q8>()>
-#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8, WIDE) \
-  mfma_lds_bytes<BK, NBUF, NBUFW, AP, Q8, WIDE, WIDE && use_tiny_items<(AP > 1), Q8>()>()
+  mfma_group_kernel<BK, NBUF, NBUFW, SPLIT, GATEUP, Q8, WIDE>
+#define UOCR_MFMA_LDS(BK, NBUF, NBUFW, AP, Q8, WIDE) mfma_lds_bytes<BK, NBUF, NBUFW, AP, Q8, WIDE>()
 
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -647,11 +721,11 @@ static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(512);
   if (L.quant_mode != kQuantNone) {
     if (bf16_only)
-      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQS, false, GATEUP, true, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQS, 1, true, true), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQ, false, GATEUP, true, false)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 1, true, false), s>>>(L, S, P, T);
     else
-      UOCR_MFMA_KERNEL(kBkQ, kBufQS, kBufQS, true, GATEUP, true, true)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQS, kBufQS, 2, true, true), s>>>(L, S, P, T);
+      UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQ, true, GATEUP, true, false)
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 2, true, false), s>>>(L, S, P, T);
   } else if (bf16_only && T <= kWideMaxTokens) {
     UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false, true)
         <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false, true), s>>>(L, S,
@@ -689,8 +763,8 @@ void mfma_init_attributes() {
   UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, false)
   UOCR_MFMA_ATTR(kBkBf16, kBufBf16, kBufBf16W, false, false, 1, true)
   UOCR_MFMA_ATTR(kBkSplit, kBufSplit, kBufSplit, true, false, 2, true)
-  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQS, false, true, 1, true)
-  UOCR_MFMA_ATTR(kBkQ, kBufQS, kBufQS, true, true, 2, true)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQ, false, true, 1, false)
+  UOCR_MFMA_ATTR(kBkQ, kBufQ, kBufQ, true, true, 2, false)
 #undef UOCR_MFMA_ATTR
   (void)hipGetLastError();  // a refused attribute surfaces at launch instead
 }

@@ -144,6 +144,7 @@ void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                       int tiles_bound, bool bf16_only, hipStream_t s);
 constexpr int kMfmaBM = 256;
+constexpr int kMfmaQ8BM = 64;  // INT8 weights: 64-row tiles, 64 x 512 items
 void mfma_init_attributes();
 
 // gemm_i8.hip: int8 x int8 grouped GEMM with int32 block accumulation (the
