@@ -97,6 +97,19 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
 
 constexpr uint32_t kDmaOut = 0x80000000u;  // offset past every resource
 
+// A raw buffer resource over `bytes` bytes from `base` for stores: a store
+// whose offset lies past the range is dropped by the hardware range check.
+// Row offsets are passed through vgpr_offset, which keeps each whole in the
+// VGPR offset (the compiler cannot split a constant part of it into the
+// instruction or SGPR offset fields), so the check sees the full row.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ int vgpr_offset(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at maximum).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -465,91 +478,135 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   }
 
   const int wcol0 = n0 + wn * kWc;
+  if constexpr (GATEUP && !Q8) {
+    // Output element (mi, ni, r) of this lane: token row 128 wm + 32 mi +
+    // lane%32, feature column kWc wn + 32 ni + 8 (r/4) + 4 (lane/32) + r%4;
+    // registers 4j .. 4j+3 are four consecutive features of one token.
+    // Columns 64b .. 64b+63 of the wave are one (gate, up) block pair: the
+    // wave owns hidden block wn of the item, 32 columns.
+    // SiLU(g) u = g / (1 + exp(-g)) u with a hardware reciprocal.
+    //
+    // h is staged in LDS (the stage ring is free after the loop) in the
+    // layout of the k-blocked h planes ([W/32][rows][32]), then written out
+    // per (plane, block) as one contiguous run of mrows x 64 bytes with full
+    // 16-byte lanes, through a resource over exactly that run (rows >=
+    // mrows are dropped). LDS: [plane][block][TM rows][64 B], the 16-byte
+    // chunk c of row r at position c ^ ((r >> 2) & 3).
+    static_assert(kNi == 2, "one (gate, up) block pair per wave");
+    constexpr int kHB = TN / 64;                      // hidden blocks per item
+    constexpr uint32_t kPlaneB = (uint32_t)kHB * TM * 64;  // 64 KiB
+    static_assert(kAPlanes * kPlaneB <= (uint32_t)NBUF * stage_bytes, "h staging fits the ring");
+    char* hst = reinterpret_cast<char*>(lds);
+    auto hsw = [](int r) { return (r >> 2) & 3; };
+    if (wcol0 < N) {
+#pragma unroll
+      for (int mi = 0; mi < kMi; mi++) {
+        const int row = wm * kWr + 32 * mi + fr;
+        char* rowp = hst + (uint32_t)wn * (TM * 64) + row * 64 + 8 * fc;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          uint32_t hb[4], lb[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float gv = acc[mi][0][4 * j + i];
+            const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][1][4 * j + i];
+            hb[i] = bf16_bits(h);
+            if constexpr (SPLIT) lb[i] = bf16_bits(h - __uint_as_float(hb[i] << 16));
+          }
+          const int pos = 16 * (j ^ hsw(row));
+          *reinterpret_cast<uint2*>(rowp + pos) =
+              make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+          if constexpr (SPLIT)
+            *reinterpret_cast<uint2*>(rowp + kPlaneB + pos) =
+                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+        }
+      }
+    }
+    __syncthreads();
+    uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
+    uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
+    const size_t hrows = routed ? (size_t)T * L.K : (size_t)T;
+    // 4 chunks per row, TM rows per (plane, block): a workgroup pass of 512
+    // chunks covers half a square item's (plane, block) or a wide item's.
+    constexpr int kChunks = kAPlanes * kHB * TM * 4;
+    static_assert((TM * 4) % 512 == 0 || 512 % (TM * 4) == 0, "passes align with runs");
+#pragma unroll
+    for (int i = 0; i < kChunks / 512; i++) {
+      const int pb = (512 * i) / (TM * 4);  // uniform: plane * kHB + block
+      const int plane = pb / kHB, blk = pb % kHB;
+      if (n0 + 64 * blk >= N) continue;
+      const int within = tid + 512 * i - pb * TM * 4;
+      const int row = within >> 2, c = within & 3;
+      const uint4 v = *reinterpret_cast<const uint4*>(
+          hst + (uint32_t)pb * (TM * 64) + row * 64 + 16 * (c ^ hsw(row)));
+      uint16_t* run = (plane ? h_lo : h_hi) + ((size_t)(n0 / 64 + blk) * hrows + base + r0) * 32;
+      const __amdgpu_buffer_rsrc_t rs = store_rsrc(run, (uint32_t)mrows * 64u);
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 d = {v.x, v.y, v.z, v.w};
+      __builtin_amdgcn_raw_buffer_store_b128(d, rs, vgpr_offset(row * 64 + 16 * c), 0, 0);
+    }
+    return;
+  }
   if (wcol0 >= N) return;
   if (GATEUP && Q8) {
     // Activations first: element (mi, ni, r) is token row 32 mi + 8 (r/4) +
     // 4 (lane/32) + r%4 and feature column wcol0 + 32 ni + lane%32; the
     // wave's 64 columns are one (gate, up) block pair, so ni = 0 holds the
     // gate values and ni = 1 the up values of hidden column wcol0/2 + lane%32.
+    // The item's rows of that 32-column block of the k-blocked h planes
+    // are one contiguous run of mrows x 64 bytes: stores go through a
+    // resource over exactly that run (rows >= mrows are dropped).
     uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
     uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
     const size_t hrows = routed ? (size_t)T * L.K : (size_t)T;
-    const int hcol = wcol0 / 2 + fr;
+    const size_t run = ((size_t)(wcol0 / 64) * hrows + base + r0) * 32;
+    const __amdgpu_buffer_rsrc_t rs_hi = store_rsrc(h_hi + run, (uint32_t)mrows * 64u);
+    const __amdgpu_buffer_rsrc_t rs_lo = store_rsrc(h_lo + run, (uint32_t)mrows * 64u);
+    const int voff = (4 * fc) * 64 + 2 * fr;
 #pragma unroll
     for (int mi = 0; mi < kMi; mi++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int row = mi * 32 + 8 * (r >> 2) + 4 * fc + (r & 3);
-        if (row >= mrows) continue;
+        const int off = vgpr_offset(voff + (mi * 32 + 8 * (r >> 2) + (r & 3)) * 64);
         const float gv = acc[mi][0][r];
         const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][1][r];
-        const size_t at = ((size_t)(hcol / 32) * hrows + (base + r0 + row)) * 32 + hcol % 32;
         const uint16_t hb = bf16_bits(h);
-        h_hi[at] = hb;
-        if constexpr (SPLIT) h_lo[at] = bf16_bits(h - __uint_as_float((uint32_t)hb << 16));
+        __builtin_amdgcn_raw_buffer_store_b16(hb, rs_hi, off, 0, 0);
+        if constexpr (SPLIT)
+          __builtin_amdgcn_raw_buffer_store_b16(bf16_bits(h - __uint_as_float((uint32_t)hb << 16)),
+                                                rs_lo, off, 0, 0);
       }
-  } else if (GATEUP) {
-    // Output element (mi, ni, r) of this lane: token row 128 wm + 32 mi +
-    // lane%32, feature column kWc wn + 32 ni + 8 (r/4) + 4 (lane/32) + r%4;
-    // registers 4j .. 4j+3 are four consecutive features of one token.
-    // Columns 64b .. 64b+63 of the wave are one (gate, up) block pair.
-    // SiLU(g) u = g / (1 + exp(-g)) u with a hardware reciprocal.
-    uint16_t* h_hi = routed ? P.h_hi : P.hs_hi;
-    uint16_t* h_lo = routed ? P.h_lo : P.hs_lo;
-#pragma unroll
-    for (int bp = 0; bp < kNi / 2; bp++) {
-      if (wcol0 + 64 * bp >= N) break;
-      const int col0 = (wcol0 + 64 * bp) / 2 + 4 * fc;  // hidden column of register 0
-#pragma unroll
-      for (int mi = 0; mi < kMi; mi++) {
-        const int row = wm * kWr + 32 * mi + fr;
-        if (row >= mrows) continue;
-        // h planes k-blocked: [W/32][rows][32], rows = T*K (routed) or T.
-        const size_t hrows = routed ? (size_t)T * L.K : (size_t)T;
-        const size_t at0 = ((size_t)(col0 / 32) * hrows + (base + r0 + row)) * 32 + col0 % 32;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          uint32_t hb[4], lb[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const float gv = acc[mi][2 * bp][4 * j + i];
-            const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][2 * bp + 1][4 * j + i];
-            hb[i] = bf16_bits(h);
-            if constexpr (SPLIT) lb[i] = bf16_bits(h - __uint_as_float(hb[i] << 16));
-          }
-          *reinterpret_cast<uint2*>(h_hi + at0 + 8 * j) =
-              make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-          if constexpr (SPLIT)
-            *reinterpret_cast<uint2*>(h_lo + at0 + 8 * j) =
-                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
-        }
-      }
-    }
   } else {
     // Output element (mi, ni, r) of this lane: row 128 wm + 32 mi + 8 (r/4)
     // + 4 (lane/32) + r%4, column kWc wn + 32 ni + lane%32.
     // FP32-class and INT8 weights: y in f32. BF16 weights with BF16
     // activations: y rounded to bf16 (the combine's operands), in the first
     // half of the same buffer.
-    float* out = routed ? S.y : S.ys;
-    uint16_t* out16 = reinterpret_cast<uint16_t*>(out);
+    // Stores go through a resource over exactly the item's rows (rows >=
+    // mrows fall past it and are dropped); a column >= N moves the lane's
+    // offset past every resource.
+    constexpr uint32_t esz = (SPLIT || Q8) ? 4 : 2;
+    char* rows = reinterpret_cast<char*>(routed ? S.y : S.ys) + (size_t)(base + r0) * L.H * esz;
+    const __amdgpu_buffer_rsrc_t rs = store_rsrc(rows, (uint32_t)mrows * L.H * esz);
+    uint32_t voff[kNi];
+#pragma unroll
+    for (int ni = 0; ni < kNi; ni++) {
+      const int col = wcol0 + ni * 32 + fr;
+      voff[ni] = col < N ? ((uint32_t)(wm * kWr + 4 * fc) * L.H + col) * esz : kDmaOut;
+    }
 #pragma unroll
     for (int mi = 0; mi < kMi; mi++)
 #pragma unroll
-      for (int ni = 0; ni < kNi; ni++) {
-        const int col = wcol0 + ni * 32 + fr;
-        if (col >= N) continue;
+      for (int ni = 0; ni < kNi; ni++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int row = wm * kWr + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row >= mrows) continue;
-          const size_t at = (size_t)(base + r0 + row) * L.H + col;
+          const int off = vgpr_offset(
+              (int)(voff[ni] + (uint32_t)(mi * 32 + 8 * (r >> 2) + (r & 3)) * L.H * esz));
           if constexpr (SPLIT || Q8)
-            out[at] = acc[mi][ni][r];
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[mi][ni][r]), rs, off, 0, 0);
           else
-            out16[at] = bf16_bits(acc[mi][ni][r]);
+            __builtin_amdgcn_raw_buffer_store_b16(bf16_bits(acc[mi][ni][r]), rs, off, 0, 0);
         }
-      }
   }
 }
 
