@@ -610,10 +610,6 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   }
 }
 
-// Item costs for the XCD split, in units of one 32-deep k step of a 256 x
-// 256 tile (8) — a 128 x 512 item moves 1.25x the bytes of a square one for
-// the same MFMA work, so it counts 9. INT8 items all have one shape.
-constexpr int kCostSquare = 8, kCostWide = 9;
 
 // Which variants run the 128 x 512 shape. The FP32-class BF16 engine moves
 // as many bytes per stage in either shape (the A planes are hi + lo), so a
@@ -638,19 +634,22 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   static_assert(!Q8 || !WIDE, "INT8 items are 64 x 512 only");
   constexpr bool kWide = WIDE;
 
-  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8). The
-  // square items (shared expert first, then routed, each in row-tile,
-  // column-tile order) are cut into 8 contiguous ranges of equal cost, one
-  // per XCD, and so are the small-group items (128 x 512); an XCD
-  // interleaves its two ranges. An item costs its K depth times its
-  // shape's cost, so the deeper shared items of the down GEMM do not pile
-  // up on one XCD, neighbouring square items (same expert, same rows) meet
-  // in one L2, an XCD's deeper items start first, and the weight streams of
-  // the small groups (little reuse) spread over every XCD's path to HBM.
+  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8).
+  // Three item lists — the shared expert's square items, the routed square
+  // items (each in row-tile, column-tile order) and the small-group items
+  // (128 x 512) — are each cut into 8 contiguous ranges of equal count, one
+  // per XCD. An XCD runs its shared items first (in the down GEMM they are
+  // twice as deep: the longest start first), then its routed square items
+  // with its small-group items spread evenly between them. Every XCD gets
+  // the same mix: a cost-weighted cut of one combined list had put all the
+  // deeper shared items on the first two XCDs, whose fewer, longer items
+  // then set the end of the launch (down span 177 us against 147-159 us on
+  // the other XCDs). Neighbouring square items (same expert, same rows) meet
+  // in one L2, and the weight streams of the small groups (little reuse)
+  // spread over every XCD's path to HBM.
   // Tile lists (dispatch): routed [0, c2) square, [c2, c1) last tiles of
-  // <= 128 rows (in two lists, <= 128 and <= 64, both run as 128 x 512),
-  // then the shared tiles; a variant without the wide shape runs them all
-  // as square items.
+  // <= 128 rows (run as 128 x 512), then the shared tiles; a variant
+  // without the wide shape runs them all as square items.
   const int all_tiles = S.counters[0];
   const int routed_tiles = S.counters[1];
   const int square_tiles = kWide ? S.counters[2] : routed_tiles;
@@ -664,46 +663,33 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
   const long long square_items = (long long)square_tiles * nt_routed;
   const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
-  const long long c_shared = (GATEUP ? L.H : L.S) * kCostSquare;
-  const long long c_square = (GATEUP ? L.H : L.I) * kCostSquare;
-  const long long c_wide = (GATEUP ? L.H : L.I) * kCostWide;
-  const long long cost1 = shared_items * c_shared;
-  const long long cost_sq = cost1 + square_items * c_square;
-  const long long cost_sm = wide_items * c_wide;
-  // First square item of XCD x: the first whose cost prefix reaches x / 8 of
-  // the square cost; likewise the first small-group item.
-  auto first_sq = [&](int x) -> long long {
-    const long long b = cost_sq * x / kXcds;
-    if (b <= cost1) return (b + c_shared - 1) / c_shared;
-    return shared_items + (b - cost1 + c_square - 1) / c_square;
-  };
-  auto first_sm = [&](int x) -> long long {
-    return (cost_sm * x / kXcds + c_wide - 1) / c_wide;
-  };
+  auto cut = [](long long n, int x) { return n * x / kXcds; };  // XCD x's first of n
   const int xcd = blockIdx.x % kXcds;
   const long long j = blockIdx.x / kXcds;
-  const long long sq0 = first_sq(xcd), n_sq = first_sq(xcd + 1) - sq0;
-  const long long sm0 = first_sm(xcd), n_sm = first_sm(xcd + 1) - sm0;
-  const long long n_xcd = n_sq + n_sm;
-  if (j >= n_xcd) return;
-  // The XCD's j-th workgroup: its small-group items are spread evenly
-  // between its square ones (local slot j is small when floor(j n_sm / n)
-  // steps), so the HBM-bound weight streams of small groups run alongside
-  // the L2-resident square work instead of all at once.
-  const long long sm_before = j * n_sm / n_xcd;
-  const bool take_small = (j + 1) * n_sm / n_xcd > sm_before;
+  const long long sh0 = cut(shared_items, xcd), n_sh = cut(shared_items, xcd + 1) - sh0;
+  const long long sq0 = cut(square_items, xcd), n_sq = cut(square_items, xcd + 1) - sq0;
+  const long long sm0 = cut(wide_items, xcd), n_sm = cut(wide_items, xcd + 1) - sm0;
+  if (j >= n_sh + n_sq + n_sm) return;
   int tile, ntile;
-  if (take_small) {
-    const long long i = sm0 + sm_before;
-    tile = square_tiles + (int)(i / nt_wide);
-    ntile = (int)(i % nt_wide);
+  bool take_small = false;
+  if (j < n_sh) {
+    const long long item = sh0 + j;
+    tile = routed_tiles + (int)(item / nt_shared);
+    ntile = (int)(item % nt_shared);
   } else {
-    const long long item = sq0 + (j - sm_before);
-    if (item < shared_items) {
-      tile = routed_tiles + (int)(item / nt_shared);
-      ntile = (int)(item % nt_shared);
+    // The XCD's remaining slots: its small-group items are spread evenly
+    // between its routed square ones (slot r is small when floor(r n_sm /
+    // n) steps), so the HBM-bound weight streams of small groups run
+    // alongside the L2-resident square work instead of all at once.
+    const long long r = j - n_sh, n_rest = n_sq + n_sm;
+    const long long sm_before = r * n_sm / n_rest;
+    take_small = (r + 1) * n_sm / n_rest > sm_before;
+    if (take_small) {
+      const long long i = sm0 + sm_before;
+      tile = square_tiles + (int)(i / nt_wide);
+      ntile = (int)(i % nt_wide);
     } else {
-      const long long i = item - shared_items;
+      const long long i = sq0 + (r - sm_before);
       tile = (int)(i / nt_routed);
       ntile = (int)(i % nt_routed);
     }
@@ -752,19 +738,15 @@ void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, h
 }
 
 // Workgroups: 8 XCDs times the most items one XCD can take. Items are
-// bounded by every row tile times the widest column count of its items
-// (a 128 x 512 item replaces two square ones; INT8 layers: 512 columns); an XCD's two ranges hold an
-// eighth of their cost each, so at most (bound / 8) * (dearest / cheapest
-// item) + 4 items.
+// bounded by every row tile times the widest column count of its items (a
+// 128 x 512 item replaces two square ones; INT8 layers: 512 columns); an
+// XCD takes an eighth of each of three lists, so at most bound / 8 + 3.
 static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   const int n = gateup ? std::max(2 * L.S, 2 * L.I) : L.H;
   const int item_n = L.quant_mode != kQuantNone ? 2 * kTileN : kTileN;  // INT8: 64 x 512
   const long long items = (long long)tiles_bound * ((n + item_n - 1) / item_n);
-  const long long k_routed = gateup ? L.H : L.I, k_shared = gateup ? L.H : L.S;
-  const long long dear = std::max(k_shared * kCostSquare, k_routed * kCostWide);
-  const long long cheap = std::min(k_shared, k_routed) * kCostSquare;
-  // Two ranges per XCD (square, wide), each at most one item over its share.
-  const long long per_xcd = (items * dear + kXcds * cheap - 1) / (kXcds * cheap) + 4;
+  // An XCD takes an eighth of each of its three lists, each rounded up.
+  const long long per_xcd = (items + kXcds - 1) / kXcds + 3;
   return (unsigned)(per_xcd * kXcds);
 }
 
