@@ -73,6 +73,10 @@ static const char* const kPhaseNames[kPhases] = {"router", "topk",   "dispatch",
 struct uocr_gpu_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  // Second stream of the MFMA engine: the shared expert's GEMMs run there,
+  // forked after the input planes and joined before the combine.
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
   char* scratch = nullptr;
   size_t scratch_limit = 0;
   int* err = nullptr;       // device error flag
@@ -198,16 +202,27 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
 
 // Where a forward runs: a scratch region and its size, the stream, the
 // device error flag, and the context whose phase timers apply (null: none).
+// side / fork / join: the second stream for the shared expert's GEMMs and
+// its events (side null: one stream). Phase timing keeps one stream so
+// that every phase's events bracket its own kernels.
 struct Exec {
   char* scratch;
   size_t limit;
   hipStream_t stream;
   int* err;
   uocr_gpu_ctx* timing;
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
 };
 
 Exec exec_of(uocr_gpu_ctx* ctx) {
-  return {ctx->scratch, ctx->scratch_limit, ctx->stream, ctx->err, ctx};
+  Exec ex{ctx->scratch, ctx->scratch_limit, ctx->stream, ctx->err, ctx};
+  if (ctx->timing_mask == 0) {
+    ex.side = ctx->side;
+    ex.fork = ctx->fork;
+    ex.join = ctx->join;
+  }
+  return ex;
 }
 
 Scratch carve(const Exec& ex, const ScratchPlan& p) {
@@ -425,6 +440,41 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
     phase_end(ctx);
     if (int r = trace_hidden(S.gu, S.gu + (size_t)L.K * L.I)) return r;
   } else {
+    // MFMA engine: the input planes, then (two streams) the shared expert's
+    // gate/up and down on the side stream, which needs no routing, while
+    // this stream routes and runs the routed experts; each launch's last
+    // round of items then overlaps the other stream's work. It pays where
+    // those tails are a large share (1024-token Zipf layer 0.257 -> 0.235
+    // ms) and costs at 4096 tokens (12-layer stack 6.25 -> 6.52 ms: with two
+    // kernels resident, a launch's workgroups no longer reach the XCDs in
+    // the order its item split assumes), so it is limited to
+    // kOverlapMaxTokens tokens.
+    constexpr size_t kOverlapMaxTokens = 2048;
+    uocr::MfmaPlanes P{};
+    // (Under DynamicActivations the small-batch engine's single-row pass on
+    // this stream touches only routed rows' hidden and output buffers.)
+    const bool overlap = mfma && ex.side && L.S > 0 && T <= kOverlapMaxTokens;
+    if (mfma) {
+      P.x_hi = S.xb;
+      P.x_lo = S.xb + T * L.H;
+      P.h_hi = reinterpret_cast<uint16_t*>(S.h);
+      P.h_lo = P.h_hi + T * L.K * L.I;
+      P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
+      P.hs_lo = P.hs_hi + T * L.S;
+      if (!planes_ready) {
+        phase_begin(ctx, kSplit);
+        uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+        phase_end(ctx);
+      }
+      if (overlap) {
+        const int shared_tiles = (Ti + bm - 1) / bm;
+        HIP_TRY(hipEventRecord(ex.fork, st), "fork event");
+        HIP_TRY(hipStreamWaitEvent(ex.side, ex.fork, 0), "fork wait");
+        uocr::launch_mfma_gateup(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
+        uocr::launch_mfma_down(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
+        HIP_TRY(hipEventRecord(ex.join, ex.side), "join event");
+      }
+    }
     if (T <= (size_t)uocr::kGemvChunk && !mfma && !int8) {
       // Few tokens: logits with every token staged once, then one
       // workgroup routes them and builds the dispatch.
@@ -485,18 +535,6 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       uocr::launch_i8_down(L, S, P, Ti, tiles_bound, st);
       phase_end(ctx);
     } else if (mfma) {
-      uocr::MfmaPlanes P;
-      P.x_hi = S.xb;
-      P.x_lo = S.xb + T * L.H;
-      P.h_hi = reinterpret_cast<uint16_t*>(S.h);
-      P.h_lo = P.h_hi + T * L.K * L.I;
-      P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
-      P.hs_lo = P.hs_hi + T * L.S;
-      if (!planes_ready) {
-        phase_begin(ctx, kSplit);
-        uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
-        phase_end(ctx);
-      }
       if (L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS) {
         // W8A8 for groups of one row (src/decoder/mod.rs:103-104): the
         // small-batch engine, run before the MFMA GEMMs reuse its f32
@@ -509,12 +547,14 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
         uocr::launch_batch_down(L, S, Ti, tiles_bound, uocr::kGemvChunk, st, true);
         phase_end(ctx);
       }
+      const int lists = overlap ? uocr::kListRouted : uocr::kListAll;
       phase_begin(ctx, kGateUp);
-      uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, st);
+      uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, lists, st);
       phase_end(ctx);
       phase_begin(ctx, kDown);
-      uocr::launch_mfma_down(L, S, P, Ti, tiles_bound, bf16_only, st);
+      uocr::launch_mfma_down(L, S, P, Ti, tiles_bound, bf16_only, lists, st);
       phase_end(ctx);
+      if (overlap) HIP_TRY(hipStreamWaitEvent(st, ex.join, 0), "join wait");
     } else {
       phase_begin(ctx, kGateUp);
       uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st);
@@ -598,6 +638,9 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   ctx->device = device;
   ctx->scratch_limit = scratch_limit;
   hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc(&ctx->scratch, scratch_limit);
   if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
@@ -614,11 +657,15 @@ void uocr_gpu_ctx_destroy(uocr_gpu_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->side) (void)hipStreamSynchronize(ctx->side);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->err) (void)hipFree(ctx->err);
   if (ctx->err_host) (void)hipHostFree(ctx->err_host);
   collect_timings(ctx);
   for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
+  if (ctx->fork) (void)hipEventDestroy(ctx->fork);
+  if (ctx->join) (void)hipEventDestroy(ctx->join);
+  if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }

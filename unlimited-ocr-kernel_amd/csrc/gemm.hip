@@ -627,9 +627,12 @@ constexpr int kWideMaxTokens = 2048;
 // Groups of one row are skipped when the overlay runs DynamicActivations
 // (the batch engine's W8A8 path owns them). NBUF_W: stage buffers of the
 // 128 x 512 shape.
+// lists: bit 0 the shared expert's items, bit 1 the routed experts'. The
+// shared expert's row tiles are [i * TM, ...) for TM the square items' rows
+// (the dispatch's row tile), so a shared-only launch needs no dispatch.
 template <int BK, int NBUF, int NBUF_W, bool SPLIT, bool GATEUP, bool Q8, bool WIDE>
 __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scratch S,
-                                                            MfmaPlanes P, int T) {
+                                                            MfmaPlanes P, int T, int lists) {
   extern __shared__ __align__(16) uint16_t lds[];  // [stage ring][INT8 scale groups]
   static_assert(!Q8 || !WIDE, "INT8 items are 64 x 512 only");
   constexpr bool kWide = WIDE;
@@ -648,11 +651,12 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   // in one L2, and the weight streams of the small groups (little reuse)
   // spread over every XCD's path to HBM.
   // Tile lists (dispatch): routed [0, c2) square, [c2, c1) last tiles of
-  // <= 128 rows (run as 128 x 512), then the shared tiles; a variant
-  // without the wide shape runs them all as square items.
-  const int all_tiles = S.counters[0];
-  const int routed_tiles = S.counters[1];
-  const int square_tiles = kWide ? S.counters[2] : routed_tiles;
+  // <= 128 rows (run as 128 x 512); a variant without the wide shape runs
+  // them all as square items. The shared expert's tiles follow from T.
+  constexpr int kSqTM = Q8 ? 64 : 256;
+  const int shared_tiles = (lists & 1) ? (T + kSqTM - 1) / kSqTM : 0;
+  const int routed_tiles = (lists & 2) ? S.counters[1] : 0;
+  const int square_tiles = kWide && (lists & 2) ? S.counters[2] : routed_tiles;
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
   // INT8 layers: every tile is 64 rows, every item 64 x 512.
@@ -660,7 +664,7 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   const int nt_routed = (n_routed + kItemN - 1) / kItemN;
   const int nt_wide = (n_routed + 2 * kTileN - 1) / (2 * kTileN);
   const int nt_shared = (n_shared + kItemN - 1) / kItemN;
-  const long long shared_items = (long long)(all_tiles - routed_tiles) * nt_shared;
+  const long long shared_items = (long long)shared_tiles * nt_shared;
   const long long square_items = (long long)square_tiles * nt_routed;
   const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
   auto cut = [](long long n, int x) { return n * x / kXcds; };  // XCD x's first of n
@@ -670,11 +674,12 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   const long long sq0 = cut(square_items, xcd), n_sq = cut(square_items, xcd + 1) - sq0;
   const long long sm0 = cut(wide_items, xcd), n_sm = cut(wide_items, xcd + 1) - sm0;
   if (j >= n_sh + n_sq + n_sm) return;
-  int tile, ntile;
+  int tile = -1, ntile, g, r0;
   bool take_small = false;
   if (j < n_sh) {
     const long long item = sh0 + j;
-    tile = routed_tiles + (int)(item / nt_shared);
+    g = L.E;
+    r0 = (int)(item / nt_shared) * kSqTM;
     ntile = (int)(item % nt_shared);
   } else {
     // The XCD's remaining slots: its small-group items are spread evenly
@@ -694,7 +699,10 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
       ntile = (int)(i % nt_routed);
     }
   }
-  const int g = S.tiles[2 * tile], r0 = S.tiles[2 * tile + 1];
+  if (tile >= 0) {
+    g = S.tiles[2 * tile];
+    r0 = S.tiles[2 * tile + 1];
+  }
   if (Q8 && g < L.E && L.quant_mode == kQuantDynamic &&
       S.offsets[g + 1] - S.offsets[g] == 1)
     return;
@@ -756,38 +764,38 @@ static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
 
 template <bool GATEUP>
 static void launch_mfma(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
-                        int tiles_bound, bool bf16_only, hipStream_t s) {
+                        int tiles_bound, bool bf16_only, int lists, hipStream_t s) {
   const dim3 grid(mfma_grid(L, tiles_bound, GATEUP)), block(512);
   if (L.quant_mode != kQuantNone) {
     if (bf16_only)
       UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQ, false, GATEUP, true, false)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 1, true, false), s>>>(L, S, P, T);
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 1, true, false), s>>>(L, S, P, T, lists);
     else
       UOCR_MFMA_KERNEL(kBkQ, kBufQ, kBufQ, true, GATEUP, true, false)
-          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 2, true, false), s>>>(L, S, P, T);
+          <<<grid, block, UOCR_MFMA_LDS(kBkQ, kBufQ, kBufQ, 2, true, false), s>>>(L, S, P, T, lists);
   } else if (bf16_only && T <= kWideMaxTokens) {
     UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false, true)
         <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false, true), s>>>(L, S,
-                                                                                         P, T);
+                                                                                         P, T, lists);
   } else if (bf16_only) {
     UOCR_MFMA_KERNEL(kBkBf16, kBufBf16, kBufBf16W, false, GATEUP, false, false)
         <<<grid, block, UOCR_MFMA_LDS(kBkBf16, kBufBf16, kBufBf16W, 1, false, false), s>>>(L, S,
-                                                                                          P, T);
+                                                                                          P, T, lists);
   } else {
     UOCR_MFMA_KERNEL(kBkSplit, kBufSplit, kBufSplit, true, GATEUP, false, true)
         <<<grid, block, UOCR_MFMA_LDS(kBkSplit, kBufSplit, kBufSplit, 2, false, true), s>>>(L, S,
-                                                                                           P, T);
+                                                                                           P, T, lists);
   }
 }
 
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
-                        int tiles_bound, bool bf16_only, hipStream_t s) {
-  launch_mfma<true>(L, S, P, T, tiles_bound, bf16_only, s);
+                        int tiles_bound, bool bf16_only, int lists, hipStream_t s) {
+  launch_mfma<true>(L, S, P, T, tiles_bound, bf16_only, lists, s);
 }
 
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
-                      int tiles_bound, bool bf16_only, hipStream_t s) {
-  launch_mfma<false>(L, S, P, T, tiles_bound, bf16_only, s);
+                      int tiles_bound, bool bf16_only, int lists, hipStream_t s) {
+  launch_mfma<false>(L, S, P, T, tiles_bound, bf16_only, lists, s);
 }
 
 void mfma_init_attributes() {

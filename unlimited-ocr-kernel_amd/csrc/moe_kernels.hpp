@@ -139,10 +139,12 @@ struct MfmaPlanes {
   uint16_t* hs_lo;
 };
 void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
+// lists: kListShared, kListRouted or both (the items each launch runs).
+constexpr int kListShared = 1, kListRouted = 2, kListAll = 3;
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
-                        int tiles_bound, bool bf16_only, hipStream_t s);
+                        int tiles_bound, bool bf16_only, int lists, hipStream_t s);
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
-                      int tiles_bound, bool bf16_only, hipStream_t s);
+                      int tiles_bound, bool bf16_only, int lists, hipStream_t s);
 constexpr int kMfmaBM = 256;
 constexpr int kMfmaQ8BM = 64;  // INT8 weights: 64-row tiles, 64 x 512 items
 void mfma_init_attributes();
