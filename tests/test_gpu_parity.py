@@ -347,6 +347,24 @@ def test_full_dynamic(ctx, full_dynamic, T):
     check_layer(full_dynamic, ctx, syn.activations(T, 1280, seed=300 + T))
 
 
+@pytest.mark.parametrize("kind", ["bf16", "int8", "w8a8"])
+def test_decode_many_tokens(ctx, full_bf16, full_int8, full_dynamic, kind):
+    """32 consecutive one-token forwards of different tokens at the model
+    shape, each against the oracle: state carried from one decode forward
+    to the next (scratch, routing, hidden values) would show here."""
+    case = {"bf16": full_bf16, "int8": full_int8, "w8a8": full_dynamic}[kind]
+    worst = 0.0
+    for i in range(32):
+        x = syn.activations(1, 1280, seed=5000 + i)
+        y, _ = case.run(ctx, x)
+        ref, _ = oracle_ref(case, x)
+        assert np.all(np.isfinite(y)), i
+        err = normwise(y, ref)
+        worst = max(worst, err)
+        assert err <= FP32_TOL, (i, err)
+    say(f"  {kind}: 32 one-token forwards, worst normwise {worst:.3e}")
+
+
 def _w8a8_trace(T, K, E):
     """Device buffers of uocr_w8a8_trace at the full layer shape."""
     S = FULL["inter"] * FULL["shared"]
