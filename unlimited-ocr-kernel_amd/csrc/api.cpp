@@ -639,8 +639,11 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   ctx->scratch_limit = scratch_limit;
   hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming);
+  // fork/join only order the two streams of this device, so a device-scope release is
+  // enough: no system-scope cache write-back and invalidate at each record.
+  const unsigned ev_flags = hipEventDisableTiming | hipEventDisableSystemFence;
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork, ev_flags);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join, ev_flags);
   if (e == hipSuccess) e = hipMalloc(&ctx->scratch, scratch_limit);
   if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));

@@ -357,7 +357,6 @@ constexpr int kRouteWaves = 16;
 
 __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(DeviceLayer L,
                                                                                Scratch S, int T) {
-  __shared__ RouteSmem rs[kRouteWaves];
   __shared__ unsigned long long masks[kRouteWaves];
   __shared__ int count[64];
   __shared__ int start[65];
@@ -366,8 +365,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(
   const bool mine = wave < T;
   // Waves past T route a neutral row (their result is not used).
   const float v = mine && lane < E ? S.logits[(size_t)wave * E + lane] : 0.0f;
-  const LdsRoute r = route_wave_lds(v, E, K, rs[wave]);
-  const float w = route_wave_weight(r, K, L.normalize, L.scale, rs[wave]);
+  const WaveSel r = route_wave_sel(v, E, K);
+  const float w = route_weight(r, L.normalize, L.scale);
   if (mine && !r.ok && lane == 0) raise_error(S.err, kErrNumerical);
   if (lane == 0) masks[wave] = mine ? r.mask : 0ull;
   __syncthreads();

@@ -72,7 +72,6 @@ struct GateUpSmem {
   float xs[kWide / kQBlock];
   float logits[64];
   unsigned long long mask;
-  RouteSmem rs;
 };
 
 // Stages the activation row (wave 0) into LDS, quantised per 32-block for
@@ -145,10 +144,10 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
   // workgroup's wave 0 also writes the logits, the routing and the
   // one-token dispatch (ids, weights, offsets, permutation, row tiles).
   if (wave == 0) {
-    const LdsRoute r = route_wave_lds(sm.logits[lane], L.E, L.K, sm.rs);
+    const WaveSel r = route_wave_sel(sm.logits[lane], L.E, L.K);
     if (lane == 0) sm.mask = r.mask;
     if (rb == 0) {
-      const float w = route_wave_weight(r, L.K, L.normalize, L.scale, sm.rs);
+      const float w = route_weight(r, L.normalize, L.scale);
       if (!r.ok && lane == 0) raise_error(S.err, kErrNumerical);
       const unsigned long long below_mask = r.mask & ((1ull << lane) - 1ull);
       const int asc = __popcll(below_mask);  // ascending slot / selected ids below lane

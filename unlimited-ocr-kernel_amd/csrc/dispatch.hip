@@ -187,7 +187,21 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // Raised issue priority, as the router's: this launch shares CUs with the
+  // shared expert's GEMM on a two-stream forward.
+  __builtin_amdgcn_s_setprio(3);
   const int c = blockIdx.x;
+  // Wave 0's lanes < 16 own the chunk's tokens; their selections and
+  // weights are loaded first, in flight while the counts are summed.
+  const int t = c * kChunk + lane;
+  const bool valid = wave == 0 && lane < kChunk && t < T;
+  int my_e[8];
+  float my_w[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    my_e[j] = (valid && j < K) ? ids[(size_t)t * K + j] : -1;
+    my_w[j] = (valid && j < K) ? w[(size_t)t * K + j] : 0.0f;
+  }
   // Thread (row = tid / 16, quad = tid % 16) sums experts 4 quad .. 4 quad + 3
   // of chunks row, row + 16, ...; 16 loads in flight per pass, chunks past
   // the end read as zero.
@@ -240,14 +254,9 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
   // among the chunk's earlier tokens of that expert is a popcount. One wave
   // sets and reads the masks: a wavefront-scope release/acquire pair around
   // a wave barrier orders every lane's atomicOr before any lane's read.
-  const int t = c * kChunk + lane;
-  const bool valid = lane < kChunk && t < T;
-  int my_e[8];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    my_e[j] = (valid && j < K) ? ids[(size_t)t * K + j] : -1;
+  for (int j = 0; j < 8; j++)
     if (my_e[j] >= 0) atomicOr(&emask[my_e[j]], 1ull << lane);
-  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -259,7 +268,7 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(
       const int e = my_e[j];
       const int pos = base[e] + __popcll(emask[e] & lt);
       perm_rows[pos] = t;
-      perm_w[pos] = w[(size_t)t * K + j];
+      perm_w[pos] = my_w[j];
       inv_pos[(size_t)t * K + j] = pos;
     }
   }

@@ -345,6 +345,12 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   constexpr int kLps = (kSplitA ? 1 : kSegA * kAPlanes) + kSegB + (Q8 ? 1 : 0);
   constexpr int kSub = BK / 16;
   const int grp = wave >> 2;
+  // A wave whose columns all lie past N (the second half of a 512-wide
+  // item over the last 256 columns: 2I = 1792 and H = 1280 are 3.5 and 2.5
+  // such items) keeps its share of the loads and every barrier but reads
+  // no fragments and issues no MFMAs; waves w and w + 4 share a SIMD, so
+  // each SIMD keeps one busy wave.
+  const bool wlive = (int)__builtin_amdgcn_readfirstlane(n0 + wn * kWc) < N;
   if constexpr (Q8)
     for (int part = 0; part < kSGroup; part++) issue_scales(0, part);
   for (int i = 0; i < kDepth; i++)
@@ -366,45 +372,47 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     };
     float bscale[kNi];
     uint4 qraw[kNi];
-    if constexpr (Q8) {
+    if (wlive) {
+      if constexpr (Q8) {
 #pragma unroll
-      for (int ni = 0; ni < kNi; ni++) {
-        const int row = wn * kWc + ni * 32 + fr;
-        bscale[ni] = *reinterpret_cast<const float*>(
-            reinterpret_cast<const char*>(lds) + sg_at + (ks / kSGroup) % 3 * sg_bytes +
-            row * (kSGroup * 4) + ((ks % kSGroup) ^ sws(row)) * 4);
-        qraw[ni] = *reinterpret_cast<const uint4*>(cur + b_at + row * BK + 16 * (fc ^ swzb(row)));
-      }
-    }
-#pragma unroll
-    for (int sub = 0; sub < kSub; sub++) {
-      const int c = Q8 ? 2 * fc + sub : 2 * sub + fc;
-#pragma unroll
-      for (int ni = 0; ni < kNi; ni++) {
-        if constexpr (Q8) {
-          // Eight int8 weights of row (output feature) wn*64 + 32 ni + fr,
-          // k = 16 fc + 8 sub ..: |q| <= 127 is exact in bf16 (the f32 of a
-          // small integer has zero low half), so the bf16 is its high half.
-          const uint32_t lo = sub ? qraw[ni].z : qraw[ni].x;
-          const uint32_t hi = sub ? qraw[ni].w : qraw[ni].y;
-          uint32_t hp[4];
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            const uint32_t word = j < 4 ? lo : hi;
-            const int s0 = 8 * (j & 3), s1 = s0 + 8;
-            const float w0 = (float)(int8_t)((word >> s0) & 0xffu);
-            const float w1 = (float)(int8_t)((word >> s1) & 0xffu);
-            hp[j / 2] = __builtin_amdgcn_perm(__float_as_uint(w1), __float_as_uint(w0), 0x07060302u);
-          }
-          fb[sub][ni] = as_bf16x8(make_uint4(hp[0], hp[1], hp[2], hp[3]));
-        } else {
-          fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
+        for (int ni = 0; ni < kNi; ni++) {
+          const int row = wn * kWc + ni * 32 + fr;
+          bscale[ni] = *reinterpret_cast<const float*>(
+              reinterpret_cast<const char*>(lds) + sg_at + (ks / kSGroup) % 3 * sg_bytes +
+              row * (kSGroup * 4) + ((ks % kSGroup) ^ sws(row)) * 4);
+          qraw[ni] = *reinterpret_cast<const uint4*>(cur + b_at + row * BK + 16 * (fc ^ swzb(row)));
         }
       }
 #pragma unroll
-      for (int mi = 0; mi < kMi; mi++) {
-        fa[sub][mi] = frag(cur, wm * kWr + mi * 32 + fr, c);
-        if constexpr (SPLIT) fl[sub][mi] = frag(cur + alo_at, wm * kWr + mi * 32 + fr, c);
+      for (int sub = 0; sub < kSub; sub++) {
+        const int c = Q8 ? 2 * fc + sub : 2 * sub + fc;
+#pragma unroll
+        for (int ni = 0; ni < kNi; ni++) {
+          if constexpr (Q8) {
+            // Eight int8 weights of row (output feature) wn*64 + 32 ni + fr,
+            // k = 16 fc + 8 sub ..: |q| <= 127 is exact in bf16 (the f32 of a
+            // small integer has zero low half), so the bf16 is its high half.
+            const uint32_t lo = sub ? qraw[ni].z : qraw[ni].x;
+            const uint32_t hi = sub ? qraw[ni].w : qraw[ni].y;
+            uint32_t hp[4];
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+              const uint32_t word = j < 4 ? lo : hi;
+              const int s0 = 8 * (j & 3), s1 = s0 + 8;
+              const float w0 = (float)(int8_t)((word >> s0) & 0xffu);
+              const float w1 = (float)(int8_t)((word >> s1) & 0xffu);
+              hp[j / 2] = __builtin_amdgcn_perm(__float_as_uint(w1), __float_as_uint(w0), 0x07060302u);
+            }
+            fb[sub][ni] = as_bf16x8(make_uint4(hp[0], hp[1], hp[2], hp[3]));
+          } else {
+            fb[sub][ni] = frag(cur + b_at, wn * kWc + ni * 32 + fr, c);
+          }
+        }
+#pragma unroll
+        for (int mi = 0; mi < kMi; mi++) {
+          fa[sub][mi] = frag(cur, wm * kWr + mi * 32 + fr, c);
+          if constexpr (SPLIT) fl[sub][mi] = frag(cur + alo_at, wm * kWr + mi * 32 + fr, c);
+        }
       }
     }
     if (steady)
@@ -423,47 +431,49 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
       c = GATEUP && !Q8 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0)
                         : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     };
-    if constexpr (Q8) {
-      // Tile by tile: the stage's partial (one 32-block of K) of tile t,
-      // while the block scales fold the partial of tile t - 1 into acc (one
-      // FMA per element, the scale of this lane's output feature); tile 0
-      // folds the previous stage's last tile, so only the last fold of the
-      // item waits for its MFMAs.
-      constexpr int kT = kMi * kNi;
+    if (wlive) {
+      if constexpr (Q8) {
+        // Tile by tile: the stage's partial (one 32-block of K) of tile t,
+        // while the block scales fold the partial of tile t - 1 into acc (one
+        // FMA per element, the scale of this lane's output feature); tile 0
+        // folds the previous stage's last tile, so only the last fold of the
+        // item waits for its MFMAs.
+        constexpr int kT = kMi * kNi;
 #pragma unroll
-      for (int t = 0; t < kT; t++) {
-        const int mi = t / kNi, ni = t % kNi;
-        floatx16 z = {};
-        part[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][mi], fb[0][ni], z, 0, 0, 0);
-        if constexpr (SPLIT) mma(fl[0][mi], fb[0][ni], part[mi][ni]);
+        for (int t = 0; t < kT; t++) {
+          const int mi = t / kNi, ni = t % kNi;
+          floatx16 z = {};
+          part[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][mi], fb[0][ni], z, 0, 0, 0);
+          if constexpr (SPLIT) mma(fl[0][mi], fb[0][ni], part[mi][ni]);
 #pragma unroll
-        for (int sub = 1; sub < kSub; sub++) {
-          mma(fa[sub][mi], fb[sub][ni], part[mi][ni]);
-          if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], part[mi][ni]);
-        }
-        const int pt = (t + kT - 1) % kT, pmi = pt / kNi, pni = pt % kNi;
-        const float sc = t == 0 ? last_scale : bscale[pni];
-#pragma unroll
-        for (int r = 0; r < 16; r++)
-          acc[pmi][pni][r] = __builtin_fmaf(part[pmi][pni][r], sc, acc[pmi][pni][r]);
-      }
-      last_scale = bscale[kNi - 1];
-      // One MFMA, then its share of the fold's FMAs (16 per tile), in turn.
-#pragma unroll
-      for (int i = 0; i < kT * kSub * kAPlanes; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 16 / (kSub * kAPlanes), 0);
-      }
-    } else {
-#pragma unroll
-      for (int sub = 0; sub < kSub; sub++)
-#pragma unroll
-        for (int mi = 0; mi < kMi; mi++)
-#pragma unroll
-          for (int ni = 0; ni < kNi; ni++) {
-            mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
-            if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
+          for (int sub = 1; sub < kSub; sub++) {
+            mma(fa[sub][mi], fb[sub][ni], part[mi][ni]);
+            if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], part[mi][ni]);
           }
+          const int pt = (t + kT - 1) % kT, pmi = pt / kNi, pni = pt % kNi;
+          const float sc = t == 0 ? last_scale : bscale[pni];
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            acc[pmi][pni][r] = __builtin_fmaf(part[pmi][pni][r], sc, acc[pmi][pni][r]);
+        }
+        last_scale = bscale[kNi - 1];
+        // One MFMA, then its share of the fold's FMAs (16 per tile), in turn.
+#pragma unroll
+        for (int i = 0; i < kT * kSub * kAPlanes; i++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 16 / (kSub * kAPlanes), 0);
+        }
+      } else {
+#pragma unroll
+        for (int sub = 0; sub < kSub; sub++)
+#pragma unroll
+          for (int mi = 0; mi < kMi; mi++)
+#pragma unroll
+            for (int ni = 0; ni < kNi; ni++) {
+              mma(fa[sub][mi], fb[sub][ni], acc[mi][ni]);
+              if constexpr (SPLIT) mma(fl[sub][mi], fb[sub][ni], acc[mi][ni]);
+            }
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();

@@ -173,10 +173,13 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     float* __restrict__ weights, int* __restrict__ chunk_counts, int* err) {
   __shared__ float part[kRouteWaves][kRouteChunk][65];
   __shared__ int cnt[64];
-  __shared__ RouteSmem rs[kRouteWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // Raised issue priority: on a two-stream forward this launch shares CUs
+  // with the shared expert's GEMM, whose waves would otherwise take turns
+  // with it on every SIMD.
+  __builtin_amdgcn_s_setprio(3);
   const int t0 = blockIdx.x * kRouteChunk;
   if (tid < 64) cnt[tid] = 0;
   const int ar = lane & 15;        // fragment row (token) / column (expert)
@@ -250,8 +253,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
 #pragma unroll
     for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][lane];
     if (live && lane < E) logits[(size_t)t * E + lane] = v;
-    const LdsRoute r = route_wave_lds(live ? v : 0.0f, E, K, rs[wave]);
-    const float wgt = route_wave_weight(r, K, normalize, scale, rs[wave]);
+    const WaveSel r = route_wave_sel(live ? v : 0.0f, E, K);
+    const float wgt = route_weight(r, normalize, scale);
     if (!live) continue;
     if (!r.ok && lane == 0) raise_error(err, kErrNumerical);
     if ((r.mask >> lane) & 1ull) {

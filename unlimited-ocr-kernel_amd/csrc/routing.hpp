@@ -61,30 +61,24 @@ __device__ inline WaveRoute route_wave(float v, int n, int K, int normalize, flo
 
 namespace uocr {
 
-// LDS staging for route_wave_lds (one token per wave).
-struct RouteSmem {
-  __attribute__((aligned(16))) float v[64];
-  __attribute__((aligned(16))) unsigned long long key[64];
-  float selp[64];
-};
-
-struct LdsRoute {
+struct WaveSel {
   bool ok;                   // false: non-finite logits (then ids 0..K-1, weights 0)
-  int rank;                  // this lane's position in (probability desc, id asc)
+  int rank;                  // selected lanes: position in (probability desc, id asc)
   float p;                   // this lane's probability
+  float den;                 // sum of the selected probabilities in selection order
   unsigned long long mask;   // bit e set: expert e selected
 };
 
-// Routing of one token by one wave on its own (no workgroup barrier; lane
-// = expert), with as few instructions as the math allows: the maximum and
-// the softmax sum are 16-lane DPP reductions combined over the 4 rows, each
-// lane's rank is the number of larger (probability, -id) keys, read back
-// from the wave's own LDS keys (a wave's LDS operations complete in order;
-// the wave barriers keep the compiler from moving reads above writes). The
-// probabilities are e / sum as ops::softmax computes them; only the order
-// of the 64-term sum differs from the reference's sequential one. Also
-// fills sm.selp with the selected probabilities in rank order for
-// route_wave_weight.
+// Routing of one token by one wave on its own (lane = expert; no LDS, no
+// workgroup barrier). The maximum and the softmax sum are 16-lane DPP
+// reductions combined over the 4 rows; the probabilities are e / sum as
+// ops::softmax computes them, only the order of the 64-term sum differing
+// from the reference's sequential one. The selection is K rounds of a wave
+// arg-max: the key is the probability's bit pattern plus one (a
+// non-negative float orders as its bits; 0 marks lanes out of the race),
+// ties go to the lowest lane, i.e. (probability desc, id asc) as
+// moe::route sorts (src/decoder/moe.rs:19). Each round's probability is
+// added to den in selection order, the renormalisation sum of :21-25.
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]
   v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]
@@ -92,7 +86,18 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
   return v;
 }
-__device__ inline LdsRoute route_wave_lds(float v, int n, int K, RouteSmem& sm) {
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_move_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_move_u32<0xB1>(v));
+  v = max(v, dpp_move_u32<0x4E>(v));
+  v = max(v, dpp_move_u32<0x141>(v));
+  v = max(v, dpp_move_u32<0x140>(v));
+  return v;
+}
+__device__ inline WaveSel route_wave_sel(float v, int n, int K) {
   const int lane = threadIdx.x & 63;
   const bool live = lane < n;
   const bool bad = __ballot(live && (isnan(v) || v == INFINITY)) != 0ull;
@@ -100,12 +105,13 @@ __device__ inline LdsRoute route_wave_lds(float v, int n, int K, RouteSmem& sm) 
   auto at = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
   const float vr = row16_max(live ? v : -INFINITY);
   const float m = fmaxf(fmaxf(at(vr, 0), at(vr, 16)), fmaxf(at(vr, 32), at(vr, 48)));
-  LdsRoute r;
+  WaveSel r;
   if (bad || !isfinite(m)) {
     // Distinct ids 0..K-1 with weight 0 keep any dispatch a permutation.
     r.ok = false;
     r.rank = lane;
     r.p = 0.0f;
+    r.den = 1.0f;
     r.mask = K >= 64 ? ~0ull : ((1ull << K) - 1ull);
     return r;
   }
@@ -113,34 +119,37 @@ __device__ inline LdsRoute route_wave_lds(float v, int n, int K, RouteSmem& sm) 
   const float sr = row16_sum(ex);
   const float sum = (at(sr, 0) + at(sr, 16)) + (at(sr, 32) + at(sr, 48));
   const float p = ex / sum;
-  const unsigned long long key =
-      live ? ((unsigned long long)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)lane) : 0ull;
-  sm.key[lane] = key;
-  __builtin_amdgcn_wave_barrier();
-  int rank = 0;
-#pragma unroll
-  for (int e = 0; e < 64; e += 2) {
-    const ulonglong2 u = *reinterpret_cast<const ulonglong2*>(&sm.key[e]);
-    rank += (u.x > key ? 1 : 0) + (u.y > key ? 1 : 0);
+  uint32_t cand = live ? __float_as_uint(p) + 1u : 0u;
+  int rank = 64;
+  float den = -0.0f;
+  for (int j = 0; j < K; j++) {
+    const uint32_t cr = row16_max_u32(cand);
+    const uint32_t top = max(max((uint32_t)__builtin_amdgcn_readlane((int)cr, 0),
+                                 (uint32_t)__builtin_amdgcn_readlane((int)cr, 16)),
+                             max((uint32_t)__builtin_amdgcn_readlane((int)cr, 32),
+                                 (uint32_t)__builtin_amdgcn_readlane((int)cr, 48)));
+    if (top == 0u) break;  // fewer than K experts
+    const int id = __ffsll((long long)__ballot(cand == top)) - 1;
+    if (lane == id) {
+      rank = j;
+      cand = 0u;
+    }
+    den += __uint_as_float(top - 1u);
   }
   r.ok = true;
   r.rank = rank;
   r.p = p;
-  r.mask = __ballot(live && rank < K);
-  if (live && rank < K) sm.selp[rank] = p;
-  __builtin_amdgcn_wave_barrier();
+  r.den = den;
+  r.mask = __ballot(rank < K);
   return r;
 }
 
-// Routing weights of the selected lanes (route_wave_lds ranks < K): the
-// renormalisation sums the top-k probabilities in selection order
-// (src/decoder/moe.rs:21-25), then scales (:26-28).
-__device__ inline float route_wave_weight(const LdsRoute& r, int K, int normalize, float scale,
-                                          const RouteSmem& sm) {
+// Routing weight of a selected lane: the renormalisation adds 1e-20 to
+// the selection-order sum (src/decoder/moe.rs:21-25), then the scale
+// (:26-28).
+__device__ __forceinline__ float route_weight(const WaveSel& r, int normalize, float scale) {
   if (!r.ok) return 0.0f;
-  float den = -0.0f;
-  for (int j = 0; j < K; j++) den += sm.selp[j];
-  den = normalize ? den + 1e-20f : 1.0f;
+  const float den = normalize ? r.den + 1e-20f : 1.0f;
   return r.p / den * scale;
 }
 
