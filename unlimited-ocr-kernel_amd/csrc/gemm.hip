@@ -647,19 +647,23 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   static_assert(!Q8 || !WIDE, "INT8 items are 64 x 512 only");
   constexpr bool kWide = WIDE;
 
-  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8).
-  // Three item lists — the shared expert's square items, the routed square
-  // items (each in row-tile, column-tile order) and the small-group items
-  // (128 x 512) — are each cut into 8 contiguous ranges of equal count, one
-  // per XCD. An XCD runs its shared items first (in the down GEMM they are
-  // twice as deep: the longest start first), then its routed square items
-  // with its small-group items spread evenly between them. Every XCD gets
-  // the same mix: a cost-weighted cut of one combined list had put all the
-  // deeper shared items on the first two XCDs, whose fewer, longer items
-  // then set the end of the launch (down span 177 us against 147-159 us on
-  // the other XCDs). Neighbouring square items (same expert, same rows) meet
-  // in one L2, and the weight streams of the small groups (little reuse)
-  // spread over every XCD's path to HBM.
+  // ---- work item. Workgroup ids reach the XCDs round-robin (id % 8), and
+  // an XCD starts its workgroups in id order as its CUs free up. Five item
+  // lists — the shared expert's items; the routed square items and the
+  // small-group items (128 x 512) whose column tile is whole; then those
+  // two kinds over a last, half-empty column tile (2I = 1792 and H = 1280
+  // are 3.5 and 2.5 tiles of 512: half their waves idle, ~0.6 of an item) —
+  // are each cut into 8 contiguous ranges of equal count, one per XCD. An
+  // XCD runs its shared items first (in the down GEMM they are twice as
+  // deep), then its whole-tile square items with its whole-tile small ones
+  // spread evenly between them, then its half-tile items: the longest
+  // first, so the round that ends the launch holds the shortest items.
+  // Every XCD gets the same mix: a cost-weighted cut of one combined list
+  // had put all the deeper shared items on the first two XCDs, whose
+  // fewer, longer items then set the end of the launch (down span 177 us
+  // against 147-159 us on the other XCDs). Neighbouring square items (same
+  // expert, same rows) meet in one L2, and the weight streams of the small
+  // groups (little reuse) spread over every XCD's path to HBM.
   // Tile lists (dispatch): routed [0, c2) square, [c2, c1) last tiles of
   // <= 128 rows (run as 128 x 512); a variant without the wide shape runs
   // them all as square items. The shared expert's tiles follow from T.
@@ -667,6 +671,7 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   const int shared_tiles = (lists & 1) ? (T + kSqTM - 1) / kSqTM : 0;
   const int routed_tiles = (lists & 2) ? S.counters[1] : 0;
   const int square_tiles = kWide && (lists & 2) ? S.counters[2] : routed_tiles;
+  const int wide_tiles = routed_tiles - square_tiles;
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
   // INT8 layers: every tile is 64 rows, every item 64 x 512.
@@ -674,39 +679,58 @@ __global__ __launch_bounds__(512, 1) void mfma_group_kernel(DeviceLayer L, Scrat
   const int nt_routed = (n_routed + kItemN - 1) / kItemN;
   const int nt_wide = (n_routed + 2 * kTileN - 1) / (2 * kTileN);
   const int nt_shared = (n_shared + kItemN - 1) / kItemN;
+  // Column tiles past the last whole one (0 or 1 per row tile).
+  const int half_sq = n_routed % kItemN != 0 && n_routed % kItemN <= kItemN / 2 ? 1 : 0;
+  const int half_w = n_routed % (2 * kTileN) != 0 && n_routed % (2 * kTileN) <= kTileN ? 1 : 0;
+  const int nf_sq = nt_routed - half_sq, nf_w = nt_wide - half_w;
   const long long shared_items = (long long)shared_tiles * nt_shared;
-  const long long square_items = (long long)square_tiles * nt_routed;
-  const long long wide_items = (long long)(routed_tiles - square_tiles) * nt_wide;
+  const long long sqf_items = (long long)square_tiles * nf_sq;
+  const long long wf_items = (long long)wide_tiles * nf_w;
+  const long long sqh_items = (long long)square_tiles * half_sq;
+  const long long wh_items = (long long)wide_tiles * half_w;
   auto cut = [](long long n, int x) { return n * x / kXcds; };  // XCD x's first of n
   const int xcd = blockIdx.x % kXcds;
-  const long long j = blockIdx.x / kXcds;
+  long long j = blockIdx.x / kXcds;
   const long long sh0 = cut(shared_items, xcd), n_sh = cut(shared_items, xcd + 1) - sh0;
-  const long long sq0 = cut(square_items, xcd), n_sq = cut(square_items, xcd + 1) - sq0;
-  const long long sm0 = cut(wide_items, xcd), n_sm = cut(wide_items, xcd + 1) - sm0;
-  if (j >= n_sh + n_sq + n_sm) return;
+  const long long sq0 = cut(sqf_items, xcd), n_sq = cut(sqf_items, xcd + 1) - sq0;
+  const long long sm0 = cut(wf_items, xcd), n_sm = cut(wf_items, xcd + 1) - sm0;
+  const long long hq0 = cut(sqh_items, xcd), n_hq = cut(sqh_items, xcd + 1) - hq0;
+  const long long hw0 = cut(wh_items, xcd), n_hw = cut(wh_items, xcd + 1) - hw0;
+  if (j >= n_sh + n_sq + n_sm + n_hq + n_hw) return;
   int tile = -1, ntile, g, r0;
   bool take_small = false;
+  // Slot r of n_a + n_b slots interleaving two lists: the b item index when
+  // floor(r n_b / n) steps (b items spread evenly), else the a index.
+  auto spread = [](long long r, long long n_a, long long n_b, bool& is_b) {
+    const long long b_before = r * n_b / (n_a + n_b);
+    is_b = (r + 1) * n_b / (n_a + n_b) > b_before;
+    return is_b ? b_before : r - b_before;
+  };
   if (j < n_sh) {
     const long long item = sh0 + j;
     g = L.E;
     r0 = (int)(item / nt_shared) * kSqTM;
     ntile = (int)(item % nt_shared);
-  } else {
-    // The XCD's remaining slots: its small-group items are spread evenly
-    // between its routed square ones (slot r is small when floor(r n_sm /
-    // n) steps), so the HBM-bound weight streams of small groups run
-    // alongside the L2-resident square work instead of all at once.
-    const long long r = j - n_sh, n_rest = n_sq + n_sm;
-    const long long sm_before = r * n_sm / n_rest;
-    take_small = (r + 1) * n_sm / n_rest > sm_before;
+  } else if ((j -= n_sh) < n_sq + n_sm) {
+    // The small-group items spread between the square ones, so the
+    // HBM-bound weight streams of small groups run alongside the
+    // L2-resident square work instead of all at once.
+    const long long i = spread(j, n_sq, n_sm, take_small);
     if (take_small) {
-      const long long i = sm0 + sm_before;
-      tile = square_tiles + (int)(i / nt_wide);
-      ntile = (int)(i % nt_wide);
+      tile = square_tiles + (int)((sm0 + i) / nf_w);
+      ntile = (int)((sm0 + i) % nf_w);
     } else {
-      const long long i = sq0 + (r - sm_before);
-      tile = (int)(i / nt_routed);
-      ntile = (int)(i % nt_routed);
+      tile = (int)((sq0 + i) / nf_sq);
+      ntile = (int)((sq0 + i) % nf_sq);
+    }
+  } else {
+    const long long i = spread(j - n_sq - n_sm, n_hq, n_hw, take_small);
+    if (take_small) {
+      tile = square_tiles + (int)(hw0 + i);
+      ntile = nt_wide - 1;
+    } else {
+      tile = (int)(hq0 + i);
+      ntile = nt_routed - 1;
     }
   }
   if (tile >= 0) {
@@ -758,13 +782,13 @@ void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, h
 // Workgroups: 8 XCDs times the most items one XCD can take. Items are
 // bounded by every row tile times the widest column count of its items (a
 // 128 x 512 item replaces two square ones; INT8 layers: 512 columns); an
-// XCD takes an eighth of each of three lists, so at most bound / 8 + 3.
+// XCD takes an eighth of each of five lists, so at most bound / 8 + 5.
 static unsigned mfma_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   const int n = gateup ? std::max(2 * L.S, 2 * L.I) : L.H;
   const int item_n = L.quant_mode != kQuantNone ? 2 * kTileN : kTileN;  // INT8: 64 x 512
   const long long items = (long long)tiles_bound * ((n + item_n - 1) / item_n);
-  // An XCD takes an eighth of each of its three lists, each rounded up.
-  const long long per_xcd = (items + kXcds - 1) / kXcds + 3;
+  // An XCD takes an eighth of each of its five lists, each rounded up.
+  const long long per_xcd = (items + kXcds - 1) / kXcds + 5;
   return (unsigned)(per_xcd * kXcds);
 }
 
