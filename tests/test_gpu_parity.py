@@ -530,6 +530,25 @@ def test_int8_mfma(ctx, full_int8, full_dynamic, T):
         assert (counts == 1).any(), counts  # the W8A8 single-row path ran
 
 
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_one_stream_matches_two_streams(ctx, full_bf16, full_int8, kind):
+    """Up to 2048 tokens the shared expert's GEMMs run on a second stream
+    after a split of the input into bf16 planes; on one stream (phase
+    timing on) the router writes those planes itself. Same bits either way,
+    in both activation classes."""
+    case = full_bf16 if kind == "bf16" else full_int8
+    x = syn.activations(512, 1280, seed=811)
+    for flags, name in ((0, "fp32-class"), (um.FLAG_BF16_ACTIVATIONS, "bf16 activations")):
+        say(f"{kind} T=512 {name}: two streams vs one")
+        y2, _ = case.run(ctx, x, flags=um.FLAG_FORCE_MFMA | flags)
+        ctx.set_timing("all")
+        try:
+            y1, _ = case.run(ctx, x, flags=um.FLAG_FORCE_MFMA | flags)
+        finally:
+            ctx.set_timing(())
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), name
+
+
 @pytest.fixture(scope="module")
 def hot_bf16(ctx):
     hot = syn.route_profile(syn.hot_share(FULL["experts"], 6, 8, 0.8), 6)

@@ -461,19 +461,28 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       P.h_lo = P.h_hi + T * L.K * L.I;
       P.hs_hi = reinterpret_cast<uint16_t*>(S.hs);
       P.hs_lo = P.hs_hi + T * L.S;
-      if (!planes_ready) {
-        phase_begin(ctx, kSplit);
-        uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
-        phase_end(ctx);
-      }
-      if (overlap) {
-        const int shared_tiles = (Ti + bm - 1) / bm;
-        HIP_TRY(hipEventRecord(ex.fork, st), "fork event");
-        HIP_TRY(hipStreamWaitEvent(ex.side, ex.fork, 0), "fork wait");
-        uocr::launch_mfma_gateup(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
-        uocr::launch_mfma_down(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
-        HIP_TRY(hipEventRecord(ex.join, ex.side), "join event");
-      }
+    }
+    // One stream: the fused MFMA router writes the planes itself (it reads
+    // every value of x once anyway), so no split launch precedes it. Two
+    // streams keep the split first, so that the fork comes before the
+    // routing and the shared expert's GEMMs reach the CUs ahead of the
+    // routed ones (forking after the router took the 512-token INT8 layer
+    // from 0.165 to 0.199 ms; forking first with a side-stream copy of the
+    // planes measured the same as the split here).
+    const bool fused_router = T > (size_t)uocr::kGemvChunk && uocr::router_mfma_supported(L.H);
+    const bool router_planes = mfma && !planes_ready && fused_router && !overlap;
+    if (mfma && !planes_ready && !router_planes) {
+      phase_begin(ctx, kSplit);
+      uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+      phase_end(ctx);
+    }
+    if (overlap) {
+      const int shared_tiles = (Ti + bm - 1) / bm;
+      HIP_TRY(hipEventRecord(ex.fork, st), "fork event");
+      HIP_TRY(hipStreamWaitEvent(ex.side, ex.fork, 0), "fork wait");
+      uocr::launch_mfma_gateup(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
+      uocr::launch_mfma_down(L, S, P, Ti, shared_tiles, bf16_only, uocr::kListShared, ex.side);
+      HIP_TRY(hipEventRecord(ex.join, ex.side), "join event");
     }
     if (T <= (size_t)uocr::kGemvChunk && !mfma && !int8) {
       // Few tokens: logits with every token staged once, then one
@@ -481,11 +490,13 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       phase_begin(ctx, kRouter);
       uocr::launch_small_route(S.xn, L, S, Ti, st);
       phase_end(ctx);
-    } else if (T > (size_t)uocr::kGemvChunk && uocr::router_mfma_supported(L.H)) {
+    } else if (fused_router) {
       // Many tokens: fused MFMA router + top-k, then the chunked dispatch.
       phase_begin(ctx, kRouter);
       uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
-                                    S.logits, S.topk_ids, S.topk_w, S.chunk_counts, S.err, st);
+                                    S.logits, S.topk_ids, S.topk_w, S.chunk_counts,
+                                    router_planes ? P.x_hi : nullptr,
+                                    router_planes && !bf16_only ? P.x_lo : nullptr, S.err, st);
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
       uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, narrow, S.chunk_counts,

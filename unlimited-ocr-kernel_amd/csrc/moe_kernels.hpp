@@ -91,9 +91,12 @@ void launch_topk(const float* logits, int T, int E, int K, int normalize, float 
 
 // The fused router covers hidden widths up to 2048 (64 K steps of 32).
 inline bool router_mfma_supported(int H) { return H % 32 == 0 && H <= 2048; }
+// x_hi (and x_lo) set: also writes the bf16 hi (and lo) planes of x that
+// the MFMA grouped GEMM reads, as launch_split_planes would.
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
-                             int* chunk_counts, int* err, hipStream_t s);
+                             int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
+                             hipStream_t s);
 
 // dispatch.hip
 // narrow > 0 moves each expert's last tile of at most `narrow` rows into a

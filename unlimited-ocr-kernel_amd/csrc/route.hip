@@ -170,7 +170,8 @@ template <int KS>
 __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ w, int T, int H, int E, int K,
     int normalize, float scale, float* __restrict__ logits, int* __restrict__ ids,
-    float* __restrict__ weights, int* __restrict__ chunk_counts, int* err) {
+    float* __restrict__ weights, int* __restrict__ chunk_counts, uint16_t* __restrict__ x_hi,
+    uint16_t* __restrict__ x_lo, int* err) {
   __shared__ float part[kRouteWaves][kRouteChunk][65];
   __shared__ int cnt[64];
   const int tid = threadIdx.x;
@@ -212,6 +213,14 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
   floatx4 acc[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ni++) acc[ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // The grouped GEMM's input planes (x_hi set): hi = bf16(x), lo = bf16(x
+  // - hi), the first two of the three terms below, written for this
+  // workgroup's tokens through a resource over exactly their rows (the
+  // rows past T and the steps past H / 32 fall outside it).
+  const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+      x_hi ? x_hi + (size_t)t0 * H : nullptr, 0, (int)((uint32_t)nt * H * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
+      x_lo ? x_lo + (size_t)t0 * H : nullptr, 0, (int)((uint32_t)nt * H * 2u), 0x00020000);
 #pragma unroll
   for (int i = 0; i < KS; i++) {
     const float xv[8] = {__uint_as_float(xa[i].x), __uint_as_float(xa[i].y),
@@ -228,6 +237,14 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
       hi[j] = h;
       mid[j] = m;
       lo[j] = (__bf16)(r1 - (float)m);
+    }
+    if (x_hi) {
+      const int st = wave + kRouteWaves * i;
+      int off = st < steps ? (int)(((uint32_t)ar * H + (uint32_t)st * 32u + aq) * 2u) : (int)kFar;
+      asm volatile("" : "+v"(off));  // the whole offset in the range-checked VGPR field
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), hr, off, 0, 0);
+      if (x_lo) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, mid), lr, off, 0, 0);
     }
 #pragma unroll
     for (int ni = 0; ni < 4; ni++) {
@@ -269,16 +286,17 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
 
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
-                             int* chunk_counts, int* err, hipStream_t s) {
+                             int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
+                             hipStream_t s) {
   if (T <= 0 || !router_mfma_supported(H)) return;
   const dim3 grid((T + kRouteChunk - 1) / kRouteChunk), block(64 * kRouteWaves);
   const int ks = (H / 32 + kRouteWaves - 1) / kRouteWaves;
   if (ks <= 5)
     router_mfma_kernel<5><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, err);
+                                                 weights, chunk_counts, x_hi, x_lo, err);
   else
     router_mfma_kernel<8><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, err);
+                                                 weights, chunk_counts, x_hi, x_lo, err);
 }
 
 void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
