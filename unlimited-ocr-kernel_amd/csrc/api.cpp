@@ -766,10 +766,13 @@ int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
     }
     return e;
   };
-  void *router = nullptr, *w13 = nullptr, *w2 = nullptr, *norm = nullptr;
+  void *router = nullptr, *w13 = nullptr, *w2 = nullptr, *w13k = nullptr, *w2k = nullptr,
+       *norm = nullptr;
   hipError_t e = alloc(E * H * 2, &router);
   if (e == hipSuccess) e = alloc(n13 * 2, &w13);
   if (e == hipSuccess) e = alloc(n2 * 2, &w2);
+  if (e == hipSuccess) e = alloc(n13 * 2, &w13k);
+  if (e == hipSuccess) e = alloc(n2 * 2, &w2k);
   if (e == hipSuccess) e = alloc(H * 4, &norm);
   if (e != hipSuccess) {
     uocr_moe_layer_destroy(layer);
@@ -797,6 +800,14 @@ int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
   if ((e = hipMemcpyAsync(static_cast<char*>(w2) + E * H * I * 2, w->shared_down, H * S * 2, kind,
                           st)) != hipSuccess)
     return finish(hip_fail(e, "upload shared down"));
+  // The MFMA engine's k-blocked panels of the same matrices.
+  uocr::launch_panelize(w13, w13k, 2, (int)(2 * I), (int)H, (int)E, st);
+  uocr::launch_panelize(static_cast<char*>(w13) + E * 2 * I * H * 2,
+                        static_cast<char*>(w13k) + E * 2 * I * H * 2, 2, (int)(2 * S), (int)H, 1, st);
+  uocr::launch_panelize(w2, w2k, 2, (int)H, (int)I, (int)E, st);
+  uocr::launch_panelize(static_cast<char*>(w2) + E * H * I * 2, static_cast<char*>(w2k) + E * H * I * 2,
+                        2, (int)H, (int)S, 1, st);
+  if ((e = hipGetLastError()) != hipSuccess) return finish(hip_fail(e, "weight panels"));
   if (w->norm_weight) {
     void* tmp = nullptr;
     if ((e = hipMalloc(&tmp, H * 2)) != hipSuccess) return finish(hip_fail(e, "norm staging"));
@@ -816,6 +827,8 @@ int uocr_moe_layer_create(uocr_gpu_ctx* ctx, const uocr_moe_config* cfg,
   L.router = static_cast<const uint16_t*>(router);
   L.w13 = static_cast<const uint16_t*>(w13);
   L.w2 = static_cast<const uint16_t*>(w2);
+  L.w13k = static_cast<const uint16_t*>(w13k);
+  L.w2k = static_cast<const uint16_t*>(w2k);
   *out = layer;
   return UOCR_OK;
 }
@@ -841,7 +854,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   DeviceLayer& L = layer->dev;
   const size_t H = L.H, I = L.I, S = L.S, E = L.E;
   const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
-  void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr;
+  void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr, *q13k = nullptr, *q2k = nullptr;
   std::vector<void*> fresh;
   auto alloc = [&](size_t bytes, void** p) -> hipError_t {
     hipError_t e = hipMalloc(p, bytes);
@@ -856,6 +869,8 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   if (e == hipSuccess) e = alloc(n13 / 32 * 4, &s13);
   if (e == hipSuccess) e = alloc(n2, &q2);
   if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2);
+  if (e == hipSuccess) e = alloc(n13, &q13k);
+  if (e == hipSuccess) e = alloc(n2, &q2k);
   if (e != hipSuccess) return release(hip_fail(e, "INT8 allocation"));
   const hipMemcpyKind kind = kind_of(where);
   hipStream_t st = ctx->stream;
@@ -885,6 +900,13 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
       (e = hipMemcpyAsync(static_cast<char*>(s2) + E * H * (I / 32) * 4, w->shared_down_scales,
                           H * (S / 32) * 4, kind, st)) != hipSuccess)
     return release(hip_fail(e, "upload INT8 down"));
+  // The MFMA engine's k-blocked panels of the int8 values.
+  uocr::launch_panelize(q13, q13k, 1, (int)(2 * I), (int)H, (int)E, st);
+  uocr::launch_panelize(static_cast<char*>(q13) + E * 2 * I * H, static_cast<char*>(q13k) + E * 2 * I * H,
+                        1, (int)(2 * S), (int)H, 1, st);
+  uocr::launch_panelize(q2, q2k, 1, (int)H, (int)I, (int)E, st);
+  uocr::launch_panelize(static_cast<char*>(q2) + E * H * I, static_cast<char*>(q2k) + E * H * I, 1,
+                        (int)H, (int)S, 1, st);
   // Validate the uploaded values on the device.
   HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), st), "clear flag");
   hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q13, n13,
@@ -897,7 +919,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
                                                  : "INT8 scales must be finite and nonnegative"));
   }
   // Replace any previous overlay.
-  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2}) {
+  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2, (void*)L.q13k, (void*)L.q2k}) {
     if (!p) continue;
     for (auto it = layer->allocations.begin(); it != layer->allocations.end(); ++it)
       if (*it == p) {
@@ -907,11 +929,13 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     (void)hipFree(p);
   }
   for (void* p : fresh) layer->allocations.push_back(p);
-  layer->bytes += n13 + n13 / 32 * 4 + n2 + n2 / 32 * 4;
+  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + n2 / 32 * 4;
   L.q13 = static_cast<const int8_t*>(q13);
   L.s13 = static_cast<const float*>(s13);
   L.q2 = static_cast<const int8_t*>(q2);
   L.s2 = static_cast<const float*>(s2);
+  L.q13k = static_cast<const int8_t*>(q13k);
+  L.q2k = static_cast<const int8_t*>(q2k);
   L.quant_mode = mode;
   layer->quant_mode = mode;
   return UOCR_OK;

@@ -222,7 +222,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   for (int i = 0; i < kSegB; i++) {
     const int r = (segB0 + i) * kSegRowsB + lane / kCprB;
     const int c = (lane % kCprB) ^ swzb(r);
-    b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * row_bytes_b + 16u * c : kDmaOut;
+    // Weights come from the k-blocked panels ([K/32][N][BK]): a stage's rows
+    // are one contiguous run of N * BK elements.
+    b_off[i] = n0 + r < N ? (uint32_t)(n0 + r) * (BK * (Q8 ? 1u : 2u)) + 16u * c : kDmaOut;
   }
   const int nblk = K / kQBlock;
   static_assert(!Q8 || TN == WAVES * 64, "a scale group is one dword load per wave and stage");
@@ -242,10 +244,10 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   const void* wmat;
   const float* wscale = nullptr;
   if constexpr (Q8) {
-    wmat = GATEUP ? (const void*)(L.q13 + L.w13_offset(g)) : (const void*)(L.q2 + L.w2_offset(g));
+    wmat = GATEUP ? (const void*)(L.q13k + L.w13_offset(g)) : (const void*)(L.q2k + L.w2_offset(g));
     wscale = GATEUP ? L.s13 + L.s13_offset(g) : L.s2 + L.s2_offset(g);
   } else {
-    wmat = GATEUP ? (const void*)(L.w13 + L.w13_offset(g)) : (const void*)(L.w2 + L.w2_offset(g));
+    wmat = GATEUP ? (const void*)(L.w13k + L.w13_offset(g)) : (const void*)(L.w2k + L.w2_offset(g));
   }
   const i32x4 rs_a = buffer_rsrc(a_hi_src, a_rows * row_bytes);
   const i32x4 rs_l = buffer_rsrc(a_lo_src, a_rows * row_bytes);
@@ -290,7 +292,7 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     }
 #pragma unroll
     for (int i = 0; i < kSegB; i++)
-      buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + (Q8 ? (uint32_t)k0 : kb));
+      buffer_load_lds16(rs_b, lds_b + st + i * 1024u, b_off[i] + (uint32_t)k0 * (Q8 ? 1u : 2u) * (uint32_t)N);
     if constexpr (Q8) {
       const int stage = k0 / BK;
       issue_scales(stage / kSGroup + 1, stage % kSGroup);
@@ -830,6 +832,27 @@ void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes
 void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
                       int tiles_bound, bool bf16_only, int lists, hipStream_t s) {
   launch_mfma<false>(L, S, P, T, tiles_bound, bf16_only, lists, s);
+}
+
+// One 16-byte chunk per thread: chunk c of (matrix, block kb, row n).
+__global__ __launch_bounds__(256) void panelize_kernel(const uint4* __restrict__ in, uint4* __restrict__ out,
+                                                       int N, int K, int cpb, size_t total) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const size_t per_matrix = (size_t)N * (K / 32) * cpb;  // chunks per matrix
+  const size_t m = i / per_matrix, rest = i % per_matrix;
+  const size_t kb = rest / ((size_t)N * cpb), n = (rest / cpb) % N, c = rest % cpb;
+  // Source: row n, elements 32 kb .. (chunk c); K / 32 * cpb chunks per row.
+  out[i] = in[m * per_matrix + n * (size_t)(K / 32) * cpb + kb * cpb + c];
+}
+
+void launch_panelize(const void* in, void* out, int elem_bytes, int N, int K, int groups,
+                     hipStream_t s) {
+  if (N <= 0 || K <= 0 || groups <= 0) return;
+  const int cpb = 32 * elem_bytes / 16;  // 16-byte chunks per 32-element block
+  const size_t total = (size_t)groups * N * (K / 32) * cpb;
+  hipLaunchKernelGGL(panelize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     (const uint4*)in, (uint4*)out, N, K, cpb, total);
 }
 
 void mfma_init_attributes() {

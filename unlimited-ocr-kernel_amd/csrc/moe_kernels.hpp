@@ -30,6 +30,14 @@ struct DeviceLayer {
   const int8_t* q2;
   const float* s2;
   const float* norm_w;       // [H] post-attention RMSNorm weight (f32)
+  // The MFMA engine's copies of w13 / w2 (BF16) and q13 / q2 (INT8 overlay)
+  // in k-blocked panels: each group's [N rows, K] matrix as [K/32][N][32],
+  // so the 32-deep stage of a row tile is one contiguous run (same group
+  // offsets as the row-major arrays).
+  const uint16_t* w13k;
+  const uint16_t* w2k;
+  const int8_t* q13k;
+  const int8_t* q2k;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
   __host__ __device__ size_t n13() const { return ((size_t)E * 2 * I + 2 * (size_t)S) * H; }
@@ -151,6 +159,10 @@ void launch_mfma_down(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& 
 constexpr int kMfmaBM = 256;
 constexpr int kMfmaQ8BM = 64;  // INT8 weights: 64-row tiles, 64 x 512 items
 void mfma_init_attributes();
+// out = `groups` row-major [N, K] matrices (elem_bytes 1 or 2, K % 32 == 0,
+// matrix g at g * N * K) as k-blocked panels [K/32][N][32].
+void launch_panelize(const void* in, void* out, int elem_bytes, int N, int K, int groups,
+                     hipStream_t s);
 
 // gemm_i8.hip: int8 x int8 grouped GEMM with int32 block accumulation (the
 // opt-in UOCR_FLAG_INT8_MFMA mode). Activations enter quantised per 32-block.
