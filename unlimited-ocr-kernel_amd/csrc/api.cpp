@@ -473,7 +473,7 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
     const bool router_planes = mfma && !planes_ready && fused_router && !overlap;
     if (mfma && !planes_ready && !router_planes) {
       phase_begin(ctx, kSplit);
-      uocr::launch_split_planes(S.xn, T * L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
+      uocr::launch_split_planes(S.xn, Ti, L.H, P.x_hi, bf16_only ? nullptr : P.x_lo, st);
       phase_end(ctx);
     }
     if (overlap) {

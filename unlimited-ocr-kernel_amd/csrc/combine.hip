@@ -92,8 +92,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(
     row[it] = acc;
   }
   if constexpr (NORM)
-    norm_row(row, H, nn.w, nn.eps, nn.out + (size_t)t * H, nn.hi ? nn.hi + (size_t)t * H : nullptr,
-             nn.lo ? nn.lo + (size_t)t * H : nullptr, err);
+    norm_row(row, H, nn.w, nn.eps, nn.out + (size_t)t * H, nn.hi, nn.lo, err, (int)gridDim.x, t);
 }
 
 void launch_combine(const Scratch& S, const float* residual, int T, int H, int K, float* out,
@@ -124,9 +123,8 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_kernel(const float* __re
     if (i >= width) break;
     row[it] = *reinterpret_cast<const float4*>(x + (size_t)t * width + i);
   }
-  norm_row(row, width, nn.w, nn.eps, nn.out + (size_t)t * width,
-           nn.hi ? nn.hi + (size_t)t * width : nullptr, nn.lo ? nn.lo + (size_t)t * width : nullptr,
-           err);
+  norm_row(row, width, nn.w, nn.eps, nn.out + (size_t)t * width, nn.hi, nn.lo, err, (int)gridDim.x,
+           t);
 }
 
 // Wider rows: one workgroup per row, scalar passes.

@@ -40,12 +40,15 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// Split FP32 activations [rows, K] into bf16 hi and lo planes.
-__global__ void split_planes_kernel(const float* __restrict__ x, size_t n,
+// Split FP32 activations [rows, K] into bf16 hi and lo planes, k-blocked
+// ([K/32][rows][32], as the GEMM reads them).
+__global__ void split_planes_kernel(const float* __restrict__ x, int rows, int K,
                                     uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
-  size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  if (i >= n) return;
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= (size_t)rows * K) return;
   const float4 v = *reinterpret_cast<const float4*>(x + i);
+  const size_t t = i / K, k = i % K;
+  const size_t o = ((k / 32) * rows + t) * 32 + k % 32;
   const float f[4] = {v.x, v.y, v.z, v.w};
   uint16_t h[4], l[4];
 #pragma unroll
@@ -53,10 +56,10 @@ __global__ void split_planes_kernel(const float* __restrict__ x, size_t n,
     h[j] = bf16_bits(f[j]);
     l[j] = bf16_bits(f[j] - __uint_as_float((uint32_t)h[j] << 16));
   }
-  *reinterpret_cast<uint2*>(hi + i) =
+  *reinterpret_cast<uint2*>(hi + o) =
       make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
   if (lo)
-    *reinterpret_cast<uint2*>(lo + i) =
+    *reinterpret_cast<uint2*>(lo + o) =
         make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
 }
 
@@ -214,9 +217,9 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
     const int r = (segA0 + i) * kSegRows + lane / kCpr;
     const int c = (lane % kCpr) ^ swz(r);
     const int src_row = a_source(r);
-    // x planes are row-major [T, H]; the h planes the gate/up epilogue
-    // writes are k-blocked ([W/32][rows][32]: each stage's rows contiguous).
-    a_off[i] = src_row >= 0 ? (uint32_t)src_row * (GATEUP ? row_bytes : 64u) + 16u * c : kDmaOut;
+    // The x planes and the h planes the gate/up epilogue writes are
+    // k-blocked ([K/32][rows][32]: a stage's panel holds every row's 32 k).
+    a_off[i] = src_row >= 0 ? (uint32_t)src_row * 64u + 16u * c : kDmaOut;
   }
 #pragma unroll
   for (int i = 0; i < kSegB; i++) {
@@ -279,8 +282,7 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   };
   auto issue = [&](int buf, int k0) {
     const uint32_t st = (uint32_t)buf * stage_bytes;
-    const uint32_t kb = (uint32_t)k0 * 2u;
-    const uint32_t ka = GATEUP ? kb : (uint32_t)(k0 / 32) * a_rows * 64u;
+    const uint32_t ka = (uint32_t)(k0 / 32) * a_rows * 64u;
     if constexpr (kSplitA) {
       buffer_load_lds16(rs_a1, lds_a1 + st, a_off[0] + ka);
     } else {
@@ -774,11 +776,12 @@ constexpr size_t mfma_lds_bytes() {
 constexpr int kBkBf16 = 32, kBufBf16 = 4, kBufBf16W = 3, kBkSplit = 32, kBufSplit = 3;
 constexpr int kBkQ = 32, kBufQ = 4;
 
-void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s) {
-  if (n == 0) return;
-  const size_t threads = (n + 3) / 4;
+void launch_split_planes(const float* x, int rows, int K, uint16_t* hi, uint16_t* lo,
+                         hipStream_t s) {
+  if (rows <= 0) return;
+  const size_t threads = ((size_t)rows * K + 3) / 4;
   hipLaunchKernelGGL(split_planes_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     s, x, n, hi, lo);
+                     s, x, rows, K, hi, lo);
 }
 
 // Workgroups: 8 XCDs times the most items one XCD can take. Items are

@@ -81,7 +81,7 @@ struct Scratch {
   float* y;         // [T*K, H] routed expert outputs in dispatched order
   float* ys;        // [T, H] shared expert output
   float* xn;        // [T, H] normalised block input
-  uint16_t* xb;     // [2, T, H] bf16 planes of the layer input (MFMA engine)
+  uint16_t* xb;     // [2][H/32][T][32] bf16 planes (hi, lo) of the layer input (MFMA engine)
   float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
   int8_t* q8x;      // int8 mode: quantised input [T, H] and hidden rows [T*K*I + T*S]
   float* q8s;       // int8 mode: their block scales [T*H/32 + (T*K*I + T*S)/32]
@@ -100,7 +100,7 @@ void launch_topk(const float* logits, int T, int E, int K, int normalize, float 
 // The fused router covers hidden widths up to 2048 (64 K steps of 32).
 inline bool router_mfma_supported(int H) { return H % 32 == 0 && H <= 2048; }
 // x_hi (and x_lo) set: also writes the bf16 hi (and lo) planes of x that
-// the MFMA grouped GEMM reads, as launch_split_planes would.
+// the MFMA grouped GEMM reads ([H/32][T][32]), as launch_split_planes would.
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
@@ -142,14 +142,15 @@ void gemv_init_attributes();
 // gemm.hip: MFMA grouped GEMM engine. Activations enter as bf16 planes
 // (hi, and lo for FP32-class precision).
 struct MfmaPlanes {
-  uint16_t* x_hi;   // [T, H]
+  uint16_t* x_hi;   // [H/32][T][32] (k-blocked)
   uint16_t* x_lo;
   uint16_t* h_hi;   // [T*K, I] routed hidden, dispatched order
   uint16_t* h_lo;
   uint16_t* hs_hi;  // [T, S] shared hidden
   uint16_t* hs_lo;
 };
-void launch_split_planes(const float* x, size_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
+void launch_split_planes(const float* x, int rows, int K, uint16_t* hi, uint16_t* lo,
+                         hipStream_t s);
 // lists: kListShared, kListRouted or both (the items each launch runs).
 constexpr int kListShared = 1, kListRouted = 2, kListAll = 3;
 void launch_mfma_gateup(const DeviceLayer& L, const Scratch& S, const MfmaPlanes& P, int T,
@@ -194,8 +195,9 @@ void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, cons
                          float* out, hipStream_t s);
 
 // combine.hip
-// RMSNorm output of a row: the normalised row (out) and optionally its
-// bf16 planes (hi, and lo for FP32-class precision).
+// RMSNorm output of rows: the normalised rows (out, [T, H]) and optionally
+// their bf16 planes (hi, and lo for FP32-class precision), k-blocked
+// ([H/32][T][32]) as the MFMA engine reads them.
 struct RowNorm {
   const float* w = nullptr;
   float eps = 0.0f;

@@ -214,13 +214,13 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
 #pragma unroll
   for (int ni = 0; ni < 4; ni++) acc[ni] = floatx4{0.f, 0.f, 0.f, 0.f};
   // The grouped GEMM's input planes (x_hi set): hi = bf16(x), lo = bf16(x
-  // - hi), the first two of the three terms below, written for this
-  // workgroup's tokens through a resource over exactly their rows (the
-  // rows past T and the steps past H / 32 fall outside it).
+  // - hi), the first two of the three terms below, k-blocked ([H/32][T][32]:
+  // step st of token t at (st T + t) 32), through a resource over the whole
+  // plane; tokens past T and steps past H / 32 store nothing.
   const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-      x_hi ? x_hi + (size_t)t0 * H : nullptr, 0, (int)((uint32_t)nt * H * 2u), 0x00020000);
+      x_hi, 0, (int)((uint32_t)T * H * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
-      x_lo ? x_lo + (size_t)t0 * H : nullptr, 0, (int)((uint32_t)nt * H * 2u), 0x00020000);
+      x_lo, 0, (int)((uint32_t)T * H * 2u), 0x00020000);
 #pragma unroll
   for (int i = 0; i < KS; i++) {
     const float xv[8] = {__uint_as_float(xa[i].x), __uint_as_float(xa[i].y),
@@ -240,7 +240,9 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     }
     if (x_hi) {
       const int st = wave + kRouteWaves * i;
-      int off = st < steps ? (int)(((uint32_t)ar * H + (uint32_t)st * 32u + aq) * 2u) : (int)kFar;
+      int off = st < steps && ar < nt
+                    ? (int)((((uint32_t)st * T + (uint32_t)(t0 + ar)) * 32u + aq) * 2u)
+                    : (int)kFar;
       asm volatile("" : "+v"(off));  // the whole offset in the range-checked VGPR field
       typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), hr, off, 0, 0);

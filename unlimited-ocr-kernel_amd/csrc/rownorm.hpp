@@ -18,10 +18,12 @@ constexpr int kRowThreads = 256, kRowChunks = 2;
 // The sum runs per thread over its chunks (x, y, z, w in turn), then over
 // the wave and the four waves in order, so the standalone and the fused
 // norms give the same bits. Writes the normalised row and, when hi is set,
-// its bf16 planes (hi = bf16(v), lo = bf16(v - hi) when lo is set).
+// its bf16 planes (hi = bf16(v), lo = bf16(v - hi) when lo is set): row t
+// of `rows` into planes laid out [width/32][rows][32], as the MFMA engine
+// reads them (hi / lo are the planes' bases).
 __device__ inline void norm_row(const float4 (&v)[kRowChunks], int width, const float* __restrict__ w,
                                 float eps, float* __restrict__ out, uint16_t* __restrict__ hi,
-                                uint16_t* __restrict__ lo, int* err) {
+                                uint16_t* __restrict__ lo, int* err, int rows = 0, int t = 0) {
   __shared__ float partial[kRowThreads / 64];
   __shared__ int bad_any;
   const int tid = threadIdx.x;
@@ -59,16 +61,17 @@ __device__ inline void norm_row(const float4 (&v)[kRowChunks], int width, const 
                         x.w * scale * wv[it].w};
     *reinterpret_cast<float4*>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
     if (hi) {
+      const size_t p = ((size_t)(i / 32) * rows + t) * 32 + i % 32;
       uint16_t h[4], l[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         h[j] = __builtin_bit_cast(uint16_t, (__bf16)o[j]);
         l[j] = __builtin_bit_cast(uint16_t, (__bf16)(o[j] - __uint_as_float((uint32_t)h[j] << 16)));
       }
-      *reinterpret_cast<uint2*>(hi + i) =
+      *reinterpret_cast<uint2*>(hi + p) =
           make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
       if (lo)
-        *reinterpret_cast<uint2*>(lo + i) =
+        *reinterpret_cast<uint2*>(lo + p) =
             make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
     }
   }
