@@ -177,7 +177,8 @@ const char* uocr_last_error(const uocr_gpu_ctx* ctx);
  * reference's per-phase Timings, src/model/mod.rs:36-45). Bit i of
  * phase_mask brackets every launch of phase i with events; totals
  * accumulate until read. Phases, in bit order: router, topk, dispatch,
- * split, gateup, down, combine, norm. 0 disables timing. */
+ * split, gateup, down, combine, norm, decode (the one-token engine's
+ * single launch). 0 disables timing. */
 typedef struct uocr_phase_time {
   const char* name;
   uint64_t launches;
@@ -187,6 +188,13 @@ int uocr_gpu_ctx_set_timing(uocr_gpu_ctx* ctx, uint32_t phase_mask);
 /* Synchronises, then copies up to `cap` phase totals (all phases when cap
  * allows) and resets them. *count receives the number of phases. */
 int uocr_gpu_ctx_timings(uocr_gpu_ctx* ctx, uocr_phase_time* out, size_t cap, size_t* count);
+/* No counterpart in the reference: a diagnostic control for the one-token
+ * engine, whose single launch has workgroups wait for others (bounded
+ * polls; a wait that reaches its bound raises Resource and the launch
+ * still ends). polls < 0 restores the default bound (~100 ms); 0 makes
+ * every wait that is not already satisfied give up at once, which is how
+ * the tests drive that error path. */
+int uocr_gpu_ctx_set_wait_limit(uocr_gpu_ctx* ctx, int polls);
 /* Bytes of scratch a forward of T tokens needs (CpuContext::check_elements,
  * src/cpu/mod.rs:73-78); forwards above the context's limit fail with
  * Resource. */
@@ -237,16 +245,20 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * allocation). Same engines and results as uocr_moe_forward_async, but its
  * scratch is a static device array of UOCR_STATIC_SCRATCH_BYTES per GPU
  * (held until the process ends) instead of a context's reservation, and it
- * calls no allocating routine. Forwards whose uocr_moe_scratch_bytes
- * exceeds UOCR_STATIC_SCRATCH_BYTES - 256 fail with Resource (at the model
- * shape: up to about 126 tokens). Every call on one GPU shares that GPU's
+ * calls no allocating routine. Its first UOCR_STATIC_RESERVED_BYTES hold
+ * the device flag and the one-token engine's synchronisation words;
+ * forwards whose uocr_moe_scratch_bytes exceeds UOCR_STATIC_SCRATCH_BYTES -
+ * UOCR_STATIC_RESERVED_BYTES fail with Resource (at the model shape: up to
+ * 117 tokens). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU race, so serialise them (one
  * stream, or events). Enqueued on `stream` (a hipStream_t; NULL: the null
  * stream) and returns once queued. Device-side errors (non-finite
- * routing, normalisation or W8A8 inputs: Numerical) are written as a
- * status code to *device_status (a device int32 the call first clears; NULL:
- * an internal flag nobody reads). No trace, no phase timers. */
+ * routing, normalisation or W8A8 inputs: Numerical; a one-token launch
+ * whose workgroups did not all run: Resource) are written as a status code
+ * to *device_status (a device int32 the call first clears; NULL: an
+ * internal flag nobody reads). No trace, no phase timers. */
 #define UOCR_STATIC_SCRATCH_BYTES (16u << 20)
+#define UOCR_STATIC_RESERVED_BYTES (256u + (64u << 10))
 int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t T, float* y,
                             uint32_t flags, int32_t* device_status, void* stream);
 /* The post-attention half of Decoder::layer (src/decoder/mod.rs:351-363)

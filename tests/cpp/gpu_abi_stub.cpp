@@ -32,6 +32,7 @@ void uocr_gpu_ctx_destroy(uocr_gpu_ctx*) {}
 void* uocr_gpu_ctx_stream(uocr_gpu_ctx*) { return nullptr; }
 int uocr_gpu_ctx_synchronize(uocr_gpu_ctx*) { return unsupported(); }
 int uocr_gpu_ctx_set_timing(uocr_gpu_ctx*, uint32_t) { return unsupported(); }
+int uocr_gpu_ctx_set_wait_limit(uocr_gpu_ctx*, int) { return unsupported(); }
 int uocr_gpu_ctx_timings(uocr_gpu_ctx*, uocr_phase_time*, size_t, size_t*) {
   return unsupported();
 }

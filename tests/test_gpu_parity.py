@@ -6,6 +6,7 @@ oracle's logits tie within 1e-6; int8 x int8 block accumulators bit-exact;
 outputs within a normwise 1e-3 (max over rows of ||y - ref||_inf /
 ||ref||_inf) on FP32-accumulate paths.
 """
+import itertools
 import sys
 
 import numpy as np
@@ -41,11 +42,18 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+_CASE_IDS = itertools.count()
+
+
 class Case:
     """A layer in oracle form and uploaded to the GPU."""
 
     def __init__(self, ctx, shape, top_k, seed, quant=orc.QUANT_NONE, normalize=True, scale=1.0,
                  router_scale=None):
+        # A serial number, not id(): a freed case's id can come back for the
+        # next one, and the oracle cache must never serve one case's result
+        # for another.
+        self.uid = next(_CASE_IDS)
         self.shape = shape
         self.top_k = top_k
         w = syn.moe_weights(seed=seed, router_scale=router_scale, norm=True, **shape)
@@ -107,7 +115,7 @@ _REF_CACHE = {}
 
 
 def oracle_ref(case, x):
-    key = (id(case), x.shape, hash(x.tobytes()))
+    key = (case.uid, x.shape, x.tobytes())
     if key not in _REF_CACHE:
         _REF_CACHE[key] = orc.moe_experts(case.orc, x, trace=True)
     return _REF_CACHE[key]
@@ -363,6 +371,57 @@ def test_decode_many_tokens(ctx, full_bf16, full_int8, full_dynamic, kind):
         worst = max(worst, err)
         assert err <= FP32_TOL, (i, err)
     say(f"  {kind}: 32 one-token forwards, worst normwise {worst:.3e}")
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
+    """48 one-token forwards queued back to back (one synchronisation at the
+    end), each against the oracle. The decode engine's single launch orders
+    its workgroups through counts and flags that every launch must leave
+    at zero: a word left set would let the next launch read logits or
+    hidden values before they are written."""
+    case = {"bf16": full_bf16, "int8": full_int8}[kind]
+    xs = [syn.activations(1, 1280, seed=7000 + i) for i in range(48)]
+    xd = [dev(x) for x in xs]
+    yd = [torch.full_like(x, float("nan")) for x in xd]
+    torch.cuda.synchronize()
+    for x, y in zip(xd, yd):
+        um.forward(ctx, case.layer, x, y, sync=False)
+    ctx.synchronize()
+    worst = 0.0
+    for i, (x, y) in enumerate(zip(xs, yd)):
+        got = y.cpu().numpy()
+        ref, _ = oracle_ref(case, x)
+        err = normwise(got, ref)
+        worst = max(worst, err)
+        assert np.all(np.isfinite(got)) and err <= FP32_TOL, (i, err)
+    say(f"  {kind}: 48 queued one-token forwards, worst normwise {worst:.3e}")
+
+
+def test_decode_wait_bound(ctx, full_int8):
+    """The one-token engine's cross-workgroup waits are bounded. With the
+    bound at 0 polls, the down workgroups' wait for the hidden rows cannot
+    be satisfied at its first poll (those rows come microseconds later):
+    the forward reports Resource and the launch still ends. The words it
+    leaves set are cleared with the error, so the same context at the
+    default bound gives the right result again, twice in a row."""
+    case = full_int8
+    x = syn.activations(1, 1280, seed=9100)
+    ref, _ = oracle_ref(case, x)
+    c2 = um.Context(0, 64 << 20)
+    try:
+        c2.set_wait_limit(0)
+        xd, yd = dev(x), torch.empty((1, 1280), device="cuda")
+        torch.cuda.synchronize()
+        with pytest.raises(um.UocrError) as e:
+            um.forward(c2, case.layer, xd, yd)
+        assert e.value.status == um.RESOURCE
+        c2.set_wait_limit(-1)
+        for _ in range(2):
+            um.forward(c2, case.layer, xd, yd)
+            assert normwise(yd.cpu().numpy(), ref) <= FP32_TOL
+    finally:
+        c2.close()
 
 
 def _w8a8_trace(T, K, E):

@@ -77,7 +77,7 @@ def test_static_forward_matches_context_forward(setup, sizes):
 def test_static_forward_limits_and_errors(setup):
     ctx, cfg, layer, qlayer, ow = setup
     big = 1
-    while um.scratch_bytes(cfg, big + 1) <= um.STATIC_SCRATCH_BYTES - 256:
+    while um.scratch_bytes(cfg, big + 1) <= um.STATIC_SCRATCH_BYTES - um.STATIC_RESERVED_BYTES:
         big += 1
     say(f"largest static forward: {big} tokens")
     x = syn.activations(big, H, seed=77)

@@ -66,9 +66,15 @@ int set_last_error(int status, const char* message) {
 }
 }  // namespace uocr::host
 
-enum Phase { kRouter, kTopk, kDispatch, kSplit, kGateUp, kDown, kCombine, kNorm, kPhases };
-static const char* const kPhaseNames[kPhases] = {"router", "topk",   "dispatch", "split",
-                                                 "gateup", "down",   "combine",  "norm"};
+enum Phase { kRouter, kTopk, kDispatch, kSplit, kGateUp, kDown, kCombine, kNorm, kDecode, kPhases };
+static const char* const kPhaseNames[kPhases] = {"router", "topk",    "dispatch", "split", "gateup",
+                                                 "down",   "combine", "norm",     "decode"};
+
+// The context's flag allocation: the device error flag at byte 0, the
+// decode engine's cross-workgroup words (zeroed once, zero again after
+// every launch) from byte kSyncOffset.
+constexpr size_t kSyncOffset = 256;
+constexpr size_t kFlagBytes = kSyncOffset + uocr::kDecodeSyncBytes;
 
 struct uocr_gpu_ctx {
   int device = 0;
@@ -81,6 +87,7 @@ struct uocr_gpu_ctx {
   size_t scratch_limit = 0;
   int* err = nullptr;       // device error flag
   int* err_host = nullptr;  // pinned readback
+  int wait_limit = -1;      // decode engine's wait bound in polls (< 0: its default)
   // Phase timing: bit i of timing_mask enables phase i.
   uint32_t timing_mask = 0;
   std::vector<hipEvent_t> free_events;
@@ -213,10 +220,14 @@ struct Exec {
   uocr_gpu_ctx* timing;
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  int* sync = nullptr;  // the decode engine's cross-workgroup words (zero between launches)
+  int wait_limit = -1;  // the decode engine's wait bound in polls (< 0: its default)
 };
 
 Exec exec_of(uocr_gpu_ctx* ctx) {
   Exec ex{ctx->scratch, ctx->scratch_limit, ctx->stream, ctx->err, ctx};
+  ex.sync = reinterpret_cast<int*>(reinterpret_cast<char*>(ctx->err) + kSyncOffset);
+  ex.wait_limit = ctx->wait_limit;
   if (ctx->timing_mask == 0) {
     ex.side = ctx->side;
     ex.fork = ctx->fork;
@@ -248,6 +259,8 @@ Scratch carve(const Exec& ex, const ScratchPlan& p) {
   s.q8x = reinterpret_cast<int8_t*>(b + p.q8x);
   s.q8s = reinterpret_cast<float*>(b + p.q8s);
   s.err = ex.err;
+  s.sync = ex.sync;
+  s.wait_limit = ex.wait_limit;
   return s;
 }
 
@@ -323,9 +336,12 @@ int read_and_clear_error(uocr_gpu_ctx* ctx) {
   HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
   int e = *ctx->err_host;
   if (e != 0) {
-    HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), ctx->stream), "clear device error flag");
+    // The decode engine's words too: a wait that gave up (Resource) can
+    // leave a flag that its producer set later.
+    HIP_TRY(hipMemsetAsync(ctx->err, 0, kFlagBytes, ctx->stream), "clear device error flag");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
-    return fail(e, e == UOCR_ERR_NUMERICAL ? "nonfinite numerical input on device"
+    return fail(e, e == UOCR_ERR_NUMERICAL  ? "nonfinite numerical input on device"
+                   : e == UOCR_ERR_RESOURCE ? "a one-token launch's cross-workgroup wait reached its bound"
                                             : "device reported an error");
   }
   return UOCR_OK;
@@ -430,13 +446,10 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
   if (tiles_bound > 65535)
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
   if (engine == Engine::Decode) {
-    // One token: two launches with no routing launch of their own (every
-    // routed gate/up workgroup computes the router logits and routes).
-    phase_begin(ctx, kGateUp);
-    uocr::launch_decode_stage(1, L, S, residual, y, st);
-    phase_end(ctx);
-    phase_begin(ctx, kDown);
-    uocr::launch_decode_stage(2, L, S, residual, y, st);
+    // One token: one launch, its workgroups ordered by the words at S.sync.
+    if (!S.sync) return fail(UOCR_ERR_UNSUPPORTED, "decode engine without its sync words");
+    phase_begin(ctx, kDecode);
+    uocr::launch_decode(L, S, residual, y, st);
     phase_end(ctx);
     if (int r = trace_hidden(S.gu, S.gu + (size_t)L.K * L.I)) return r;
   } else {
@@ -602,18 +615,28 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
 // ------------------------------------------------ allocation-free forward
 //
 // Scratch of uocr_moe_forward_static: one array of UOCR_STATIC_SCRATCH_BYTES
-// per GPU, held until the process ends. Its first 256 bytes hold the device
-// error flag when the caller passes none; the forward's scratch follows. In
+// per GPU, held until the process ends. Its first kStaticFlagBytes hold the
+// device error flag when the caller passes none and, from byte kSyncOffset,
+// the decode engine's cross-workgroup words (cleared at every call); the
+// forward's scratch follows. In
 // host code `scratch` only names the host-side stand-in: the device address
 // comes from hipGetSymbolAddress, once per device, and only that address is
 // ever passed to kernels.
 
 constexpr int kMaxStaticDevices = 64;
-constexpr size_t kStaticFlagBytes = 256;
+constexpr size_t kStaticFlagBytes = kFlagBytes;
+static_assert(kStaticFlagBytes == UOCR_STATIC_RESERVED_BYTES, "static reservation");
 std::mutex g_static_mu;
 char* g_static_base[kMaxStaticDevices] = {};
 
-__global__ void clear_flag_kernel(int* flag) { *flag = 0; }
+// Clears the error flag and the decode engine's words at the start of each
+// static forward (256 threads, 16 bytes each per pass).
+__global__ void clear_flag_kernel(int* flag, int* sync) {
+  if (threadIdx.x == 0) *flag = 0;
+  uint4* w = reinterpret_cast<uint4*>(sync);
+  for (size_t i = threadIdx.x; i < uocr::kDecodeSyncBytes / 16; i += blockDim.x)
+    w[i] = make_uint4(0, 0, 0, 0);
+}
 
 // The device address of this device's array (the device must be current).
 int static_scratch_of(int device, char** out) {
@@ -656,9 +679,9 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork, ev_flags);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join, ev_flags);
   if (e == hipSuccess) e = hipMalloc(&ctx->scratch, scratch_limit);
-  if (e == hipSuccess) e = hipMalloc(&ctx->err, sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&ctx->err, kFlagBytes);
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
-  if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->err, 0, kFlagBytes);
   if (e != hipSuccess) {
     uocr_gpu_ctx_destroy(ctx);
     return hip_fail(e, "context allocation");
@@ -695,6 +718,12 @@ int uocr_gpu_ctx_synchronize(uocr_gpu_ctx* ctx) {
 int uocr_gpu_ctx_set_timing(uocr_gpu_ctx* ctx, uint32_t phase_mask) {
   if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
   ctx->timing_mask = phase_mask;
+  return UOCR_OK;
+}
+
+int uocr_gpu_ctx_set_wait_limit(uocr_gpu_ctx* ctx, int polls) {
+  if (!ctx) return fail(UOCR_ERR_SHAPE, "null context");
+  ctx->wait_limit = polls;
   return UOCR_OK;
 }
 
@@ -1006,8 +1035,10 @@ int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t 
   hipStream_t st = static_cast<hipStream_t>(stream);
   int* err = device_status ? reinterpret_cast<int*>(device_status) : reinterpret_cast<int*>(base);
   // A fill kernel, not a memset, so that graph capture records a kernel node.
-  hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(1), 0, st, err);
-  const Exec ex{base + kStaticFlagBytes, have, st, err, nullptr};
+  int* sync = reinterpret_cast<int*>(base + kSyncOffset);
+  hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(256), 0, st, err, sync);
+  Exec ex{base + kStaticFlagBytes, have, st, err, nullptr};
+  ex.sync = sync;
   return enqueue_experts(ex, layer, x, T, nullptr, y, flags, nullptr, false);
 }
 

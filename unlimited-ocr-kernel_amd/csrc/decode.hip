@@ -1,17 +1,45 @@
 // One-token (decode) expert engine: bound by the bytes of the active
-// experts' weights. Two launches, and no cross-workgroup synchronisation
-// inside a launch (the kernel boundary orders them):
-//   gate/up  shared-expert workgroups stream their gate/up rows at once;
-//            routed workgroups first compute all E router logits
-//            themselves (the router is 160 KiB, read from L2 by every
-//            routed workgroup, instead of a launch of its own and a
-//            dependent read of its output), route the token in LDS, and
-//            stream the gate/up rows of the expert of their slot
-//   down     routed down of all K experts and the shared-expert down for an
-//            8-feature block, then the ordered combine of that block.
+// experts' weights and by the latency of the steps that depend on each
+// other (router logits -> selection -> expert rows; hidden values -> down).
+// One launch, four kinds of workgroup by id:
+//   logit     ceil(E/8) workgroups, one wave each: 8 router logits
+//   shared    S/32 workgroups: shared-expert gate/up (no routing needed)
+//   routed    K (I/32) workgroups: all E router logits (from L2: the
+//             router is 160 KiB), select, gate/up of the expert of their
+//             slot (routing in the workgroup is ~2 us sooner than waiting
+//             for the logit workgroups)
+//   down      H/8 workgroups: wait for the logits, select, issue the down
+//             rows of every selected expert, wait for every gate/up wave,
+//             then the routed and shared down of 8 output features and
+//             their ordered combine.
+// Workgroups wait only on workgroups with smaller ids (logit < gate/up <
+// down). The dispatcher starts a launch's workgroups in id order, so every
+// workgroup waited on has started, and none of those waits itself on a
+// later one; every wait is also bounded (kSpinLimit polls) and raises
+// Resource when the bound is hit, so a launch always ends.
+//
+// Cross-workgroup words (Scratch::sync, kDecodeSyncBytes, zero before the
+// launch; 64-byte lines): a count of logit workgroups done, 16 sub-counts
+// of gate/up workgroups done (gate/up workgroup b counts in sub-count b %
+// 16), one flag line per workgroup waiting for the logits and one line of
+// 16 flags per down workgroup (flag i: sub-set i of the gate/up
+// workgroups is done). The data that crosses workgroups (the logits, the
+// hidden rows) is written and read only with device-coherent accesses
+// (sc1: agent-scope relaxed atomic stores and loads, sc1 buffer loads),
+// which neither leave it in nor read it from a cache that another XCD's
+// writes bypass. A producer waits for its stores to complete (vmcnt 0)
+// before it counts itself; the workgroup whose count completes a set sets
+// the flag of every workgroup waiting for that set and zeroes the count;
+// a waiting workgroup polls its own line, zeroes it, then reads the data.
+// So every word is zero again when the launch ends. Why this shape: an
+// agent-scope release / acquire fence per wave (an L2 write-back or
+// invalidate each) made a call take 160 us instead of 17, and hundreds of
+// waves counting into and polling one word took 80 us (accesses to one
+// line serialise where the XCDs meet); now every poll has a line of its
+// own and at most 14 workgroups count into one word.
+//
 // Weights are read with range-checked buffer loads (out-of-range chunks
-// read as zero without a memory access), all issued before the first use,
-// and before the activation row is staged into LDS.
+// read as zero without a memory access), all issued before the first use.
 //
 // Arithmetic is that of Decoder::projection / feed_forward for one row
 // (src/decoder/mod.rs:99-122): BF16 widened exactly; INT8 weight-only as
@@ -32,17 +60,20 @@ namespace {
 constexpr int kWide = 2048;     // widest reduction dimension (H, S)
 constexpr int kNarrow = 1024;   // widest routed intermediate size (I)
 constexpr int kMaxK = 8;        // most routed experts per token
+constexpr int kUpWaves = 8;                 // waves of a gate/up workgroup
+constexpr int kHidPerWg = kUpWaves * 4;     // hidden values per gate/up workgroup
+constexpr int kLogitsPerWg = 8;             // router rows per logit workgroup
+// Polls of a wait (each followed by a short sleep, ~0.1 us) before it gives
+// up and raises Resource: far beyond any launch's own duration.
+constexpr int kSpinLimit = 1 << 20;
+constexpr int kLine = 16;         // sync words per 64-byte line
+constexpr int kSubCounts = 16;    // gate/up sub-counts
+constexpr int kErrResource = 6;  // uocr_status Resource
 
 // Row of w13 holding gate value k (up value k is 32 rows further).
 __device__ __forceinline__ int gate_row(int k) { return (k >> 5) * 64 + (k & 31); }
 
 __device__ __forceinline__ int clamp_group(int g, int n) { return g < 0 ? 0 : (g >= n ? n - 1 : g); }
-
-struct RowSmem {
-  float xl[kWide];
-  int8_t xq[kWide];
-  float xs[kWide / kQBlock];
-};
 
 template <int KIND>
 __device__ __forceinline__ const void* w13_of(const DeviceLayer& L, int g) {
@@ -63,9 +94,6 @@ __device__ __forceinline__ const void* w2_of(const DeviceLayer& L, int g) {
                        : (const void*)(L.q2 + L.w2_offset(g));
 }
 
-constexpr int kUpWaves = 8;                     // waves per gate/up workgroup
-constexpr int kHidPerWg = kUpWaves * 4;         // hidden values per gate/up workgroup
-
 struct GateUpSmem {
   float xl[kWide];
   int8_t xq[kWide];
@@ -73,6 +101,140 @@ struct GateUpSmem {
   float logits[64];
   unsigned long long mask;
 };
+
+struct DownSmem {
+  float hl[kMaxK + 2][kNarrow];
+  int8_t hq[kMaxK + 2][kNarrow];
+  float hs[kMaxK + 2][kNarrow / kQBlock];
+  float yl[kMaxK + 2][8];
+  float pw[kMaxK];
+  unsigned long long mask;
+};
+
+union DecodeSmem {
+  GateUpSmem up;
+  DownSmem down;
+};
+
+// Device-coherent store and load of one value that another workgroup reads.
+__device__ __forceinline__ void shared_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float shared_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kCoherent = 16;  // buffer-load cache policy: sc1 (device coherent)
+
+__device__ __forceinline__ void sync_store(int* w, int v) {
+  __hip_atomic_store(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int sync_add(int* w) {
+  return __hip_atomic_fetch_add(w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup counts: ceil(E/8) logit, S/32 shared and K I/32 routed gate/up,
+// H/8 down.
+struct DecodeGrid {
+  int n_logit, n_shared, n_routed, n_down;
+  __host__ __device__ DecodeGrid(const DeviceLayer& L)
+      : n_logit((L.E + kLogitsPerWg - 1) / kLogitsPerWg),
+        n_shared(L.S / kHidPerWg),
+        n_routed(L.K * (L.I / kHidPerWg)),
+        n_down(L.H / 8) {}
+  __host__ __device__ int blocks() const { return n_logit + n_shared + n_routed + n_down; }
+  __host__ __device__ int n_up() const { return n_shared + n_routed; }
+};
+
+// The sync words: line 0 the logit count, lines 1..16 the gate/up
+// sub-counts, then one flag line per down workgroup for the logits and one
+// line of sub-set flags per down workgroup.
+struct SyncMap {
+  int* logit_count;
+  int* sub;
+  int* route_flag;
+  int* down_flags;
+  __device__ SyncMap(int* w, const DecodeGrid& G)
+      : logit_count(w),
+        sub(w + kLine),
+        route_flag(w + (1 + kSubCounts) * kLine),
+        down_flags(w + (1 + kSubCounts + G.n_down) * kLine) {}
+};
+
+// A waiting workgroup's wave: polls its own flag, then zeroes it for the
+// next launch; the wave's later memory accesses stay behind the poll.
+// Gives up after kSpinLimit polls (Resource raised; the caller's results
+// are then not valid, and the forward reports the error).
+__device__ __forceinline__ int wait_bound(const Scratch& S) {
+  return S.wait_limit >= 0 ? S.wait_limit : kSpinLimit;
+}
+__device__ __forceinline__ void wait_flag(int* flag, const Scratch& S) {
+  int* err = S.err;
+  const int bound = wait_bound(S);
+  for (int n = 0;; n++) {
+    const int v = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (v) break;
+    if (n >= bound) {
+      if ((threadIdx.x & 63) == 0) raise_error(err, kErrResource);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(4);
+  }
+  if ((threadIdx.x & 63) == 0) sync_store(flag, 0);
+  asm volatile("" ::: "memory");
+}
+
+// Sets flags[0 .. n) (stride kLine) with the 64 lanes of one wave.
+__device__ __forceinline__ void set_flags(int* flags, int n, int lane) {
+  for (int j = lane; j < n; j += 64) sync_store(flags + j * kLine, 1);
+}
+
+// The token's selection from the E logits the logit workgroups published
+// (one wave, after its flag).
+__device__ __forceinline__ WaveSel select_token(const DeviceLayer& L, const Scratch& S, int* flag,
+                                                int lane) {
+  wait_flag(flag, S);
+  const float v = lane < L.E ? shared_load(S.logits + lane) : 0.0f;
+  return route_wave_sel(v, L.E, L.K);
+}
+
+// End of a gate/up workgroup (every wave calls it once its hidden values
+// are stored): counts the workgroup in sub-count b % 16; the one completing
+// its sub-set sets that sub-set's flag in every down workgroup's line and
+// zeroes the sub-count.
+__device__ __forceinline__ void count_gateup(const SyncMap& M, const DecodeGrid& G, int b, int wave,
+                                             int lane) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
+  __syncthreads();
+  if (wave != 0) return;
+  const int i = b % kSubCounts;
+  int last = 0;
+  if (lane == 0) last = sync_add(M.sub + i * kLine) == (G.n_up() - 1 - i) / kSubCounts;
+  if (__builtin_amdgcn_readfirstlane(last)) {
+    for (int j = lane; j < G.n_down; j += 64) sync_store(M.down_flags + j * kLine + i, 1);
+    if (lane == 0) sync_store(M.sub + i * kLine, 0);
+  }
+}
+
+// A down workgroup's wave 0: polls its line until the flags of all n
+// gate/up sub-sets are set, then zeroes them (bounded like wait_flag).
+__device__ __forceinline__ void wait_line(int* line, int n, const Scratch& S) {
+  int* err = S.err;
+  const int bound = wait_bound(S);
+  const int lane = threadIdx.x & 63;
+  const unsigned long long want = (1ull << n) - 1ull;
+  for (int it = 0;; it++) {
+    const int v = lane < n ? __hip_atomic_load(line + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    if ((__ballot(v != 0) & want) == want) break;
+    if (it >= bound) {
+      if (lane == 0) raise_error(err, kErrResource);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(4);
+  }
+  if (lane < n) sync_store(line + lane, 0);
+  asm volatile("" ::: "memory");
+}
 
 // Stages the activation row (wave 0) into LDS, quantised per 32-block for
 // W8A8; the caller's loads stay in flight meanwhile.
@@ -91,21 +253,48 @@ __device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, 
   }
 }
 
-// Gate/up. Workgroups [0, S/32): shared-expert hidden values 32b .. 32b+31
-// (4 per wave: its 4 gate rows and the 4 matching up rows), h =
-// silu(gate) * up into gu[K*I ..]. Workgroups after that: routed slot
-// s = b' / (I/32), hidden values 32 (b' % (I/32)) .., into gu[s * I ..];
-// the first routed workgroup also writes the logits, the routing and the
-// one-token dispatch (ids, weights, offsets, permutation, row tiles).
+// Logit workgroup b: router rows 8b + q and 8b + q + 4 (q = lane / 16; BF16
+// router, FP32 x; rows past E read as zero) dotted with x by one wave.
+template <int KH>
+__device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
+                           const SyncMap& M, const DecodeGrid& G, int b, int lane) {
+  const int q = lane >> 4;
+  const int ra = kLogitsPerWg * b + q, rb = ra + 4;
+  RowPair<kBF16, KH> R;
+  issue_rows(R, L.router, nullptr, L.E, L.H, ra, rb);
+  RowStage<KH> X;
+  load_row(X, S.xn, L.H, lane);
+  store_row(X, sm.xl, L.H, lane);  // read back by this wave only
+  float r0, r1;
+  dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
+  if ((lane & 15) == 0) {
+    if (ra < L.E) shared_store(S.logits + ra, r0);
+    if (rb < L.E) shared_store(S.logits + rb, r1);
+  }
+  // Counted once the logits are stored; the last logit workgroup releases
+  // every workgroup waiting for them.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  int last = 0;
+  if (lane == 0) last = sync_add(M.logit_count) == G.n_logit - 1;
+  if (__builtin_amdgcn_readfirstlane(last)) {
+    set_flags(M.route_flag, G.n_down, lane);
+    if (lane == 0) sync_store(M.logit_count, 0);
+  }
+}
+
+// Gate/up workgroup b. b < S/32: shared-expert hidden values 32b .. 32b+31
+// (4 per wave: its 4 gate rows and the 4 matching up rows), h = silu(gate)
+// * up into gu[K*I ..]. After that: routed slot s = b' / (I/32), hidden
+// values 32 (b' % (I/32)) .., into gu[s * I ..]; the first routed workgroup
+// also writes the routing and the one-token dispatch (ids, weights,
+// offsets, permutation, row tiles). Each wave counts itself done once its
+// hidden values are stored.
 template <int KIND, int KH>
-__global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLayer L, Scratch S) {
-  __shared__ __align__(16) GateUpSmem sm;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+__device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
+                            const SyncMap& M, const DecodeGrid& G, int b, int wave, int lane) {
   const int q = lane >> 4;
   const int n_shared = L.S / kHidPerWg;
   const int per_expert = L.I / kHidPerWg;
-  const int b = blockIdx.x;
   if (b < n_shared) {
     const int k = b * kHidPerWg + 4 * wave + q;
     const int ra = gate_row(k);
@@ -121,17 +310,23 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
     }
     float r0, r1;
     dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
-    if ((lane & 15) == 0) S.gu[(size_t)L.K * L.I + k] = silu(r0) * r1;
+    if ((lane & 15) == 0) shared_store(S.gu + (size_t)L.K * L.I + k, silu(r0) * r1);
+    count_gateup(M, G, b, wave, lane);
     return;
   }
   const int rb = b - n_shared;
   const int slot = rb / per_expert;
   // Router rows 8 wave + q and 8 wave + q + 4 (BF16 router, FP32 x; rows
-  // past E read as zero), then the logits into LDS.
+  // past E read as zero), the logits into LDS; x is issued first, so it is
+  // staged while the router rows are still in flight. Same rows and the
+  // same dot as the logit workgroups: the same logits, bit for bit.
   {
+    RowStage<KH> X;
+    if (wave == 0) load_row(X, S.xn, L.H, lane);
     RowPair<kBF16, KH> R;
     issue_rows(R, L.router, nullptr, L.E, L.H, 8 * wave + q, 8 * wave + q + 4);
-    stage_x<KIND, KH>(L, S, sm, wave, lane);
+    if (wave == 0) store_row(X, sm.xl, L.H, lane);
+    __syncthreads();
     float r0, r1;
     dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
     if ((lane & 15) == 0) {
@@ -139,9 +334,12 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
       sm.logits[8 * wave + q + 4] = r1;
     }
   }
+  if constexpr (KIND == kW8A8) {
+    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
+  }
   __syncthreads();
-  // Wave 0 routes the token and publishes the selection; the first routed
-  // workgroup's wave 0 also writes the logits, the routing and the
+  // Wave 0 selects the token's experts and publishes the selection; the
+  // first routed workgroup's wave 0 also writes the routing and the
   // one-token dispatch (ids, weights, offsets, permutation, row tiles).
   if (wave == 0) {
     const WaveSel r = route_wave_sel(sm.logits[lane], L.E, L.K);
@@ -160,10 +358,7 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
         S.tiles[2 * asc] = lane;
         S.tiles[2 * asc + 1] = 0;
       }
-      if (lane < L.E) {
-        S.offsets[lane] = asc;
-        S.logits[lane] = sm.logits[lane];
-      }
+      if (lane < L.E) S.offsets[lane] = asc;
       if (lane == 0) {
         S.offsets[L.E] = L.K;
         S.tiles[2 * L.K] = L.E;
@@ -191,53 +386,54 @@ __global__ __launch_bounds__(64 * kUpWaves) void decode_gateup_kernel(DeviceLaye
   }
   float r0, r1;
   dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
-  if ((lane & 15) == 0) S.gu[(size_t)slot * L.I + k] = silu(r0) * r1;
+  if ((lane & 15) == 0) shared_store(S.gu + (size_t)slot * L.I + k, silu(r0) * r1);
+  count_gateup(M, G, b, wave, lane);
 }
 
-struct DownSmem {
-  float hl[kMaxK + 2][kNarrow];
-  int8_t hq[kMaxK + 2][kNarrow];
-  float hs[kMaxK + 2][kNarrow / kQBlock];
-  float yl[kMaxK + 2][8];
-};
-
-// Down: one workgroup per 8 output features; wave w < K = routed expert in
-// ascending slot w, waves K and K+1 = the two halves of the shared expert's
-// reduction (S/2 columns each); then the ordered combine of the 8 features:
-// out = (residual +) ((y_s0 + y_s1) + p_0 y_0 + p_1 y_1 + ...), mul then add.
+// Down workgroup b: output features 8b .. 8b+7; wave w < K = the selected
+// expert of ascending slot w, waves K and K+1 = the two halves of the
+// shared expert's reduction (S/2 columns each); then the ordered combine
+// of the 8 features: out = (residual +) ((y_s0 + y_s1) + p_0 y_0 + p_1 y_1
+// + ...), mul then add.
 template <int KIND>
-__global__ __launch_bounds__(64 * (kMaxK + 2)) void decode_down_kernel(DeviceLayer L, Scratch S,
-                                                                       const float* residual,
-                                                                       float* out) {
-  __shared__ __align__(16) DownSmem sm;
-  // Wave-uniform (scalar) so the per-wave buffer bases stay scalar.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+__device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, const SyncMap& M,
+                          const DecodeGrid& G, int b, const float* residual, float* out, int wave,
+                          int lane) {
   const int q = lane >> 4;
-  const int f0 = 8 * blockIdx.x;
+  const int f0 = 8 * b;
   const bool routed = wave < L.K;
   const int half = L.S / 2;
   // This wave's hidden row: an expert's I values, or half the shared S.
   const int n = routed ? L.I : half;
+  // The shared expert's rows need no routing: issued first.
+  RowPair<KIND, kNarrow> P;
+  if (!routed)
+    issue_rows_cols(P, w2_of<KIND>(L, L.E), s2_of<KIND>(L, L.E), L.H, L.S, (wave - L.K) * half, n,
+                    f0 + q, f0 + q + 4);
+  // Wave 0 selects; every routed wave needs its slot's expert, the combine
+  // the routing weights in ascending slot order.
+  if (wave == 0) {
+    const WaveSel r = select_token(L, S, M.route_flag + b * kLine, lane);
+    const float w = route_weight(r, L.normalize, L.scale);
+    const int asc = __popcll(r.mask & ((1ull << lane) - 1ull));
+    if ((r.mask >> lane) & 1ull) sm.pw[asc] = w;
+    if (lane == 0) sm.mask = r.mask;
+  }
+  __syncthreads();
+  const int g =
+      routed ? clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, wave)), L.E) : L.E;
+  if (routed) issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, 0, n, f0 + q, f0 + q + 4);
+  const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
+  // The hidden rows are whole once every gate/up workgroup has counted
+  // itself (wave 0 waits for this workgroup's flag).
+  if (wave == 0) wait_line(M.down_flags + b * kLine, G.n_up() < kSubCounts ? G.n_up() : kSubCounts, S);
+  __syncthreads();
   const float* hrow = routed ? S.gu + (size_t)wave * L.I
                              : S.gu + (size_t)L.K * L.I + (size_t)(wave - L.K) * half;
   RowStage<kNarrow> Hr;
-  load_row(Hr, hrow, n, lane);
-  const int g = routed ? clamp_group(__builtin_amdgcn_readfirstlane(S.tiles[2 * wave]), L.E) : L.E;
-  RowPair<KIND, kNarrow> P;
-  issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.width(g),
-                  routed ? 0 : (wave - L.K) * half, n, f0 + q, f0 + q + 4);
-  // The combine inputs are loaded now and used last.
-  float pw[kMaxK];
-#pragma unroll
-  for (int j = 0; j < kMaxK; j++) pw[j] = j < L.K ? S.perm_w[j] : 0.0f;
-  const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
-  store_row(Hr, sm.hl[wave], n, lane);
-  __syncthreads();
-  if constexpr (KIND == kW8A8) {
-    quantize_lds(sm.hl[wave], n, sm.hq[wave], sm.hs[wave], lane, S.err);
-    __syncthreads();
-  }
+  load_row<kNarrow, kCoherent>(Hr, hrow, n, lane);
+  store_row(Hr, sm.hl[wave], n, lane);  // each wave reads back its own row only
+  if constexpr (KIND == kW8A8) quantize_lds(sm.hl[wave], n, sm.hq[wave], sm.hs[wave], lane, S.err);
   BlockSumOut bs;
   if (KIND == kW8A8 && (routed ? S.q8.down : S.q8.s_down)) {
     const int nb = L.width(g) / kQBlock;
@@ -258,51 +454,80 @@ __global__ __launch_bounds__(64 * (kMaxK + 2)) void decode_down_kernel(DeviceLay
     float acc = sm.yl[L.K][lane] + sm.yl[L.K + 1][lane];
 #pragma unroll
     for (int j = 0; j < kMaxK; j++)
-      if (j < L.K) acc = acc + pw[j] * sm.yl[j][lane];
+      if (j < L.K) acc = acc + sm.pw[j] * sm.yl[j][lane];
     if (residual) acc = res_f + acc;
     out[f0 + lane] = acc;
   }
 }
 
+constexpr int kBlockWaves = kUpWaves > kMaxK + 2 ? kUpWaves : kMaxK + 2;
+
 template <int KIND, int KH>
-void launch_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
-                  float* out, hipStream_t s) {
-  if (stage == 1)
-    decode_gateup_kernel<KIND, KH>
-        <<<dim3(L.S / kHidPerWg + L.K * (L.I / kHidPerWg)), dim3(64 * kUpWaves), 0, s>>>(L, S);
-  else
-    decode_down_kernel<KIND><<<dim3(L.H / 8), dim3(64 * (L.K + 2)), 0, s>>>(L, S, residual, out);
+__global__ __launch_bounds__(64 * kBlockWaves) void decode_kernel(DeviceLayer L, Scratch S,
+                                                                  const float* residual, float* out) {
+  __shared__ __align__(16) DecodeSmem sm;
+  // Wave-uniform (scalar) so the per-wave buffer bases stay scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const DecodeGrid G(L);
+  const SyncMap M(S.sync, G);
+  int b = blockIdx.x;
+  if (b < G.n_logit) {
+    if (wave == 0) logit_role<KH>(L, S, sm.up, M, G, b, lane);
+    return;
+  }
+  b -= G.n_logit;
+  if (b < G.n_up()) {
+    if (wave < kUpWaves) gateup_role<KIND, KH>(L, S, sm.up, M, G, b, wave, lane);
+    return;
+  }
+  b -= G.n_up();
+  if (wave < L.K + 2) down_role<KIND>(L, S, sm.down, M, G, b, residual, out, wave, lane);
+}
+
+template <int KIND, int KH>
+void launch_kind(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                 hipStream_t s) {
+  const DecodeGrid G(L);
+  const int waves = L.K + 2 > kUpWaves ? L.K + 2 : kUpWaves;
+  decode_kernel<KIND, KH><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
 }
 
 template <int KH>
-void launch_kind(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
-                 float* out, hipStream_t s) {
+void launch_width(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                  hipStream_t s) {
   if (L.quant_mode == 0)
-    launch_stage<kBF16, KH>(stage, L, S, residual, out, s);
+    launch_kind<kBF16, KH>(L, S, residual, out, s);
   else if (L.quant_mode == 1)
-    launch_stage<kInt8, KH>(stage, L, S, residual, out, s);
+    launch_kind<kInt8, KH>(L, S, residual, out, s);
   else
-    launch_stage<kW8A8, KH>(stage, L, S, residual, out, s);
+    launch_kind<kW8A8, KH>(L, S, residual, out, s);
 }
 
 }  // namespace
 
 bool decode_supported(const DeviceLayer& L) {
   // Gate/up rows reduce over H (<= 2048), 32 hidden values per workgroup;
-  // the down launch reduces over I (<= 1024, one wave per routed expert) and
-  // the two halves of S (<= 2048, each a whole number of 32-blocks);
+  // the down workgroups reduce over I (<= 1024, one wave per routed expert)
+  // and the two halves of S (<= 2048, each a whole number of 32-blocks);
   // routing is one wave over E <= 64 logits.
+  // The sync words: 1 + 16 counter lines and a flag line per waiting
+  // workgroup (K I/32 + 2 H/8 <= 768) fit kDecodeSyncBytes.
+  static_assert((1 + kSubCounts + kMaxK * kNarrow / kHidPerWg + 2 * kWide / 8) * kLine * 4 <=
+                    (int)kDecodeSyncBytes,
+                "decode sync words");
+  static_assert(kSubCounts <= kLine, "a down workgroup's sub-set flags share one line");
   return L.H <= kWide && L.S <= kWide && L.I <= kNarrow && L.K >= 1 && L.K <= kMaxK &&
          L.E <= 64 && L.H % 8 == 0 && L.I % kHidPerWg == 0 && L.S % kHidPerWg == 0 &&
          L.S % 64 == 0;
 }
 
-void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
-                         float* out, hipStream_t s) {
+void launch_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                   hipStream_t s) {
   if (L.H <= 1280)
-    launch_kind<1280>(stage, L, S, residual, out, s);
+    launch_width<1280>(L, S, residual, out, s);
   else
-    launch_kind<kWide>(stage, L, S, residual, out, s);
+    launch_width<kWide>(L, S, residual, out, s);
 }
 
 }  // namespace uocr

@@ -86,6 +86,8 @@ struct Scratch {
   int8_t* q8x;      // int8 mode: quantised input [T, H] and hidden rows [T*K*I + T*S]
   float* q8s;       // int8 mode: their block scales [T*H/32 + (T*K*I + T*S)/32]
   int* err;         // device error flag
+  int* sync;        // kDecodeSyncBytes: the decode engine's counts and flags (zero between launches)
+  int wait_limit;   // the decode engine's wait bound in polls (< 0: its default)
   Q8Trace q8;       // W8A8 trace (tests), all null by default
 };
 
@@ -186,13 +188,14 @@ void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, i
                     int tiles_bound, hipStream_t s);
 constexpr int kGemvChunk = 16;
 
-// decode.hip: one-token expert engine, two launches (stage 1: gate/up of
-// the shared expert and, after routing in every routed workgroup, of the
-// routed experts; stage 2: routed and shared down + ordered combine into
-// out).
+// decode.hip: one-token expert engine, one launch (router logits, the
+// shared and the routed gate/up, routed and shared down + ordered combine
+// into out), ordered inside by the kDecodeSyncBytes at S.sync, which must
+// be zero when it starts and are zero again when it ends.
+constexpr size_t kDecodeSyncBytes = 64 << 10;
 bool decode_supported(const DeviceLayer& L);
-void launch_decode_stage(int stage, const DeviceLayer& L, const Scratch& S, const float* residual,
-                         float* out, hipStream_t s);
+void launch_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                   hipStream_t s);
 
 // combine.hip
 // RMSNorm output of rows: the normalised rows (out, [T, H]) and optionally

@@ -220,20 +220,20 @@ __device__ __forceinline__ void dot_rows(const RowPair<KIND, KMAX>& P, int K, co
 }
 
 // An FP32 row of n <= N values (n % 4 == 0) held in registers of one wave
-// (float4 at lane, lane + 64, ...): load_row issues every load, store_row
-// writes the row into LDS.
+// (float4 at lane, lane + 64, ...): load_row issues every load (with buffer
+// cache policy AUX), store_row writes the row into LDS.
 template <int N>
 struct RowStage {
   static constexpr int kV = N / 4 / 64;
   u32x4 v[kV];
 };
-template <int N>
+template <int N, int AUX = 0>
 __device__ __forceinline__ void load_row(RowStage<N>& R, const float* src, int n, int lane) {
   const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)n * 4u);
 #pragma unroll
   for (int i = 0; i < RowStage<N>::kV; i++) {
     const int at = lane + 64 * i;
-    R.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, at * 4 < n ? (uint32_t)at * 16u : kOut, 0, 0);
+    R.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, at * 4 < n ? (uint32_t)at * 16u : kOut, 0, AUX);
   }
 }
 template <int N>

@@ -33,14 +33,14 @@ FLAG_BF16_ACTIVATIONS = 1
 FLAG_FORCE_GEMV = 2
 FLAG_FORCE_MFMA = 4
 FLAG_INT8_MFMA = 8
-PHASES = ["router", "topk", "dispatch", "split", "gateup", "down", "combine", "norm"]
+PHASES = ["router", "topk", "dispatch", "split", "gateup", "down", "combine", "norm", "decode"]
 
 # Every symbol include/uocr_moe.h declares.
 EXPORTS = [
     "uocr_gpu_ctx_create", "uocr_gpu_ctx_destroy", "uocr_gpu_ctx_stream",
     "uocr_gpu_ctx_synchronize", "uocr_last_error", "uocr_moe_scratch_bytes",
     "uocr_moe_max_tokens",
-    "uocr_gpu_ctx_set_timing", "uocr_gpu_ctx_timings",
+    "uocr_gpu_ctx_set_timing", "uocr_gpu_ctx_timings", "uocr_gpu_ctx_set_wait_limit",
     "uocr_moe_layer_create", "uocr_moe_layer_attach_int8", "uocr_moe_layer_precision",
     "uocr_moe_layer_device_bytes", "uocr_moe_layer_destroy", "uocr_moe_forward_async",
     "uocr_moe_forward", "uocr_moe_forward_static", "uocr_moe_block_forward",
@@ -136,6 +136,7 @@ def _load():
         "uocr_moe_scratch_bytes": (_SZ, [ctypes.POINTER(MoeConfig), _SZ]),
         "uocr_moe_max_tokens": (_SZ, [ctypes.POINTER(MoeConfig)]),
         "uocr_gpu_ctx_set_timing": (ctypes.c_int, [_P, _U32]),
+        "uocr_gpu_ctx_set_wait_limit": (ctypes.c_int, [_P, ctypes.c_int]),
         "uocr_gpu_ctx_timings": (ctypes.c_int, [_P, ctypes.POINTER(PhaseTime), _SZ,
                                                 ctypes.POINTER(_SZ)]),
         "uocr_moe_layer_create": (ctypes.c_int, [_P, ctypes.POINTER(MoeConfig),
@@ -242,6 +243,11 @@ class Context:
                 mask |= 1 << PHASES.index(p)
         _check(lib.uocr_gpu_ctx_set_timing(self.handle, mask))
 
+    def set_wait_limit(self, polls: int):
+        """Bound of the one-token engine's cross-workgroup waits (diagnostic:
+        0 drives the Resource error path; < 0 restores the default)."""
+        _check(lib.uocr_gpu_ctx_set_wait_limit(self.handle, polls))
+
     def timings(self) -> dict:
         """{phase: (launches, total_ms)} since the last read; resets them."""
         arr = (PhaseTime * 16)()
@@ -335,6 +341,7 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
 
 
 STATIC_SCRATCH_BYTES = 16 << 20
+STATIC_RESERVED_BYTES = 256 + (64 << 10)  # the device flag and the decode engine's words
 
 
 def forward_static(layer: MoeLayer, x, y, flags: int = 0, status=None, stream=None):
