@@ -249,7 +249,7 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * the device flag and the one-token engine's synchronisation words;
  * forwards whose uocr_moe_scratch_bytes exceeds UOCR_STATIC_SCRATCH_BYTES -
  * UOCR_STATIC_RESERVED_BYTES fail with Resource (at the model shape: up to
- * 117 tokens). Every call on one GPU shares that GPU's
+ * 115 tokens). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU race, so serialise them (one
  * stream, or events). Enqueued on `stream` (a hipStream_t; NULL: the null
  * stream) and returns once queued. Device-side errors (non-finite

@@ -167,7 +167,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
-      h, hs, y, ys, xn, xb, gu, q8x, q8s, total;
+      h, hs, y, ys, xn, xb, gu, q8x, q8s, router_part, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -203,6 +203,8 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   const size_t q8_elems = T * H + T * K * I + T * S;
   p.q8x = take(q8_elems);
   p.q8s = take(q8_elems / 32 * 4);
+  // The router's partial logits when it splits H (few tokens).
+  p.router_part = take(uocr::router_part_bytes((int)T, (int)H));
   p.total = at;
   return p;
 }
@@ -258,6 +260,7 @@ Scratch carve(const Exec& ex, const ScratchPlan& p) {
   s.gu = reinterpret_cast<float*>(b + p.gu);
   s.q8x = reinterpret_cast<int8_t*>(b + p.q8x);
   s.q8s = reinterpret_cast<float*>(b + p.q8s);
+  s.router_part = reinterpret_cast<float*>(b + p.router_part);
   s.err = ex.err;
   s.sync = ex.sync;
   s.wait_limit = ex.wait_limit;
@@ -509,7 +512,8 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       uocr::launch_router_topk_mfma(S.xn, L.router, Ti, L.H, L.E, L.K, L.normalize, L.scale,
                                     S.logits, S.topk_ids, S.topk_w, S.chunk_counts,
                                     router_planes ? P.x_hi : nullptr,
-                                    router_planes && !bf16_only ? P.x_lo : nullptr, S.err, st);
+                                    router_planes && !bf16_only ? P.x_lo : nullptr, S.err,
+                                    S.router_part, st);
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
       uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, narrow, S.chunk_counts,

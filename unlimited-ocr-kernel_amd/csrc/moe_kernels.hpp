@@ -84,6 +84,7 @@ struct Scratch {
   uint16_t* xb;     // [2][H/32][T][32] bf16 planes (hi, lo) of the layer input (MFMA engine)
   float* gu;        // one token: hidden rows, routed [K, I] (ascending slot) then shared [S]
   int8_t* q8x;      // int8 mode: quantised input [T, H] and hidden rows [T*K*I + T*S]
+  float* router_part;  // router_part_bytes(T, H): the split router's partial logits
   float* q8s;       // int8 mode: their block scales [T*H/32 + (T*K*I + T*S)/32]
   int* err;         // device error flag
   int* sync;        // kDecodeSyncBytes: the decode engine's counts and flags (zero between launches)
@@ -103,10 +104,26 @@ void launch_topk(const float* logits, int T, int E, int K, int normalize, float 
 inline bool router_mfma_supported(int H) { return H % 32 == 0 && H <= 2048; }
 // x_hi (and x_lo) set: also writes the bf16 hi (and lo) planes of x that
 // the MFMA grouped GEMM reads ([H/32][T][32]), as launch_split_planes would.
+// part set: few tokens split H over router_ksplit(T, H) workgroups per
+// 16-token chunk (partial logits in part, router_part_bytes of them), then
+// a second launch adds them in order and routes.
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
-                             hipStream_t s);
+                             float* part, hipStream_t s);
+// Workgroups per 16-token chunk of the router: enough for ~256 workgroups
+// in all, at most 8 and at most one 32-wide step of H per workgroup's wave.
+inline int router_ksplit(int T, int H) {
+  const int chunks = (T + 15) / 16, steps = H / 32;
+  int k = 256 / (chunks > 0 ? chunks : 1);
+  k = k > 8 ? 8 : k;
+  k = k > steps ? steps : k;
+  return k < 2 ? 1 : k;
+}
+inline size_t router_part_bytes(int T, int H) {
+  const int k = router_ksplit(T, H);
+  return k > 1 ? (size_t)((T + 15) / 16) * k * 16 * 64 * 4 : 0;
+}
 
 // dispatch.hip
 // narrow > 0 moves each expert's last tile of at most `narrow` rows into a

@@ -164,14 +164,49 @@ constexpr int kRouteChunk = 16;
 
 constexpr int kRouteWaves = 8;
 
-// KS = K steps (32 wide) per wave: wave w takes steps w, w + 8, ...; steps
-// past H / 32 read as zero. All loads of a wave are issued before its MFMAs.
+// Routes tokens t0 .. t0+15 from their logits v(tl, lane) (two tokens per
+// wave): stores logits, ids and weights, and the chunk's per-expert counts.
+template <typename LogitOf>
+__device__ __forceinline__ void route_chunk(LogitOf logit_of, int t0, int T, int E, int K,
+                                            int normalize, float scale, float* __restrict__ logits,
+                                            int* __restrict__ ids, float* __restrict__ weights,
+                                            int* __restrict__ chunk_counts, int* cnt, int* err) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
+    const int tl = wave * (kRouteChunk / kRouteWaves) + j;
+    const int t = t0 + tl;
+    const bool live = t < T;
+    const float v = logit_of(tl, lane);
+    if (live && lane < E) logits[(size_t)t * E + lane] = v;
+    const WaveSel r = route_wave_sel(live ? v : 0.0f, E, K);
+    const float wgt = route_weight(r, normalize, scale);
+    if (!live) continue;
+    if (!r.ok && lane == 0) raise_error(err, kErrNumerical);
+    if ((r.mask >> lane) & 1ull) {
+      ids[(size_t)t * K + r.rank] = lane;
+      weights[(size_t)t * K + r.rank] = wgt;
+      atomicAdd(&cnt[lane], 1);
+    }
+  }
+  __syncthreads();
+  if (tid < 64) chunk_counts[(size_t)blockIdx.x * 64 + tid] = cnt[tid];
+}
+
+// KS = K steps (32 wide) per wave. Unsplit (ksplit = 1): workgroup c owns
+// tokens 16c.. and wave w takes steps w, w + 8, ...; it reduces, routes and
+// counts the chunk. Split (ksplit > 1, few tokens): workgroup c ksplit + p
+// takes steps p, p + ksplit, ... (wave w: p + ksplit (w + 8 i)) and writes
+// its partial logits [16][64] to part_out[c ksplit + p]; router_finish_kernel
+// adds the ksplit partials in order and routes. Steps past H / 32 read as
+// zero. All loads of a wave are issued before its MFMAs.
 template <int KS>
 __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ w, int T, int H, int E, int K,
     int normalize, float scale, float* __restrict__ logits, int* __restrict__ ids,
     float* __restrict__ weights, int* __restrict__ chunk_counts, uint16_t* __restrict__ x_hi,
-    uint16_t* __restrict__ x_lo, int* err) {
+    uint16_t* __restrict__ x_lo, int* err, int ksplit, float* __restrict__ part_out) {
   __shared__ float part[kRouteWaves][kRouteChunk][65];
   __shared__ int cnt[64];
   const int tid = threadIdx.x;
@@ -181,7 +216,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
   // with the shared expert's GEMM, whose waves would otherwise take turns
   // with it on every SIMD.
   __builtin_amdgcn_s_setprio(3);
-  const int t0 = blockIdx.x * kRouteChunk;
+  const int chunk = blockIdx.x / ksplit, p = blockIdx.x % ksplit;
+  const int t0 = chunk * kRouteChunk;
   if (tid < 64) cnt[tid] = 0;
   const int ar = lane & 15;        // fragment row (token) / column (expert)
   const int aq = (lane >> 4) * 8;  // fragment k offset within a 32-wide step
@@ -196,9 +232,10 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
   constexpr uint32_t kFar = 0x80000000u;
   const uint32_t xoff = (uint32_t)ar * H * 4u + aq * 4u;
   u32x4 xa[KS], xb[KS], wv[KS][4];
+  auto step_of = [&](int i) { return p + ksplit * (wave + kRouteWaves * i); };
 #pragma unroll
   for (int i = 0; i < KS; i++) {
-    const int st = wave + kRouteWaves * i;
+    const int st = step_of(i);
     const bool ok = st < steps;
     const uint32_t k0 = (uint32_t)st * 32u;
     xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + k0 * 4u : kFar, 0, 0);
@@ -239,7 +276,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
       lo[j] = (__bf16)(r1 - (float)m);
     }
     if (x_hi) {
-      const int st = wave + kRouteWaves * i;
+      const int st = step_of(i);
       int off = st < steps && ar < nt
                     ? (int)((((uint32_t)st * T + (uint32_t)(t0 + ar)) * 32u + aq) * 2u)
                     : (int)kFar;
@@ -262,43 +299,83 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < 4; r++) part[wave][4 * (lane >> 4) + r][ni * 16 + ar] = acc[ni][r];
   __syncthreads();
-  // Wave partial sums in wave order (deterministic); each wave then routes
-  // two tokens on its own with the wave top-k.
-  for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
-    const int tl = wave * (kRouteChunk / kRouteWaves) + j;
-    const int t = t0 + tl;
-    const bool live = t < T;
-    float v = part[0][tl][lane];
+  // Wave partial sums in wave order (deterministic).
+  auto wave_sum_of = [&](int tl, int e) {
+    float v = part[0][tl][e];
 #pragma unroll
-    for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][lane];
-    if (live && lane < E) logits[(size_t)t * E + lane] = v;
-    const WaveSel r = route_wave_sel(live ? v : 0.0f, E, K);
-    const float wgt = route_weight(r, normalize, scale);
-    if (!live) continue;
-    if (!r.ok && lane == 0) raise_error(err, kErrNumerical);
-    if ((r.mask >> lane) & 1ull) {
-      ids[(size_t)t * K + r.rank] = lane;
-      weights[(size_t)t * K + r.rank] = wgt;
-      atomicAdd(&cnt[lane], 1);
+    for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][e];
+    return v;
+  };
+  if (ksplit > 1) {
+    float* out = part_out + (size_t)blockIdx.x * kRouteChunk * 64;
+    for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
+      const int tl = wave * (kRouteChunk / kRouteWaves) + j;
+      out[tl * 64 + lane] = wave_sum_of(tl, lane);
     }
+    return;
+  }
+  // Each wave routes two tokens on its own with the wave top-k.
+  route_chunk(wave_sum_of, t0, T, E, K, normalize, scale, logits, ids, weights, chunk_counts, cnt,
+              err);
+}
+
+// Split router, second step: workgroup c adds chunk c's ksplit partial
+// logits in order (deterministic) and routes its 16 tokens.
+// Every partial of the thread's two (token, expert) values is loaded
+// before the first add.
+constexpr int kMaxRouteSplit = 8;
+__global__ __launch_bounds__(64 * kRouteWaves) void router_finish_kernel(
+    const float* __restrict__ part_in, int ksplit, int T, int E, int K, int normalize, float scale,
+    float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ weights,
+    int* __restrict__ chunk_counts, int* err) {
+  __shared__ int cnt[64];
+  __shared__ float lg[kRouteChunk][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x < 64) cnt[threadIdx.x] = 0;
+  const float* in = part_in + (size_t)blockIdx.x * ksplit * kRouteChunk * 64;
+  constexpr int kPer = kRouteChunk / kRouteWaves;
+  float v[kPer][kMaxRouteSplit];
+#pragma unroll
+  for (int j = 0; j < kPer; j++)
+#pragma unroll
+    for (int q = 0; q < kMaxRouteSplit; q++)
+      v[j][q] = q < ksplit ? in[((size_t)q * kRouteChunk + wave * kPer + j) * 64 + lane] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    float a = v[j][0];
+#pragma unroll
+    for (int q = 1; q < kMaxRouteSplit; q++)
+      if (q < ksplit) a = a + v[j][q];
+    lg[wave * kPer + j][lane] = a;
   }
   __syncthreads();
-  if (tid < 64) chunk_counts[(size_t)blockIdx.x * 64 + tid] = cnt[tid];
+  auto sum_of = [&](int tl, int e) { return lg[tl][e]; };
+  route_chunk(sum_of, (int)blockIdx.x * kRouteChunk, T, E, K, normalize, scale, logits, ids,
+              weights, chunk_counts, cnt, err);
 }
 
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
-                             hipStream_t s) {
+                             float* part, hipStream_t s) {
   if (T <= 0 || !router_mfma_supported(H)) return;
-  const dim3 grid((T + kRouteChunk - 1) / kRouteChunk), block(64 * kRouteWaves);
-  const int ks = (H / 32 + kRouteWaves - 1) / kRouteWaves;
-  if (ks <= 5)
+  const int chunks = (T + kRouteChunk - 1) / kRouteChunk;
+  const int ksplit = part ? router_ksplit(T, H) : 1;
+  const dim3 grid(chunks * ksplit), block(64 * kRouteWaves);
+  const int steps = H / 32;
+  const int ks = (steps + ksplit * kRouteWaves - 1) / (ksplit * kRouteWaves);
+  if (ks <= 1)
+    router_mfma_kernel<1><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
+  else if (ks <= 5)
     router_mfma_kernel<5><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, x_hi, x_lo, err);
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
   else
     router_mfma_kernel<8><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, x_hi, x_lo, err);
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
+  if (ksplit > 1)
+    router_finish_kernel<<<dim3(chunks), block, 0, s>>>(part, ksplit, T, E, K, normalize, scale,
+                                                        logits, ids, weights, chunk_counts, err);
 }
 
 void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
