@@ -373,6 +373,20 @@ def test_decode_many_tokens(ctx, full_bf16, full_int8, full_dynamic, kind):
     say(f"  {kind}: 32 one-token forwards, worst normwise {worst:.3e}")
 
 
+# The one-token engine at its other limits: the widest hidden row (its
+# 2048-wide instantiation), 8 experts per token (10-wave down workgroups),
+# an expert count that is not a multiple of 8 (a partial logit workgroup).
+DECODE_EDGE = dict(hidden=2048, inter=512, experts=37, shared=2)
+
+
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY, orc.QUANT_DYNAMIC])
+def test_decode_edge_shapes(ctx, quant):
+    case = Case(ctx, DECODE_EDGE, 8, seed=1200 + quant, quant=quant)
+    for i in range(4):
+        say(f"decode edge shape quant={quant} token {i}")
+        check_layer(case, ctx, syn.activations(1, DECODE_EDGE["hidden"], seed=1300 + i))
+
+
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
     """48 one-token forwards queued back to back (one synchronisation at the
