@@ -115,3 +115,37 @@ def test_static_forward_on_a_stream(setup):
     um.forward_static(layer, xd, got, stream=s)
     s.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("T", [1, 24])
+def test_static_forward_graph_replays(setup, T):
+    """The allocation-free forward captured in a HIP graph (the one-token
+    engine's single launch with its self-clearing synchronisation words at
+    T = 1; router, dispatch and the MFMA engine at T = 24) and replayed four
+    times, with eager forwards between the replays: every replay gives the
+    eager forward's bits."""
+    ctx, cfg, layer, qlayer, ow = setup
+    x = syn.activations(T, H, seed=95 + T)
+    xd = torch.from_numpy(x).cuda()
+    want = torch.empty_like(xd)
+    torch.cuda.synchronize()
+    um.forward(ctx, layer, xd, want)
+    s = torch.cuda.Stream()
+    got = torch.full_like(xd, float("nan"))
+    torch.cuda.synchronize()
+    um.forward_static(layer, xd, got, stream=s)  # first call outside the capture
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        um.forward_static(layer, xd, got, stream=s)
+    other = torch.empty_like(xd)
+    for rep in range(4):
+        say(f"graph replay T={T} #{rep}")
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), rep
+        um.forward(ctx, layer, xd, other)
+        torch.cuda.synchronize()
+        assert torch.equal(other, want), rep
