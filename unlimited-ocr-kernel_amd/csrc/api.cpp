@@ -513,7 +513,8 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
                                     S.logits, S.topk_ids, S.topk_w, S.chunk_counts,
                                     router_planes ? P.x_hi : nullptr,
                                     router_planes && !bf16_only ? P.x_lo : nullptr, S.err,
-                                    S.router_part, st);
+                                    S.router_part, S.sync ? S.sync + uocr::kRouterSyncWord : nullptr,
+                                    st);
       phase_end(ctx);
       phase_begin(ctx, kDispatch);
       uocr::launch_dispatch_chunked(S.topk_ids, S.topk_w, Ti, L.E, L.K, bm, narrow, S.chunk_counts,

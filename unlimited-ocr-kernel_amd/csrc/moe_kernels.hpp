@@ -104,13 +104,15 @@ void launch_topk(const float* logits, int T, int E, int K, int normalize, float 
 inline bool router_mfma_supported(int H) { return H % 32 == 0 && H <= 2048; }
 // x_hi (and x_lo) set: also writes the bf16 hi (and lo) planes of x that
 // the MFMA grouped GEMM reads ([H/32][T][32]), as launch_split_planes would.
-// part set: few tokens split H over router_ksplit(T, H) workgroups per
-// 16-token chunk (partial logits in part, router_part_bytes of them), then
-// a second launch adds them in order and routes.
+// part and route_counts set: few tokens split H over router_ksplit(T, H)
+// workgroups per 16-token chunk (partial logits in part, router_part_bytes
+// of them); the chunk's last workgroup adds them in order and routes.
+// route_counts: one word per chunk (stride 16), zero before the launch and
+// zero again after it.
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
-                             float* part, hipStream_t s);
+                             float* part, int* route_counts, hipStream_t s);
 // Workgroups per 16-token chunk of the router: enough for ~256 workgroups
 // in all, at most 8 and at most one 32-wide step of H per workgroup's wave.
 inline int router_ksplit(int T, int H) {
@@ -210,6 +212,12 @@ constexpr int kGemvChunk = 16;
 // into out), ordered inside by the kDecodeSyncBytes at S.sync, which must
 // be zero when it starts and are zero again when it ends.
 constexpr size_t kDecodeSyncBytes = 64 << 10;
+// The split router's per-chunk counts (<= 128 chunks, one word per 64 bytes)
+// live in the same zero-between-launches region, past the decode engine's
+// words (at most 1 + 16 + 2 * 256 lines).
+constexpr size_t kRouterSyncWord = 10240;
+static_assert((kRouterSyncWord + 128 * 16) * 4 <= kDecodeSyncBytes, "router counts fit");
+static_assert((1 + 16 + 2 * 256) * 16 <= kRouterSyncWord, "after the decode words");
 bool decode_supported(const DeviceLayer& L);
 void launch_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
                    hipStream_t s);

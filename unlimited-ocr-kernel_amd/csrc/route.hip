@@ -161,16 +161,18 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // (deterministic). It also emits the chunk's per-expert assignment counts
 // for the dispatch scan.
 constexpr int kRouteChunk = 16;
+constexpr int kMaxRouteSplit = 8;  // most workgroups per chunk (router_ksplit)
 
 constexpr int kRouteWaves = 8;
 
 // Routes tokens t0 .. t0+15 from their logits v(tl, lane) (two tokens per
 // wave): stores logits, ids and weights, and the chunk's per-expert counts.
 template <typename LogitOf>
-__device__ __forceinline__ void route_chunk(LogitOf logit_of, int t0, int T, int E, int K,
+__device__ __forceinline__ void route_chunk(LogitOf logit_of, int chunk, int T, int E, int K,
                                             int normalize, float scale, float* __restrict__ logits,
                                             int* __restrict__ ids, float* __restrict__ weights,
                                             int* __restrict__ chunk_counts, int* cnt, int* err) {
+  const int t0 = chunk * kRouteChunk;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -191,24 +193,29 @@ __device__ __forceinline__ void route_chunk(LogitOf logit_of, int t0, int T, int
     }
   }
   __syncthreads();
-  if (tid < 64) chunk_counts[(size_t)blockIdx.x * 64 + tid] = cnt[tid];
+  if (tid < 64) chunk_counts[(size_t)chunk * 64 + tid] = cnt[tid];
 }
 
 // KS = K steps (32 wide) per wave. Unsplit (ksplit = 1): workgroup c owns
 // tokens 16c.. and wave w takes steps w, w + 8, ...; it reduces, routes and
 // counts the chunk. Split (ksplit > 1, few tokens): workgroup c ksplit + p
 // takes steps p, p + ksplit, ... (wave w: p + ksplit (w + 8 i)) and writes
-// its partial logits [16][64] to part_out[c ksplit + p]; router_finish_kernel
-// adds the ksplit partials in order and routes. Steps past H / 32 read as
-// zero. All loads of a wave are issued before its MFMAs.
+// its partial logits [16][64] to part_out[c ksplit + p] with device-coherent
+// stores; once they are complete it counts itself in route_counts[16 c], and
+// the chunk's last workgroup (the one that sees ksplit - 1) zeroes that word,
+// adds the ksplit partials in order (device-coherent loads) and routes the
+// chunk. No workgroup waits for another. Steps past H / 32 read as zero. All
+// loads of a wave are issued before its MFMAs.
 template <int KS>
 __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ w, int T, int H, int E, int K,
     int normalize, float scale, float* __restrict__ logits, int* __restrict__ ids,
     float* __restrict__ weights, int* __restrict__ chunk_counts, uint16_t* __restrict__ x_hi,
-    uint16_t* __restrict__ x_lo, int* err, int ksplit, float* __restrict__ part_out) {
+    uint16_t* __restrict__ x_lo, int* err, int ksplit, float* __restrict__ part_out,
+    int* __restrict__ route_counts) {
   __shared__ float part[kRouteWaves][kRouteChunk][65];
   __shared__ int cnt[64];
+  __shared__ int last;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -306,76 +313,77 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_mfma_kernel(
     for (int q = 1; q < kRouteWaves; q++) v = v + part[q][tl][e];
     return v;
   };
+  constexpr int kPer = kRouteChunk / kRouteWaves;
   if (ksplit > 1) {
     float* out = part_out + (size_t)blockIdx.x * kRouteChunk * 64;
-    for (int j = 0; j < kRouteChunk / kRouteWaves; j++) {
-      const int tl = wave * (kRouteChunk / kRouteWaves) + j;
-      out[tl * 64 + lane] = wave_sum_of(tl, lane);
+    float mine[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+      const int tl = wave * kPer + j;
+      mine[j] = wave_sum_of(tl, lane);
+      __hip_atomic_store(out + tl * 64 + lane, mine[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are complete
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(route_counts + chunk * 16, 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
+    __syncthreads();
+    if (!last) return;
+    if (tid == 0) __hip_atomic_store(route_counts + chunk * 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Every partial of the chunk, loaded before the first add, then added
+    // in workgroup order (this workgroup's own from registers).
+    const float* in = part_out + (size_t)chunk * ksplit * kRouteChunk * 64;
+    float v[kPer][kMaxRouteSplit];
+#pragma unroll
+    for (int j = 0; j < kPer; j++)
+#pragma unroll
+      for (int q = 0; q < kMaxRouteSplit; q++)
+        v[j][q] = q < ksplit && q != p
+                      ? __hip_atomic_load(in + ((size_t)q * kRouteChunk + wave * kPer + j) * 64 + lane,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : mine[j];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+      float a = v[j][0];
+#pragma unroll
+      for (int q = 1; q < kMaxRouteSplit; q++)
+        if (q < ksplit) a = a + v[j][q];
+      part[0][wave * kPer + j][lane] = a;
+    }
+    __syncthreads();
+    route_chunk([&](int tl, int e) { return part[0][tl][e]; }, chunk, T, E, K, normalize, scale,
+                logits, ids, weights, chunk_counts, cnt, err);
     return;
   }
   // Each wave routes two tokens on its own with the wave top-k.
-  route_chunk(wave_sum_of, t0, T, E, K, normalize, scale, logits, ids, weights, chunk_counts, cnt,
+  route_chunk(wave_sum_of, chunk, T, E, K, normalize, scale, logits, ids, weights, chunk_counts, cnt,
               err);
 }
 
-// Split router, second step: workgroup c adds chunk c's ksplit partial
-// logits in order (deterministic) and routes its 16 tokens.
-// Every partial of the thread's two (token, expert) values is loaded
-// before the first add.
-constexpr int kMaxRouteSplit = 8;
-__global__ __launch_bounds__(64 * kRouteWaves) void router_finish_kernel(
-    const float* __restrict__ part_in, int ksplit, int T, int E, int K, int normalize, float scale,
-    float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ weights,
-    int* __restrict__ chunk_counts, int* err) {
-  __shared__ int cnt[64];
-  __shared__ float lg[kRouteChunk][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (threadIdx.x < 64) cnt[threadIdx.x] = 0;
-  const float* in = part_in + (size_t)blockIdx.x * ksplit * kRouteChunk * 64;
-  constexpr int kPer = kRouteChunk / kRouteWaves;
-  float v[kPer][kMaxRouteSplit];
-#pragma unroll
-  for (int j = 0; j < kPer; j++)
-#pragma unroll
-    for (int q = 0; q < kMaxRouteSplit; q++)
-      v[j][q] = q < ksplit ? in[((size_t)q * kRouteChunk + wave * kPer + j) * 64 + lane] : 0.0f;
-#pragma unroll
-  for (int j = 0; j < kPer; j++) {
-    float a = v[j][0];
-#pragma unroll
-    for (int q = 1; q < kMaxRouteSplit; q++)
-      if (q < ksplit) a = a + v[j][q];
-    lg[wave * kPer + j][lane] = a;
-  }
-  __syncthreads();
-  auto sum_of = [&](int tl, int e) { return lg[tl][e]; };
-  route_chunk(sum_of, (int)blockIdx.x * kRouteChunk, T, E, K, normalize, scale, logits, ids,
-              weights, chunk_counts, cnt, err);
-}
 
 void launch_router_topk_mfma(const float* x, const uint16_t* w, int T, int H, int E, int K,
                              int normalize, float scale, float* logits, int* ids, float* weights,
                              int* chunk_counts, uint16_t* x_hi, uint16_t* x_lo, int* err,
-                             float* part, hipStream_t s) {
+                             float* part, int* route_counts, hipStream_t s) {
   if (T <= 0 || !router_mfma_supported(H)) return;
   const int chunks = (T + kRouteChunk - 1) / kRouteChunk;
-  const int ksplit = part ? router_ksplit(T, H) : 1;
+  const int ksplit = part && route_counts ? router_ksplit(T, H) : 1;
   const dim3 grid(chunks * ksplit), block(64 * kRouteWaves);
   const int steps = H / 32;
   const int ks = (steps + ksplit * kRouteWaves - 1) / (ksplit * kRouteWaves);
   if (ks <= 1)
     router_mfma_kernel<1><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part,
+                                                 route_counts);
   else if (ks <= 5)
     router_mfma_kernel<5><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part,
+                                                 route_counts);
   else
     router_mfma_kernel<8><<<grid, block, 0, s>>>(x, w, T, H, E, K, normalize, scale, logits, ids,
-                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part);
-  if (ksplit > 1)
-    router_finish_kernel<<<dim3(chunks), block, 0, s>>>(part, ksplit, T, E, K, normalize, scale,
-                                                        logits, ids, weights, chunk_counts, err);
+                                                 weights, chunk_counts, x_hi, x_lo, err, ksplit, part,
+                                                 route_counts);
 }
 
 void launch_topk(const float* logits, int T, int n, int K, int normalize, float scale, int* ids,
