@@ -387,6 +387,23 @@ def test_decode_edge_shapes(ctx, quant):
         check_layer(case, ctx, syn.activations(1, DECODE_EDGE["hidden"], seed=1300 + i))
 
 
+@pytest.mark.parametrize("shape,K,T,flags", [(DECODE_EDGE, 8, 17, 0),
+                                             (WIDE, 2, 5, um.FLAG_FORCE_MFMA)],
+                         ids=["hidden2048", "inter1088"])
+def test_w8a8_singles_beside_mfma_wide(ctx, shape, K, T, flags):
+    """The single-row W8A8 groups beside the MFMA engine
+    (src/decoder/mod.rs:103-104) at the widths that take the other forms of
+    that pass: a hidden width beyond 1280 (gate/up rows of up to 2048) and
+    an expert width beyond 1024 (down rows as two column halves). The seeds
+    leave 2 and 1 groups of one row."""
+    case = Case(ctx, shape, K, seed=1400 + T, quant=orc.QUANT_DYNAMIC)
+    x = syn.activations(T, shape["hidden"], seed=1500 + T)
+    say(f"W8A8 singles beside the MFMA engine, {shape}, T={T}")
+    check_layer(case, ctx, x, flags=flags)
+    _, tr = case.run(ctx, x, flags)
+    assert (np.diff(tr["expert_offsets"]) == 1).any()
+
+
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
     """48 one-token forwards queued back to back (one synchronisation at the

@@ -569,11 +569,11 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
         // small-batch engine, run before the MFMA GEMMs reuse its f32
         // hidden rows' bytes for their bf16 planes.
         phase_begin(ctx, kGateUp);
-        uocr::launch_batch_gateup(L, S, Ti, tiles_bound, uocr::kGemvChunk, st, true);
+        uocr::launch_singles_gateup(L, S, Ti, st);
         phase_end(ctx);
         if (int r = trace_hidden(S.h, S.hs)) return r;
         phase_begin(ctx, kDown);
-        uocr::launch_batch_down(L, S, Ti, tiles_bound, uocr::kGemvChunk, st, true);
+        uocr::launch_singles_down(L, S, Ti, st);
         phase_end(ctx);
       }
       const int lists = overlap ? uocr::kListRouted : uocr::kListAll;

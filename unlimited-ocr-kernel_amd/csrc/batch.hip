@@ -58,11 +58,9 @@ struct Unit {
 
 // Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
 // holds rows [ts * kSharedRows, ...) of the shared group), then ur slices of
-// each routed tile of the dispatch list. singles: only routed groups of a single
-// row (the W8A8 rows the MFMA engine leaves to this engine under
-// DynamicActivations).
+// each routed tile of the dispatch list.
 __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
-                                          int nsh, int us, int ur, int singles, Unit& u) {
+                                          int nsh, int us, int ur, Unit& u) {
   int b = blockIdx.x;
   if (b < nsh * us) {
     const int ts = b / us;
@@ -85,10 +83,40 @@ __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S
   u.routed = true;
   u.slice = b - i * ur;
   u.group_rows = S.offsets[g + 1] - S.offsets[g];
-  if (singles && u.group_rows != 1) return false;
   u.n = min(mchunk, u.group_rows - r0);
   return u.n > 0;
 }
+
+// The single-row pass (the W8A8 rows the MFMA engine leaves to this engine
+// under DynamicActivations): kernels of their own, whose workgroups each
+// read the expert offsets once and loop over the units of the groups of
+// exactly one row, so that a pass with no such group is one short round.
+// Routed groups of one row as a mask over expert ids (E <= 64).
+__device__ __forceinline__ unsigned long long single_groups(const DeviceLayer& L,
+                                                           const Scratch& S) {
+  const int e = threadIdx.x & 63;
+  const bool one = e < L.E && S.offsets[e + 1] - S.offsets[e] == 1;
+  return __ballot(one);
+}
+
+// Unit b of those groups' units (ur per group, ascending expert id), for
+// b < popcount(m) * ur. Every lane of the wave takes part.
+__device__ __forceinline__ Unit single_unit(unsigned long long m, int ur, int b) {
+  const int lane = threadIdx.x & 63;
+  const int j = b / ur;
+  const bool hit = ((m >> lane) & 1ull) && __popcll(m & ((1ull << lane) - 1ull)) == j;
+  Unit u;
+  u.g = __ffsll((long long)__ballot(hit)) - 1;
+  u.r0 = 0;
+  u.n = 1;
+  u.group_rows = 1;
+  u.routed = true;
+  u.slice = b - j * ur;
+  return u;
+}
+
+// Workgroups of a single-row pass: three per CU, one round.
+constexpr int kSinglesGrid = 768;
 
 // Row of w13 holding gate value k (up value k is 32 rows further).
 __device__ __forceinline__ int gate_row(int k) { return (k >> 5) * 64 + (k & 31); }
@@ -207,12 +235,8 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
 // and the 4 matching up rows). h = silu(gate) * up (Decoder::feed_forward,
 // src/decoder/mod.rs:114-122).
 template <int KIND, int KH, bool DYN>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_gateup_kernel(
-    DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
-  __shared__ __align__(16) BatchSmem sm;
-  Unit u;
-  if (!load_unit(L, S, T, mchunk, nsh, (L.S + 15) / 16, (L.I + 15) / 16, singles, u)) return;
+__device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
+                                            const Unit& u) {
   const int W = L.width(u.g);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = 16 * u.slice + 4 * wave + (lane >> 4);
@@ -241,6 +265,32 @@ __attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_ga
   tile_dot<KIND, KH, 0, DYN>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
     if ((lane & 15) == 0 && k < W) hout[(size_t)t * ld + k] = silu(g) * up;
   }, bs);
+}
+
+template <int KIND, int KH, bool DYN>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_gateup_kernel(
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
+  __shared__ __align__(16) BatchSmem sm;
+  Unit u;
+  if (!load_unit(L, S, T, mchunk, nsh, (L.S + 15) / 16, (L.I + 15) / 16, u)) return;
+  gateup_body<KIND, KH, DYN>(L, S, sm, u);
+}
+
+// Gate/up of the single-row W8A8 groups (INT8 weights, DynamicActivations).
+// Hidden widths beyond 1280 take two workgroups per CU (their loop spilled
+// at three).
+template <int KH>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 3 : 2))) void singles_gateup_kernel(
+    DeviceLayer L, Scratch S) {
+  __shared__ __align__(16) BatchSmem sm;
+  const unsigned long long m = single_groups(L, S);
+  const int ur = (L.I + 15) / 16, n = __popcll(m) * ur;
+  for (int b = blockIdx.x; b < n; b += gridDim.x) {
+    gateup_body<kInt8, KH, true>(L, S, sm, single_unit(m, ur, b));
+    __syncthreads();  // this unit's LDS consumed before the next is staged
+  }
 }
 
 // Down: a unit is 32 output features of one tile (each wave 8 full rows of
@@ -295,15 +345,29 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
 template <int KIND, bool DYN>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(3))) void batch_down_kernel(
-    DeviceLayer L, Scratch S, int T, int mchunk, int nsh, int singles) {
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
   __shared__ __align__(16) BatchSmem sm;
   Unit u;
-  if (!load_unit(L, S, T, mchunk, nsh, down_units(L.H, L.S), down_units(L.H, L.I), singles, u))
+  if (!load_unit(L, S, T, mchunk, nsh, down_units(L.H, L.S), down_units(L.H, L.I), u))
     return;
   if (L.width(u.g) <= kSegK)
     down_body<KIND, false, DYN>(L, S, sm, u);
   else
     down_body<KIND, true, DYN>(L, S, sm, u);
+}
+
+// Down of the single-row W8A8 groups; HALVES as down_body (routed width
+// beyond kSegK).
+template <bool HALVES>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(3))) void singles_down_kernel(DeviceLayer L, Scratch S) {
+  __shared__ __align__(16) BatchSmem sm;
+  const unsigned long long m = single_groups(L, S);
+  const int ur = down_units(L.H, L.I), n = __popcll(m) * ur;
+  for (int b = blockIdx.x; b < n; b += gridDim.x) {
+    down_body<kInt8, HALVES, true>(L, S, sm, single_unit(m, ur, b));
+    __syncthreads();  // this unit's LDS consumed before the next is staged
+  }
 }
 
 // ------------------------------------------------------------- small router
@@ -424,22 +488,29 @@ int routed_bound(const DeviceLayer& L, int T, int tiles_bound, int mchunk) {
   return T <= mchunk ? min(L.E, T * L.K) : tiles_bound;
 }
 
+// Workgroups of a single-row pass: kSinglesGrid, or fewer where the groups
+// that can hold one row (min(E, T k)) have fewer units.
+dim3 singles_grid(const DeviceLayer& L, int T, int ur) {
+  return dim3((unsigned)std::min<long long>(
+      kSinglesGrid, std::min<long long>(L.E, (long long)T * L.K) * ur));
+}
+
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        int mchunk, int singles, hipStream_t s) {
-  const int nsh = singles ? 0 : (T + kSharedRows - 1) / kSharedRows;
+                        int mchunk, hipStream_t s) {
+  const int nsh = (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * ((L.S + 15) / 16) + routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16);
   const dim3 grid(units), block(256);
   if (L.quant_mode == kQuantDynamic) {
     if (L.H <= 1280)
-      batch_gateup_kernel<KIND, 1280, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+      batch_gateup_kernel<KIND, 1280, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
     else
-      batch_gateup_kernel<KIND, kWideK, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+      batch_gateup_kernel<KIND, kWideK, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
   } else {
     if (L.H <= 1280)
-      batch_gateup_kernel<KIND, 1280, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+      batch_gateup_kernel<KIND, 1280, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
     else
-      batch_gateup_kernel<KIND, kWideK, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+      batch_gateup_kernel<KIND, kWideK, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
   }
 }
 
@@ -452,25 +523,41 @@ bool batch_supported(const DeviceLayer& L) {
 }
 
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s, bool singles) {
+                         int mchunk, hipStream_t s) {
   if (L.quant_mode == 0)
-    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, singles, s);
+    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, s);
   else
-    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, singles, s);
+    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, s);
+}
+
+void launch_singles_gateup(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s) {
+  const dim3 grid = singles_grid(L, T, (L.I + 15) / 16), block(256);
+  if (L.H <= 1280)
+    singles_gateup_kernel<1280><<<grid, block, 0, s>>>(L, S);
+  else
+    singles_gateup_kernel<kWideK><<<grid, block, 0, s>>>(L, S);
+}
+
+void launch_singles_down(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s) {
+  const dim3 grid = singles_grid(L, T, down_units(L.H, L.I)), block(256);
+  if (L.I <= kSegK)
+    singles_down_kernel<false><<<grid, block, 0, s>>>(L, S);
+  else
+    singles_down_kernel<true><<<grid, block, 0, s>>>(L, S);
 }
 
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s, bool singles) {
-  const int nsh = singles ? 0 : (T + kSharedRows - 1) / kSharedRows;
+                       hipStream_t s) {
+  const int nsh = (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * down_units(L.H, L.S) +
                     routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I);
   const dim3 grid(units), block(256);
   if (L.quant_mode == 0)
-    batch_down_kernel<kBF16, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+    batch_down_kernel<kBF16, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
   else if (L.quant_mode == kQuantDynamic)
-    batch_down_kernel<kInt8, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+    batch_down_kernel<kInt8, true><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
   else
-    batch_down_kernel<kInt8, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh, singles);
+    batch_down_kernel<kInt8, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
 }
 
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,

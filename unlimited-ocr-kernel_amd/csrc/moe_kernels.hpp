@@ -143,9 +143,13 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 // logits, then one workgroup that routes and builds the dispatch.
 bool batch_supported(const DeviceLayer& L);
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s, bool singles = false);
+                         int mchunk, hipStream_t s);
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s, bool singles = false);
+                       hipStream_t s);
+// The routed groups of exactly one row of an INT8 DynamicActivations layer
+// (W8A8 row by row) beside the MFMA engine, after its dispatch.
+void launch_singles_gateup(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s);
+void launch_singles_down(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s);
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
                         hipStream_t s);
 
