@@ -76,6 +76,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=12,
                     help="layers in the headline stack (12 for the measured workload; fewer "
                          "only to shorten counter-collection runs; 0 skips the headline)")
+    ap.add_argument("--decode-timeline", type=int, default=0,
+                    help="after timing the one-token secondaries, this many more forwards with "
+                         "the engine's per-workgroup timeline (uocr_moe_trace::decode_stamps), "
+                         "summarised per role (0: none)")
     ap.add_argument("--profile-copy", action="store_true",
                     help="after timing, copy 256 MiB once so that counter runs can scale "
                          "FETCH_SIZE/WRITE_SIZE against a plain copy of known size")
@@ -274,6 +278,48 @@ def main():
     wanted = [] if args.secondary == "none" else args.secondary.split(",")
 
     # ------------------------------------------------------------- decode
+    def decode_timeline(dl, xs, ys, n):
+        """n one-token forwards queued back to back (as in the timed loop),
+        each with its own timeline buffer; per role and stamp, the median
+        over forwards of the median over the role's workgroups of the stamp's
+        time after the launch's first workgroup started (us; the counter runs
+        at 100 MHz). Also the median span (first start to last stamp)."""
+        rows = um.decode_stamp_rows(H, I, E, SH, K)
+        nrow = sum(rows.values())
+        st = torch.zeros((n, nrow, um.DECODE_STAMPS), dtype=torch.int64, device="cuda")
+        sync()
+        for i in range(n):
+            um.forward(ctx, dl[i % 12], xs[i % 64], ys[i % 64],
+                       trace={"decode_stamps": st[i]}, sync=False)
+        sync()
+        a = st.cpu().numpy()
+        names = {"logit": ("start", "logits stored", "stores complete", "counted in"),
+                 "shared": ("start", None, None, "rows dotted", "counted in"),
+                 "routed": ("start", "input staged", "experts selected", "rows dotted",
+                            "counted in"),
+                 "down": ("start", "experts selected", None, "hidden values ready",
+                          "rows dotted", "output written")}
+        out, spans, r0 = {}, [], 0
+        t0 = a[:, :, 0].min(axis=1)
+        for f in range(n):
+            last = a[f][a[f] > 0].max()
+            spans.append((last - t0[f]) / 100.0)
+        for role in um.DECODE_ROLES:
+            r1 = r0 + rows[role]
+            out[role] = {}
+            for j, name in enumerate(names[role]):
+                if name is None:
+                    continue
+                per = [float(np.median(a[f, r0:r1, j] - t0[f])) / 100.0 for f in range(n)]
+                out[role][name] = round(statistics.median(per), 2)
+            r0 = r1
+        out["span"] = round(statistics.median(spans), 2)
+        out["forwards"] = n
+        for role in um.DECODE_ROLES:
+            log(f"  timeline {role}: " + ", ".join(f"{k} {v:.2f}" for k, v in out[role].items()))
+        log(f"  timeline span (first start to last stamp): {out['span']:.2f} us over {n} forwards")
+        return out
+
     def decode(quant: int, T: int):
         kind = {um.QUANT_NONE: "bf16", um.QUANT_WEIGHTS_ONLY: "int8",
                 um.QUANT_DYNAMIC: "w8a8"}[quant]
@@ -325,6 +371,9 @@ def main():
         ph = ctx.timings()
         ctx.set_timing([])
         gpu_ms = sum(v[1] for v in ph.values()) / steps
+        timeline = None
+        if T == 1 and args.decode_timeline > 0:
+            timeline = decode_timeline(dl, xs, ys, args.decode_timeline)
         for l in dl:
             l.close()
         torch.cuda.empty_cache()
@@ -368,6 +417,8 @@ def main():
                "hbm_frac_wall": round(nbytes / (wall_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                "phases_ms": {k: round(v[1] / steps, 5) for k, v in ph.items() if v[0]},
                "cpu_baseline": cpu_dec}
+        if timeline:
+            out["timeline_us"] = timeline
         log(f"{name}: {wall_ms*1e3:.1f} us wall ({n_uniq:.1f} experts), kernels "
             f"{gpu_ms*1e3:.1f} us with events")
         return out

@@ -143,7 +143,24 @@ typedef struct uocr_w8a8_trace {
 } uocr_w8a8_trace;
 
 /* Optional per-forward trace, device pointers; NULL members are skipped.
- * Routing order is route()'s: probability descending, id ascending. */
+ * Routing order is route()'s: probability descending, id ascending.
+ *
+ * decode_stamps (an instrument with no counterpart in the reference): for a
+ * forward on the one-token engine, the device's 100 MHz real-time counter
+ * at the phase boundaries of every workgroup of its launch, as
+ * [UOCR_DECODE_STAMP_ROWS(E, S, k, I, H)][8] uint64 (S = the shared width,
+ * I * n_shared_experts). Rows in launch order and their stamps:
+ *   ceil(E/8) router-logit workgroups: 0 start, 1 logits stored, 2 stores
+ *     complete, 3 counted in;
+ *   S/32 shared gate/up workgroups: 0 start, 3 rows dotted, 4 counted in;
+ *   k*I/32 routed gate/up workgroups: 0 start, 1 input staged, 2 experts
+ *     selected, 3 rows dotted, 4 counted in;
+ *   H/8 down workgroups: 0 start, 1 experts selected, 3 every hidden value
+ *     ready, 4 rows dotted, 5 output written.
+ * Other stamps are left untouched. Other engines ignore the member. */
+#define UOCR_DECODE_STAMPS 8
+#define UOCR_DECODE_STAMP_ROWS(E, S, k, I, H) \
+  (((E) + 7) / 8 + (S) / 32 + (k) * ((I) / 32) + (H) / 8)
 typedef struct uocr_moe_trace {
   float* logits;           /* [T,E] router logits */
   int32_t* topk_ids;       /* [T,k] */
@@ -152,6 +169,7 @@ typedef struct uocr_moe_trace {
   int32_t* perm_rows;      /* [T*k] token row of each assignment, expert-major */
   float* perm_weights;     /* [T*k] routing weight of each assignment */
   const uocr_w8a8_trace* w8a8; /* W8A8 block sums (NULL: none) */
+  uint64_t* decode_stamps; /* one-token engine timeline (NULL: none) */
 } uocr_moe_trace;
 
 typedef struct uocr_gpu_ctx uocr_gpu_ctx;

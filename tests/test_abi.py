@@ -58,3 +58,23 @@ def test_token_cap_is_derived_from_byte_ranges():
         assert m == expect(H, I, E, SH, K)
         assert m < 262144
         assert m * max(2 * H, 2 * K * I, 2 * I * SH, K * H) <= limit
+
+
+def test_decode_timeline_layout():
+    """uocr_moe_trace ends with the decode_stamps pointer (eight pointers in
+    all) and the binding's row count per role follows the header's
+    UOCR_DECODE_STAMP_ROWS: router-logit, shared gate/up, routed gate/up and
+    down workgroups of the one-token launch."""
+    assert [f[0] for f in um.Trace._fields_][-1] == "decode_stamps"
+    assert ctypes.sizeof(um.Trace) == 8 * ctypes.sizeof(ctypes.c_void_p)
+    text = open(os.path.join(REPO, "include", "uocr_moe.h")).read()
+    assert re.search(r"#define UOCR_DECODE_STAMPS 8\b", text)
+    m = re.search(r"#define UOCR_DECODE_STAMP_ROWS\(E, S, k, I, H\) \\\n\s*(.+)\n", text)
+    assert m, "row formula not found"
+    formula = m.group(1).replace("/", "//")
+    for (H, I, E, SH, K) in ((1280, 896, 64, 2, 6), (2048, 512, 37, 2, 8), (256, 64, 8, 1, 2)):
+        rows = um.decode_stamp_rows(H, I, E, SH, K)
+        want = eval(formula, {}, {"E": E, "S": I * SH, "k": K, "I": I, "H": H})
+        assert sum(rows.values()) == want
+        assert list(rows) == list(um.DECODE_ROLES)
+    assert um.DECODE_STAMPS == 8

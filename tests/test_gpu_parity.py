@@ -455,6 +455,49 @@ def test_decode_wait_bound(ctx, full_int8):
         c2.close()
 
 
+# Stamps each role of the one-token engine writes, in the order it passes
+# them (uocr_moe_trace::decode_stamps).
+DECODE_STAMPS_SET = {"logit": (0, 1, 2, 3), "shared": (0, 3, 4), "routed": (0, 1, 2, 3, 4),
+                     "down": (0, 1, 3, 4, 5)}
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_decode_timeline_stamps(ctx, full_bf16, full_int8, kind):
+    """The one-token engine's timeline: every workgroup of the launch
+    writes its phase stamps (the device's real-time counter) in the order it
+    passes them, leaves the other stamps and anything past its rows
+    untouched, and the forward gives the same bits as without the
+    timeline."""
+    case = {"bf16": full_bf16, "int8": full_int8}[kind]
+    rows = um.decode_stamp_rows(FULL["hidden"], FULL["inter"], FULL["experts"], FULL["shared"],
+                                case.top_k)
+    assert rows == {"logit": 8, "shared": 56, "routed": 168, "down": 160}
+    n = sum(rows.values())
+    x = syn.activations(1, 1280, seed=9300)
+    xd = dev(x)
+    y0, y1 = torch.empty_like(xd), torch.empty_like(xd)
+    st = torch.full((n + 1, um.DECODE_STAMPS), -1, dtype=torch.int64, device="cuda")
+    um.forward(ctx, case.layer, xd, y0)
+    um.forward(ctx, case.layer, xd, y1, trace={"decode_stamps": st[:n]})
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
+    a = st.cpu().numpy()
+    assert (a[n] == -1).all()  # the row past the launch is never written
+    r0 = 0
+    for role in um.DECODE_ROLES:
+        blk = a[r0:r0 + rows[role]]
+        idx = DECODE_STAMPS_SET[role]
+        unset = [j for j in range(um.DECODE_STAMPS) if j not in idx]
+        assert (blk[:, list(idx)] > 0).all(), role
+        assert (blk[:, unset] == -1).all(), role
+        assert (np.diff(blk[:, list(idx)], axis=1) >= 0).all(), role
+        r0 += rows[role]
+    # One launch: its stamps span microseconds, not milliseconds (100 MHz).
+    span = a[:n][a[:n] > 0].max() - a[:n, 0].min()
+    say(f"  decode timeline {kind}: span {span / 100:.1f} us")
+    assert 0 < span < 100_000
+
+
 def _w8a8_trace(T, K, E):
     """Device buffers of uocr_w8a8_trace at the full layer shape."""
     S = FULL["inter"] * FULL["shared"]

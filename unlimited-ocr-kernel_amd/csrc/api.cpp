@@ -401,6 +401,8 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
   hipStream_t st = ex.stream;
   const uocr_w8a8_trace* q8t =
       trace && L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS ? trace->w8a8 : nullptr;
+  static_assert(uocr::kDecodeStamps == UOCR_DECODE_STAMPS, "decode timeline row");
+  if (trace) S.stamps = reinterpret_cast<unsigned long long*>(trace->decode_stamps);
   if (q8t) {
     S.q8.gateup = q8t->gateup_sums;
     S.q8.down = q8t->down_sums;

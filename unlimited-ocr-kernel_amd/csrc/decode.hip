@@ -184,6 +184,18 @@ __device__ __forceinline__ void wait_flag(int* flag, const Scratch& S) {
   asm volatile("" ::: "memory");
 }
 
+// The launch's timeline (uocr_moe_trace::decode_stamps): thread 0 of the
+// workgroup stores the device's real-time counter (100 MHz) as stamp i of
+// its workgroup's row. ST: the instantiation launched only when a timeline
+// is asked for (the others carry no trace of it).
+template <bool ST>
+__device__ __forceinline__ void stamp(const Scratch& S, int i) {
+  if constexpr (ST) {
+    if (threadIdx.x == 0)
+      S.stamps[(size_t)blockIdx.x * kDecodeStamps + i] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
 // Sets flags[0 .. n) (stride kLine) with the 64 lanes of one wave.
 __device__ __forceinline__ void set_flags(int* flags, int n, int lane) {
   for (int j = lane; j < n; j += 64) sync_store(flags + j * kLine, 1);
@@ -255,11 +267,12 @@ __device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, 
 
 // Logit workgroup b: router rows 8b + q and 8b + q + 4 (q = lane / 16; BF16
 // router, FP32 x; rows past E read as zero) dotted with x by one wave.
-template <int KH>
+template <int KH, bool ST>
 __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
                            const SyncMap& M, const DecodeGrid& G, int b, int lane) {
   const int q = lane >> 4;
   const int ra = kLogitsPerWg * b + q, rb = ra + 4;
+  stamp<ST>(S, 0);
   RowPair<kBF16, KH> R;
   issue_rows(R, L.router, nullptr, L.E, L.H, ra, rb);
   RowStage<KH> X;
@@ -271,15 +284,18 @@ __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& s
     if (ra < L.E) shared_store(S.logits + ra, r0);
     if (rb < L.E) shared_store(S.logits + rb, r1);
   }
+  stamp<ST>(S, 1);
   // Counted once the logits are stored; the last logit workgroup releases
   // every workgroup waiting for them.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  stamp<ST>(S, 2);
   int last = 0;
   if (lane == 0) last = sync_add(M.logit_count) == G.n_logit - 1;
   if (__builtin_amdgcn_readfirstlane(last)) {
     set_flags(M.route_flag, G.n_down, lane);
     if (lane == 0) sync_store(M.logit_count, 0);
   }
+  stamp<ST>(S, 3);
 }
 
 // Gate/up workgroup b. b < S/32: shared-expert hidden values 32b .. 32b+31
@@ -289,12 +305,13 @@ __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& s
 // also writes the routing and the one-token dispatch (ids, weights,
 // offsets, permutation, row tiles). Each wave counts itself done once its
 // hidden values are stored.
-template <int KIND, int KH>
+template <int KIND, int KH, bool ST>
 __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
                             const SyncMap& M, const DecodeGrid& G, int b, int wave, int lane) {
   const int q = lane >> 4;
   const int n_shared = L.S / kHidPerWg;
   const int per_expert = L.I / kHidPerWg;
+  stamp<ST>(S, 0);
   if (b < n_shared) {
     const int k = b * kHidPerWg + 4 * wave + q;
     const int ra = gate_row(k);
@@ -310,8 +327,10 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
     }
     float r0, r1;
     dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
+    stamp<ST>(S, 3);
     if ((lane & 15) == 0) shared_store(S.gu + (size_t)L.K * L.I + k, silu(r0) * r1);
     count_gateup(M, G, b, wave, lane);
+    stamp<ST>(S, 4);
     return;
   }
   const int rb = b - n_shared;
@@ -327,6 +346,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
     issue_rows(R, L.router, nullptr, L.E, L.H, 8 * wave + q, 8 * wave + q + 4);
     if (wave == 0) store_row(X, sm.xl, L.H, lane);
     __syncthreads();
+    stamp<ST>(S, 1);
     float r0, r1;
     dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
     if ((lane & 15) == 0) {
@@ -371,6 +391,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
     }
   }
   __syncthreads();
+  stamp<ST>(S, 2);
   const int g = clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, slot)), L.E);
   const int k = kHidPerWg * (rb - slot * per_expert) + 4 * wave + q;
   const int ra = gate_row(k);
@@ -386,8 +407,10 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   }
   float r0, r1;
   dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
+  stamp<ST>(S, 3);
   if ((lane & 15) == 0) shared_store(S.gu + (size_t)slot * L.I + k, silu(r0) * r1);
   count_gateup(M, G, b, wave, lane);
+  stamp<ST>(S, 4);
 }
 
 // Down workgroup b: output features 8b .. 8b+7; wave w < K = the selected
@@ -395,7 +418,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
 // shared expert's reduction (S/2 columns each); then the ordered combine
 // of the 8 features: out = (residual +) ((y_s0 + y_s1) + p_0 y_0 + p_1 y_1
 // + ...), mul then add.
-template <int KIND>
+template <int KIND, bool ST>
 __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, const SyncMap& M,
                           const DecodeGrid& G, int b, const float* residual, float* out, int wave,
                           int lane) {
@@ -403,6 +426,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   const int f0 = 8 * b;
   const bool routed = wave < L.K;
   const int half = L.S / 2;
+  stamp<ST>(S, 0);
   // This wave's hidden row: an expert's I values, or half the shared S.
   const int n = routed ? L.I : half;
   // The shared expert's rows need no routing: issued first.
@@ -420,6 +444,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
     if (lane == 0) sm.mask = r.mask;
   }
   __syncthreads();
+  stamp<ST>(S, 1);
   const int g =
       routed ? clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, wave)), L.E) : L.E;
   if (routed) issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, 0, n, f0 + q, f0 + q + 4);
@@ -428,6 +453,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   // itself (wave 0 waits for this workgroup's flag).
   if (wave == 0) wait_line(M.down_flags + b * kLine, G.n_up() < kSubCounts ? G.n_up() : kSubCounts, S);
   __syncthreads();
+  stamp<ST>(S, 3);
   const float* hrow = routed ? S.gu + (size_t)wave * L.I
                              : S.gu + (size_t)L.K * L.I + (size_t)(wave - L.K) * half;
   RowStage<kNarrow> Hr;
@@ -445,6 +471,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   }
   float r0, r1;
   dot_rows(P, n, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1, bs);
+  stamp<ST>(S, 4);
   if ((lane & 15) == 0) {
     sm.yl[wave][q] = r0;
     sm.yl[wave][q + 4] = r1;
@@ -458,11 +485,12 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
     if (residual) acc = res_f + acc;
     out[f0 + lane] = acc;
   }
+  stamp<ST>(S, 5);
 }
 
 constexpr int kBlockWaves = kUpWaves > kMaxK + 2 ? kUpWaves : kMaxK + 2;
 
-template <int KIND, int KH>
+template <int KIND, int KH, bool ST>
 __global__ __launch_bounds__(64 * kBlockWaves) void decode_kernel(DeviceLayer L, Scratch S,
                                                                   const float* residual, float* out) {
   __shared__ __align__(16) DecodeSmem sm;
@@ -473,16 +501,16 @@ __global__ __launch_bounds__(64 * kBlockWaves) void decode_kernel(DeviceLayer L,
   const SyncMap M(S.sync, G);
   int b = blockIdx.x;
   if (b < G.n_logit) {
-    if (wave == 0) logit_role<KH>(L, S, sm.up, M, G, b, lane);
+    if (wave == 0) logit_role<KH, ST>(L, S, sm.up, M, G, b, lane);
     return;
   }
   b -= G.n_logit;
   if (b < G.n_up()) {
-    if (wave < kUpWaves) gateup_role<KIND, KH>(L, S, sm.up, M, G, b, wave, lane);
+    if (wave < kUpWaves) gateup_role<KIND, KH, ST>(L, S, sm.up, M, G, b, wave, lane);
     return;
   }
   b -= G.n_up();
-  if (wave < L.K + 2) down_role<KIND>(L, S, sm.down, M, G, b, residual, out, wave, lane);
+  if (wave < L.K + 2) down_role<KIND, ST>(L, S, sm.down, M, G, b, residual, out, wave, lane);
 }
 
 template <int KIND, int KH>
@@ -490,7 +518,10 @@ void launch_kind(const DeviceLayer& L, const Scratch& S, const float* residual, 
                  hipStream_t s) {
   const DecodeGrid G(L);
   const int waves = L.K + 2 > kUpWaves ? L.K + 2 : kUpWaves;
-  decode_kernel<KIND, KH><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+  if (S.stamps)
+    decode_kernel<KIND, KH, true><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+  else
+    decode_kernel<KIND, KH, false><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
 }
 
 template <int KH>
@@ -517,6 +548,8 @@ bool decode_supported(const DeviceLayer& L) {
                     (int)kDecodeSyncBytes,
                 "decode sync words");
   static_assert(kSubCounts <= kLine, "a down workgroup's sub-set flags share one line");
+  static_assert(kLogitsPerWg == 8 && kHidPerWg == 32,
+                "the timeline's row count (UOCR_DECODE_STAMP_ROWS) follows these widths");
   return L.H <= kWide && L.S <= kWide && L.I <= kNarrow && L.K >= 1 && L.K <= kMaxK &&
          L.E <= 64 && L.H % 8 == 0 && L.I % kHidPerWg == 0 && L.S % kHidPerWg == 0 &&
          L.S % 64 == 0;

@@ -65,6 +65,9 @@ struct Q8Trace {
 };
 
 // Per-forward device scratch carved from the context's reservation.
+// Stamps per workgroup row of the decode engine's timeline.
+constexpr int kDecodeStamps = 8;
+
 struct Scratch {
   float* logits;    // [T,E]
   int* topk_ids;    // [T,K]
@@ -90,6 +93,9 @@ struct Scratch {
   int* sync;        // kDecodeSyncBytes: the decode engine's counts and flags (zero between launches)
   int wait_limit;   // the decode engine's wait bound in polls (< 0: its default)
   Q8Trace q8;       // W8A8 trace (tests), all null by default
+  // The decode engine's timeline: kDecodeStamps real-time stamps per
+  // workgroup of its launch (uocr_moe_trace::decode_stamps), null: none.
+  unsigned long long* stamps = nullptr;
 };
 
 int max_tiles(int T, int K, int E, int bm);

@@ -120,7 +120,21 @@ class W8A8Trace(ctypes.Structure):
 class Trace(ctypes.Structure):
     _fields_ = [(n, _P) for n in ("logits", "topk_ids", "topk_weights", "expert_offsets",
                                   "perm_rows", "perm_weights")] + [
-        ("w8a8", ctypes.POINTER(W8A8Trace))]
+        ("w8a8", ctypes.POINTER(W8A8Trace)), ("decode_stamps", _P)]
+
+
+# The one-token engine's timeline (uocr_moe_trace::decode_stamps): rows of
+# DECODE_STAMPS uint64 stamps of the device's 100 MHz real-time counter, one
+# row per workgroup of its launch in this order.
+DECODE_STAMPS = 8
+DECODE_ROLES = ("logit", "shared", "routed", "down")
+
+
+def decode_stamp_rows(hidden: int, inter: int, experts: int, shared: int, top_k: int) -> dict:
+    """Workgroup rows per role of the one-token engine's launch
+    (UOCR_DECODE_STAMP_ROWS), in launch order."""
+    return {"logit": (experts + 7) // 8, "shared": inter * shared // 32,
+            "routed": top_k * (inter // 32), "down": hidden // 8}
 
 
 def _load():
@@ -335,6 +349,7 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
         if trace.get("w8a8"):
             q8 = W8A8Trace(*[_ptr(trace["w8a8"].get(n)) for n in W8A8_TRACE_FIELDS])
             tr.w8a8 = ctypes.pointer(q8)
+        tr.decode_stamps = _ptr(trace.get("decode_stamps"))
     fn = lib.uocr_moe_forward if sync else lib.uocr_moe_forward_async
     _check(fn(ctx.handle, layer.handle, _ptr(x), T, _ptr(y), flags,
               ctypes.byref(tr) if tr is not None else None))
