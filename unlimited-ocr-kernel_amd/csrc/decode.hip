@@ -447,7 +447,24 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   stamp<ST>(S, 1);
   const int g =
       routed ? clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, wave)), L.E) : L.E;
-  if (routed) issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, 0, n, f0 + q, f0 + q + 4);
+  if (routed) {
+    // The routed down rows are needed only once every hidden value is in
+    // (~6 us after the selection), while the routed gate/up rows, read from
+    // HBM at the same time, are on the critical path: issued at once, they
+    // took a third of HBM from them. They wait for the time those rows take
+    // at the HBM peak (80 KB per 10 ns tick) less 0.44 us — 1.45 us INT8,
+    // 2.9 us BF16 at the model shape, measured best of 1.0-5.0 us (per
+    // token 16.1 -> 15.8 us INT8, 18.4 -> 17.9 us BF16); issuing them after
+    // the hidden values were in cost 0.8 us instead. A wait on the
+    // real-time counter always ends.
+    const long long up_bytes = (long long)L.K * 2 * L.I * L.H * (KIND == kBF16 ? 16 : 9) / 8;
+    const long long ticks = up_bytes / 81920 - 44;
+    if (ticks > 0) {
+      const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)ticks;
+      while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(2);
+    }
+    issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, 0, n, f0 + q, f0 + q + 4);
+  }
   const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
   // The hidden rows are whole once every gate/up workgroup has counted
   // itself (wave 0 waits for this workgroup's flag).
