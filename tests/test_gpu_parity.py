@@ -663,17 +663,22 @@ def test_int8_mfma(ctx, full_int8, full_dynamic, T):
         assert (counts == 1).any(), counts  # the W8A8 single-row path ran
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
-def test_one_stream_matches_two_streams(ctx, full_bf16, full_int8, kind):
+@pytest.mark.parametrize("kind", ["bf16", "int8", "w8a8"])
+def test_one_stream_matches_two_streams(ctx, full_bf16, full_int8, full_dynamic, kind):
     """Up to 2048 tokens the shared expert's GEMMs run on a second stream
     after a split of the input into bf16 planes; on one stream (phase
-    timing on) the router writes those planes itself. Same bits either way,
-    in both activation classes."""
-    case = full_bf16 if kind == "bf16" else full_int8
-    x = syn.activations(512, 1280, seed=811)
+    timing on) the router writes those planes itself. Under
+    DynamicActivations the single-row pass follows the shared expert's
+    GEMMs on the second stream (24 tokens leave 15 groups of one row). Same
+    bits either way, in both activation classes."""
+    case = {"bf16": full_bf16, "int8": full_int8, "w8a8": full_dynamic}[kind]
+    T = 24 if kind == "w8a8" else 512
+    x = syn.activations(T, 1280, seed=811)
     for flags, name in ((0, "fp32-class"), (um.FLAG_BF16_ACTIVATIONS, "bf16 activations")):
-        say(f"{kind} T=512 {name}: two streams vs one")
-        y2, _ = case.run(ctx, x, flags=um.FLAG_FORCE_MFMA | flags)
+        say(f"{kind} T={T} {name}: two streams vs one")
+        y2, tr = case.run(ctx, x, flags=um.FLAG_FORCE_MFMA | flags)
+        if kind == "w8a8":
+            assert (np.diff(tr["expert_offsets"]) == 1).sum() == 15
         ctx.set_timing("all")
         try:
             y1, _ = case.run(ctx, x, flags=um.FLAG_FORCE_MFMA | flags)

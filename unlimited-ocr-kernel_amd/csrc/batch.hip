@@ -234,7 +234,11 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
 // Gate/up: a unit is 16 hidden values of one tile (each wave 4 gate rows
 // and the 4 matching up rows). h = silu(gate) * up (Decoder::feed_forward,
 // src/decoder/mod.rs:114-122).
-template <int KIND, int KH, bool DYN>
+// SINGLE: the single-row pass beside the MFMA engine, whose hidden row of
+// group g lives at gu + g I (the MFMA engine's hidden planes take the bytes
+// of h); the W8A8 trace's hidden row is then written here, so the trace's
+// positions of multi-row groups stay untouched.
+template <int KIND, int KH, bool DYN, bool SINGLE = false>
 __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                             const Unit& u) {
   const int W = L.width(u.g);
@@ -248,8 +252,11 @@ __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch&
     const int row = u.routed ? S.perm_rows[base + t] : base + t;
     return S.xn + (size_t)row * L.H;
   };
-  float* hout = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
+  float* hout = SINGLE     ? S.gu + (size_t)u.g * L.I
+                : u.routed ? S.h + (size_t)base * L.I
+                           : S.hs + (size_t)base * L.S;
   const int ld = u.routed ? L.I : L.S;
+  float* htrace = SINGLE && S.q8.hidden ? S.q8.hidden + (size_t)base * L.I : nullptr;
   BlockSumOut bs;
   if (DYN && u.group_rows == 1 && k < W) {
     // A single-row group: position `base` (routed) or the one token (shared).
@@ -263,7 +270,11 @@ __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch&
     }
   }
   tile_dot<KIND, KH, 0, DYN>(L, S, sm, P, L.H, 0, L.H, L.H, u, row_of, [&](int t, float g, float up) {
-    if ((lane & 15) == 0 && k < W) hout[(size_t)t * ld + k] = silu(g) * up;
+    if ((lane & 15) == 0 && k < W) {
+      const float h = silu(g) * up;
+      hout[(size_t)t * ld + k] = h;
+      if (htrace) htrace[k] = h;
+    }
   }, bs);
 }
 
@@ -288,7 +299,7 @@ __attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 3 : 2))) void singles_gateup_ker
   const unsigned long long m = single_groups(L, S);
   const int ur = (L.I + 15) / 16, n = __popcll(m) * ur;
   for (int b = blockIdx.x; b < n; b += gridDim.x) {
-    gateup_body<kInt8, KH, true>(L, S, sm, single_unit(m, ur, b));
+    gateup_body<kInt8, KH, true, true>(L, S, sm, single_unit(m, ur, b));
     __syncthreads();  // this unit's LDS consumed before the next is staged
   }
 }
@@ -297,7 +308,7 @@ __attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 3 : 2))) void singles_gateup_ker
 // the down matrix), or, for widths beyond kSegK, 16 output features with
 // each row's two column halves in the lanes' two segments. Writes y
 // (routed, dispatched order) or ys.
-template <int KIND, bool HALVES, bool DYN>
+template <int KIND, bool HALVES, bool DYN, bool SINGLE = false>
 __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                           const Unit& u) {
   const int W = L.width(u.g);
@@ -308,7 +319,9 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   RowPair<KIND, kSegK> P;
   issue_segs(P, w2_of<KIND>(L, u.g), s2_of<KIND>(L, u.g), L.H, W, ra, 0, rb, HALVES ? seg : 0, seg);
   const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
-  const float* hin = u.routed ? S.h + (size_t)base * L.I : S.hs + (size_t)base * L.S;
+  const float* hin = SINGLE     ? S.gu + (size_t)u.g * L.I
+                      : u.routed ? S.h + (size_t)base * L.I
+                                 : S.hs + (size_t)base * L.S;
   auto row_of = [&](int t) { return hin + (size_t)t * W; };
   float* yout = u.routed ? S.y + (size_t)base * L.H : S.ys + (size_t)base * L.H;
   BlockSumOut bs;
@@ -365,7 +378,7 @@ __attribute__((amdgpu_waves_per_eu(3))) void singles_down_kernel(DeviceLayer L, 
   const unsigned long long m = single_groups(L, S);
   const int ur = down_units(L.H, L.I), n = __popcll(m) * ur;
   for (int b = blockIdx.x; b < n; b += gridDim.x) {
-    down_body<kInt8, HALVES, true>(L, S, sm, single_unit(m, ur, b));
+    down_body<kInt8, HALVES, true, true>(L, S, sm, single_unit(m, ur, b));
     __syncthreads();  // this unit's LDS consumed before the next is staged
   }
 }
