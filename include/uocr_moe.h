@@ -128,8 +128,9 @@ typedef struct uocr_moe_int8_weights {
  *   gateup_sums [T*k][2*I][H/32]  rows 0..I-1 gate_proj, I..2I-1 up_proj
  *   down_sums   [T*k][H][I/32]
  *   hidden      [T*k][I]
- * Positions of multi-row groups are left untouched. The shared expert is a
- * single-row group only when T == 1:
+ * Positions of multi-row groups are left untouched (under
+ * UOCR_FLAG_INT8_MFMA every group computes this way, so every position is
+ * written). The shared expert is a single-row group only when T == 1:
  *   shared_gateup_sums [2*S][H/32], shared_down_sums [H][S/32],
  *   shared_hidden [S].
  * Device pointers; NULL members are skipped. */

@@ -76,6 +76,8 @@ def _load():
                                          _SZ, _P, ctypes.c_int]),
         "orc_moe_block_rows": (ctypes.c_int, [ctypes.POINTER(MoeLayerStruct), _P, ctypes.c_float,
                                               _P, _SZ, _P, ctypes.c_int]),
+        "orc_moe_experts_threads": (ctypes.c_int, [ctypes.POINTER(MoeLayerStruct), _P, _SZ, _P,
+                                                   ctypes.c_int, ctypes.c_int]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -325,6 +327,21 @@ def moe_experts(w: MoeWeights, x, threads=1, scratch_limit=0, trace=False):
     del keep
     _check(status, "experts")
     return (y, tr) if trace else y
+
+
+def moe_experts_threads(w: MoeWeights, x, threads=1, row_threads=0):
+    """Decoder::experts with `threads` pool workers (decode tasks, row-parallel
+    GEMV) and prefill GEMM rows split over `row_threads` (bit-identical; for
+    CPU-baseline timing)."""
+    x = _f32(x)
+    T = x.shape[0]
+    y = np.zeros((T, w.hidden), np.float32)
+    st, keep = _layer_struct(w)
+    status = lib().orc_moe_experts_threads(ctypes.byref(st), _ptr(x), T, _ptr(y), int(threads),
+                                           int(row_threads))
+    del keep
+    _check(status, "experts")
+    return y
 
 
 def moe_block(w: MoeWeights, norm_weight, eps, x, threads=1, row_threads=0):

@@ -591,6 +591,12 @@ int orc_moe_experts(const orc_moe_layer* layer, const float* x, size_t T, float*
   return experts_ctx(&cpu, layer, x, T, y, trace);
 }
 
+int orc_moe_experts_threads(const orc_moe_layer* layer, const float* x, size_t T, float* y,
+                            int threads, int row_threads) {
+  orc_ctx cpu = {threads > 0 ? threads : 1, 0, row_threads};
+  return experts_ctx(&cpu, layer, x, T, y, NULL);
+}
+
 static int moe_block_ctx(const orc_ctx* cpu, const orc_moe_layer* layer,
                          const float* norm_weight, float eps, const float* x, size_t T, float* y) {
   if (!layer) return ORC_SHAPE;

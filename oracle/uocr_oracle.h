@@ -121,6 +121,13 @@ typedef struct orc_moe_trace {
  * CpuContext budget in bytes (src/cpu/mod.rs:73-78); 0 means unlimited. */
 int orc_moe_experts(const orc_moe_layer* layer, const float* x, size_t T, float* y, int threads,
                     size_t scratch_limit, orc_moe_trace* trace);
+/* Decoder::experts with `threads` workers for what the reference runs on its
+ * pool (decode tasks at T == 1, row-parallel GEMV rows above 128 K weight
+ * elements) and, when row_threads > 1, the rows of every multi-row scalar
+ * GEMM split over row_threads threads (not a reference feature; bit-identical
+ * results). Used only to time CPU baselines. */
+int orc_moe_experts_threads(const orc_moe_layer* layer, const float* x, size_t T, float* y,
+                            int threads, int row_threads);
 
 /* Post-attention half of Decoder::layer (src/decoder/mod.rs:351-363):
  * y = x + experts(rms_norm(x, norm_weight, eps)). */

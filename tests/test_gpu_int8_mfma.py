@@ -65,7 +65,7 @@ def w8a8_rows(ow, x):
     return np.concatenate([orc.moe_experts(ow, x[t:t + 1]) for t in range(x.shape[0])])
 
 
-@pytest.mark.parametrize("T", [2, 17, 64, 300])
+@pytest.mark.parametrize("T", [2, 17, 64, 300, 512])
 def test_int8_mode_block_sums_and_outputs(setup, T):
     ctx, layer, wo, ow, q = setup
     x = syn.activations(T, H, seed=1100 + T)

@@ -15,6 +15,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 import oracle as orc  # noqa: E402
+import routing_check as rc  # noqa: E402
 import uocr_moe as um  # noqa: E402
 from uocr_moe import synthetic as syn  # noqa: E402
 
@@ -91,18 +92,9 @@ class Case:
 
 
 def tie_tokens(ref_tr, gpu_tr, K):
-    """Tokens whose selected set differs; asserts each is a tie within 1e-6."""
-    bad = []
-    for t in range(ref_tr.topk_ids.shape[0]):
-        a, b = set(ref_tr.topk_ids[t].tolist()), set(gpu_tr["topk_ids"][t].tolist())
-        if a == b:
-            continue
-        lg = ref_tr.logits[t]
-        kth = np.sort(lg)[::-1][K - 1]
-        for e in a ^ b:
-            assert abs(float(lg[e]) - float(kth)) <= TIE, (t, e, lg[e], kth)
-        bad.append(t)
-    return bad
+    """Tokens whose selected set differs; raises unless each is a tie within
+    1e-6 of the oracle's k-th logit."""
+    return rc.tie_tokens(ref_tr.topk_ids, ref_tr.logits, gpu_tr["topk_ids"], K, tie=TIE)
 
 
 def normwise(a, b):
@@ -131,9 +123,9 @@ def check_layer(case, ctx, x, tol=FP32_TOL, flags=0):
     np.testing.assert_allclose(tr["topk_weights"][keep], rtr.topk_weights[keep], rtol=2e-5,
                                atol=1e-7)
     assert np.array_equal(tr["topk_ids"][keep], rtr.topk_ids[keep])
-    if not ties:
-        assert np.array_equal(tr["expert_offsets"], rtr.expert_offsets)
-        assert np.array_equal(tr["perm_rows"], rtr.perm_rows)
+    # The dispatch is checked whatever the ties: exactly the stable order of
+    # the GPU's own ids, and the oracle's on every token outside the ties.
+    rc.check_dispatch(tr, rtr, ties, case.shape["experts"])
     assert np.all(np.isfinite(y))
     err = normwise(y[keep], ref[keep])
     say(f"  T={x.shape[0]} ties={len(ties)} normwise={err:.3e}")
@@ -355,6 +347,41 @@ def test_full_dynamic(ctx, full_dynamic, T):
     check_layer(full_dynamic, ctx, syn.activations(T, 1280, seed=300 + T))
 
 
+@pytest.fixture(scope="module")
+def raw_bf16(ctx):
+    # The shipped model's routing mode: norm_topk_prob = false
+    # (src/model/config.rs:52, tests/config.rs:9), routed_scaling_factor 1.
+    return Case(ctx, FULL, 6, seed=61, normalize=False, scale=1.0)
+
+
+@pytest.fixture(scope="module")
+def raw_int8(ctx):
+    return Case(ctx, FULL, 6, seed=62, quant=orc.QUANT_WEIGHTS_ONLY, normalize=False, scale=1.0)
+
+
+@pytest.fixture(scope="module")
+def raw_dynamic(ctx):
+    return Case(ctx, FULL, 6, seed=63, quant=orc.QUANT_DYNAMIC, normalize=False, scale=1.0)
+
+
+@pytest.mark.parametrize("kind,T,flags", [
+    ("bf16", 1, 0), ("bf16", 8, 0), ("bf16", 64, 0), ("bf16", 1024, 0),
+    ("bf16", 64, um.FLAG_BF16_ACTIVATIONS), ("bf16", 8, um.FLAG_FORCE_MFMA),
+    ("int8", 1, 0), ("int8", 16, 0), ("int8", 512, 0),
+    ("w8a8", 1, 0), ("w8a8", 12, 0), ("w8a8", 200, 0)],
+    ids=lambda v: str(v))
+def test_full_shape_unnormalised_routing(ctx, raw_bf16, raw_int8, raw_dynamic, kind, T, flags):
+    """The unnormalised branch of moe::route (src/decoder/moe.rs:20-28:
+    weights are the softmax probabilities times the scale, not renormalised
+    over the chosen k) at the model shape on every engine: one-token, small
+    batch, MFMA (FP32 class and BF16 activations), INT8 weight-only and
+    W8A8 with single-row groups beside the MFMA GEMMs."""
+    case = {"bf16": raw_bf16, "int8": raw_int8, "w8a8": raw_dynamic}[kind]
+    tol = BF16_TOL if flags & um.FLAG_BF16_ACTIVATIONS else FP32_TOL
+    say(f"normalize=False {kind} T={T} flags={flags}")
+    check_layer(case, ctx, syn.activations(T, 1280, seed=1400 + T), tol=tol, flags=flags)
+
+
 @pytest.mark.parametrize("kind", ["bf16", "int8", "w8a8"])
 def test_decode_many_tokens(ctx, full_bf16, full_int8, full_dynamic, kind):
     """32 consecutive one-token forwards of different tokens at the model
@@ -509,6 +536,37 @@ def _w8a8_trace(T, K, E):
             "shared_hidden": z(S, dt=torch.float32)}
 
 
+def _check_single_groups(qd, x, offs, prow, g):
+    """Every single-row group's W8A8 trace entries against the oracle's
+    Int8Matrix::linear_dynamic_int8 (src/cpu/quantized.rs:190-198): gate/up
+    block sums on the layer input row and down block sums on the GPU's own
+    FP32 hidden row bit for bit (the oracle quantises that row again, so the
+    quantisation is pinned as well), the hidden row within 1e-5 (FP32 sums
+    of exact products in another order); the hidden rows of multi-row
+    groups' positions untouched (-7). Returns the single-row expert ids."""
+    Id = FULL["inter"]
+    singles = []
+    for e in range(FULL["experts"]):
+        p0, p1 = offs[e], offs[e + 1]
+        if p1 - p0 != 1:
+            assert np.all(g["hidden"][p0:p1] == -7), (e, "multi-row position written")
+            continue
+        singles.append(e)
+        p = p0
+        xr = x[prow[p]].reshape(1, -1)
+        _, gs = orc.int8_linear_dynamic(qd["gate"][0][e], qd["gate"][1][e], xr, with_block_sums=True)
+        _, us = orc.int8_linear_dynamic(qd["up"][0][e], qd["up"][1][e], xr, with_block_sums=True)
+        assert np.array_equal(g["gateup_sums"][p, :Id], gs), (e, "gate")
+        assert np.array_equal(g["gateup_sums"][p, Id:], us), (e, "up")
+        h = g["hidden"][p].reshape(1, -1)
+        _, ds = orc.int8_linear_dynamic(qd["down"][0][e], qd["down"][1][e], h, with_block_sums=True)
+        assert np.array_equal(g["down_sums"][p], ds), (e, "down")
+        gy = orc.int8_linear_dynamic(qd["gate"][0][e], qd["gate"][1][e], xr)
+        uy = orc.int8_linear_dynamic(qd["up"][0][e], qd["up"][1][e], xr)
+        assert normwise(h, orc.silu(gy) * uy) < 1e-5, e
+    return singles
+
+
 @pytest.mark.parametrize("T,flags", [(1, 0), (8, 0), (17, 0), (1, um.FLAG_FORCE_GEMV)],
                          ids=["decode", "small-batch", "mfma-singles", "forced-small-batch"])
 def test_w8a8_block_sums_bit_exact_in_layer(ctx, full_dynamic, T, flags):
@@ -534,24 +592,9 @@ def test_w8a8_block_sums_bit_exact_in_layer(ctx, full_dynamic, T, flags):
     g = {k: v.cpu().numpy() for k, v in q8.items()}
     qd = full_dynamic.orc.q
     Id = FULL["inter"]
-    singles = [e for e in range(FULL["experts"]) if offs[e + 1] - offs[e] == 1]
+    singles = _check_single_groups(qd, x, offs, prow, g)
     say(f"  W8A8 trace T={T} flags={flags}: {len(singles)} single-row groups")
     assert singles
-    for e in singles:
-        p = offs[e]
-        xr = x[prow[p]].reshape(1, -1)
-        _, gs = orc.int8_linear_dynamic(qd["gate"][0][e], qd["gate"][1][e], xr, with_block_sums=True)
-        _, us = orc.int8_linear_dynamic(qd["up"][0][e], qd["up"][1][e], xr, with_block_sums=True)
-        assert np.array_equal(g["gateup_sums"][p, :Id], gs), (e, "gate")
-        assert np.array_equal(g["gateup_sums"][p, Id:], us), (e, "up")
-        h = g["hidden"][p].reshape(1, -1)
-        _, ds = orc.int8_linear_dynamic(qd["down"][0][e], qd["down"][1][e], h, with_block_sums=True)
-        assert np.array_equal(g["down_sums"][p], ds), (e, "down")
-        # The hidden row itself: FP32 sums of exact products, another order.
-        gy = orc.int8_linear_dynamic(qd["gate"][0][e], qd["gate"][1][e], xr)
-        uy = orc.int8_linear_dynamic(qd["up"][0][e], qd["up"][1][e], xr)
-        want = orc.silu(gy) * uy
-        assert normwise(h, want) < 1e-5
     if T == 1:
         xr = x.reshape(1, -1)
         S = Id * FULL["shared"]
@@ -564,6 +607,53 @@ def test_w8a8_block_sums_bit_exact_in_layer(ctx, full_dynamic, T, flags):
         assert np.array_equal(g["shared_down_sums"], ds)
     else:
         assert np.all(g["shared_gateup_sums"] == -7)  # untouched: the shared group has T rows
+
+
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_w8a8_singles_beside_forced_mfma_exact_scratch(full_dynamic, T):
+    """The MFMA engine forced on 1-3 tokens of a DynamicActivations layer:
+    every group has one row, so the small-batch engine's single-row pass
+    runs every routed expert beside the MFMA kernels. Token t is built to
+    select experts 58 - 6t .. 63 - 6t (ids far above 16 T), on a context
+    whose scratch budget is exactly uocr_moe_scratch_bytes(cfg, T): the
+    pass keeps its hidden rows by dispatched position inside that budget.
+    Outputs against the oracle and the W8A8 trace bit for bit."""
+    K, E, Hd = full_dynamic.top_k, FULL["experts"], FULL["hidden"]
+    cfg = um.config(Hd, FULL["inter"], E, FULL["shared"], K, normalize=True)
+    want = [list(range(58 - 6 * t, 64 - 6 * t)) for t in range(T)]
+    r = syn.bf16_bits_to_f32(full_dynamic.w["router"]).astype(np.float64)
+    noise = np.random.default_rng(31 + T).standard_normal((T, Hd)) * 0.05
+    x = np.stack([r[w].sum(axis=0) / (r[w] ** 2).sum(axis=1).mean() * 2.0 for w in want])
+    x = (x + noise).astype(np.float32)
+    ref, rtr = oracle_ref(full_dynamic, x)
+    for t in range(T):
+        assert sorted(rtr.topk_ids[t].tolist()) == want[t], (t, rtr.topk_ids[t])
+    exact = um.scratch_bytes(cfg, T)
+    c = um.Context(0, exact)
+    try:
+        q8 = _w8a8_trace(T, K, E)
+        tr = {"expert_offsets": torch.zeros(E + 1, dtype=torch.int32, device="cuda"),
+              "perm_rows": torch.zeros(T * K, dtype=torch.int32, device="cuda"),
+              "topk_ids": torch.zeros((T, K), dtype=torch.int32, device="cuda"),
+              "w8a8": q8}
+        xd = dev(x)
+        yd = torch.full_like(xd, float("nan"))
+        um.forward(c, full_dynamic.layer, xd, yd, flags=um.FLAG_FORCE_MFMA, trace=tr)
+        torch.cuda.synchronize()
+        y = yd.cpu().numpy()
+        assert np.array_equal(tr["topk_ids"].cpu().numpy(), rtr.topk_ids)
+        offs = tr["expert_offsets"].cpu().numpy()
+        assert np.array_equal(offs, rtr.expert_offsets)
+        g = {k: v.cpu().numpy() for k, v in q8.items()}
+        singles = _check_single_groups(full_dynamic.orc.q, x, offs,
+                                       tr["perm_rows"].cpu().numpy(), g)
+        assert sorted(singles) == sorted(sum(want, []))
+        err = normwise(y, ref)
+        say(f"  forced MFMA W8A8 T={T}, scratch {exact} B: normwise {err:.3e}, "
+            f"experts {min(singles)}..{max(singles)}")
+        assert err <= FP32_TOL, err
+    finally:
+        c.close()
 
 
 def test_deterministic_and_row_independent(ctx, full_bf16):
@@ -668,9 +758,10 @@ def test_one_stream_matches_two_streams(ctx, full_bf16, full_int8, full_dynamic,
     """Up to 2048 tokens the shared expert's GEMMs run on a second stream
     after a split of the input into bf16 planes; on one stream (phase
     timing on) the router writes those planes itself. Under
-    DynamicActivations the single-row pass follows the shared expert's
-    GEMMs on the second stream (24 tokens leave 15 groups of one row). Same
-    bits either way, in both activation classes."""
+    DynamicActivations the single-row pass runs on the main stream after
+    the dispatch, before the routed GEMMs, with its hidden rows in its own
+    scratch rows by dispatched position (24 tokens leave 15 groups of one
+    row). Same bits either way, in both activation classes."""
     case = {"bf16": full_bf16, "int8": full_int8, "w8a8": full_dynamic}[kind]
     T = 24 if kind == "w8a8" else 512
     x = syn.activations(T, 1280, seed=811)

@@ -187,3 +187,22 @@ def test_row_parallel_block_is_bit_identical():
     a = orc.moe_block(w, nw, 1e-6, x)
     b = orc.moe_block(w, nw, 1e-6, x, row_threads=4)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 37])
+def test_threaded_experts_are_bit_identical(T):
+    """orc_moe_experts_threads (pool workers plus the prefill row split, the
+    CPU-baseline timing aid) returns the serial experts' bits, for BF16 and
+    for an INT8 overlay in DynamicActivations mode."""
+    w = small_layer(seed=33)
+    x = syn.activations(T, w.hidden, seed=34)
+    a = orc.moe_experts(w, x)
+    b = orc.moe_experts_threads(w, x, threads=4, row_threads=4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    q = syn.int8_overlay(hidden=w.hidden, inter=w.inter, experts=w.n_experts, shared=w.n_shared,
+                         seed=35)
+    w.quant_mode = orc.QUANT_DYNAMIC
+    w.q = q
+    a = orc.moe_experts(w, x)
+    b = orc.moe_experts_threads(w, x, threads=4, row_threads=4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

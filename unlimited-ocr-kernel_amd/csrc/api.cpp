@@ -471,7 +471,12 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
     uocr::MfmaPlanes P{};
     // (Under DynamicActivations the small-batch engine's single-row pass on
     // this stream touches only routed rows' hidden and output buffers.)
-    const bool overlap = mfma && ex.side && L.S > 0 && T <= kOverlapMaxTokens;
+    // Under DynamicActivations one token makes the shared expert a
+    // single-row group as well (src/decoder/mod.rs:103-104): with the MFMA
+    // engine forced at T = 1 it runs as W8A8 on the small-batch engine's
+    // shared units, and the MFMA launches take the routed items only.
+    const bool shared_single = mfma && T == 1 && L.quant_mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS;
+    const bool overlap = mfma && ex.side && L.S > 0 && T <= kOverlapMaxTokens && !shared_single;
     if (mfma) {
       P.x_hi = S.xb;
       P.x_lo = S.xb + T * L.H;
@@ -575,12 +580,14 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
         // 0.162 -> 0.171 ms).
         phase_begin(ctx, kGateUp);
         uocr::launch_singles_gateup(L, S, Ti, st);
+        if (shared_single) uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st, true);
         phase_end(ctx);
         phase_begin(ctx, kDown);
         uocr::launch_singles_down(L, S, Ti, st);
+        if (shared_single) uocr::launch_batch_down(L, S, Ti, tiles_bound, bm, st, true);
         phase_end(ctx);
       }
-      const int lists = overlap ? uocr::kListRouted : uocr::kListAll;
+      const int lists = overlap || shared_single ? uocr::kListRouted : uocr::kListAll;
       phase_begin(ctx, kGateUp);
       uocr::launch_mfma_gateup(L, S, P, Ti, tiles_bound, bf16_only, lists, st);
       phase_end(ctx);
@@ -589,10 +596,11 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       phase_end(ctx);
       if (overlap) HIP_TRY(hipStreamWaitEvent(st, ex.join, 0), "join wait");
     } else {
+      // (The W8A8 trace's hidden rows of single-row groups are written by
+      // the gate/up units themselves.)
       phase_begin(ctx, kGateUp);
       uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);
-      if (int r = trace_hidden(S.h, S.hs)) return r;
       phase_begin(ctx, kDown);
       uocr::launch_batch_down(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);

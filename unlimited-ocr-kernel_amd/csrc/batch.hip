@@ -235,9 +235,10 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
 // and the 4 matching up rows). h = silu(gate) * up (Decoder::feed_forward,
 // src/decoder/mod.rs:114-122).
 // SINGLE: the single-row pass beside the MFMA engine, whose hidden row of
-// group g lives at gu + g I (the MFMA engine's hidden planes take the bytes
-// of h); the W8A8 trace's hidden row is then written here, so the trace's
-// positions of multi-row groups stay untouched.
+// the group at dispatched position p lives at gu + p I (the MFMA engine's
+// hidden planes take the bytes of h; p < T K, so the T K rows of I floats
+// fit gu whatever the expert ids); the W8A8 trace's hidden row is then
+// written here, so the trace's positions of multi-row groups stay untouched.
 template <int KIND, int KH, bool DYN, bool SINGLE = false>
 __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch& S, BatchSmem& sm,
                                             const Unit& u) {
@@ -252,11 +253,15 @@ __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch&
     const int row = u.routed ? S.perm_rows[base + t] : base + t;
     return S.xn + (size_t)row * L.H;
   };
-  float* hout = SINGLE     ? S.gu + (size_t)u.g * L.I
+  float* hout = SINGLE     ? S.gu + (size_t)base * L.I
                 : u.routed ? S.h + (size_t)base * L.I
                            : S.hs + (size_t)base * L.S;
   const int ld = u.routed ? L.I : L.S;
-  float* htrace = SINGLE && S.q8.hidden ? S.q8.hidden + (size_t)base * L.I : nullptr;
+  // The W8A8 trace's hidden row of a single-row group (routed: position
+  // base; the shared expert, a single row only at T = 1: its own row).
+  float* htrace = nullptr;
+  if (DYN && u.group_rows == 1)
+    htrace = !u.routed ? S.q8.s_hidden : S.q8.hidden ? S.q8.hidden + (size_t)base * L.I : nullptr;
   BlockSumOut bs;
   if (DYN && u.group_rows == 1 && k < W) {
     // A single-row group: position `base` (routed) or the one token (shared).
@@ -319,7 +324,7 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   RowPair<KIND, kSegK> P;
   issue_segs(P, w2_of<KIND>(L, u.g), s2_of<KIND>(L, u.g), L.H, W, ra, 0, rb, HALVES ? seg : 0, seg);
   const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
-  const float* hin = SINGLE     ? S.gu + (size_t)u.g * L.I
+  const float* hin = SINGLE     ? S.gu + (size_t)base * L.I
                       : u.routed ? S.h + (size_t)base * L.I
                                  : S.hs + (size_t)base * L.S;
   auto row_of = [&](int t) { return hin + (size_t)t * W; };
@@ -510,9 +515,10 @@ dim3 singles_grid(const DeviceLayer& L, int T, int ur) {
 
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                        int mchunk, hipStream_t s) {
+                        int mchunk, hipStream_t s, bool shared_only) {
   const int nsh = (T + kSharedRows - 1) / kSharedRows;
-  const int units = nsh * ((L.S + 15) / 16) + routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16);
+  const int units = nsh * ((L.S + 15) / 16) +
+                    (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16));
   const dim3 grid(units), block(256);
   if (L.quant_mode == kQuantDynamic) {
     if (L.H <= 1280)
@@ -536,11 +542,11 @@ bool batch_supported(const DeviceLayer& L) {
 }
 
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s) {
+                         int mchunk, hipStream_t s, bool shared_only) {
   if (L.quant_mode == 0)
-    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, s);
+    launch_gateup_kind<kBF16>(L, S, T, tiles_bound, mchunk, s, shared_only);
   else
-    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, s);
+    launch_gateup_kind<kInt8>(L, S, T, tiles_bound, mchunk, s, shared_only);
 }
 
 void launch_singles_gateup(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s) {
@@ -560,10 +566,10 @@ void launch_singles_down(const DeviceLayer& L, const Scratch& S, int T, hipStrea
 }
 
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s) {
+                       hipStream_t s, bool shared_only) {
   const int nsh = (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * down_units(L.H, L.S) +
-                    routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I);
+                    (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
   const dim3 grid(units), block(256);
   if (L.quant_mode == 0)
     batch_down_kernel<kBF16, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);

@@ -148,10 +148,12 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 // math, INT8 weight-only and W8A8), and the small-batch router (T <= 16):
 // logits, then one workgroup that routes and builds the dispatch.
 bool batch_supported(const DeviceLayer& L);
+// shared_only: the shared expert's units only (the MFMA engine at one
+// token under DynamicActivations, where the shared group is a single row).
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
-                         int mchunk, hipStream_t s);
+                         int mchunk, hipStream_t s, bool shared_only = false);
 void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound, int mchunk,
-                       hipStream_t s);
+                       hipStream_t s, bool shared_only = false);
 // The routed groups of exactly one row of an INT8 DynamicActivations layer
 // (W8A8 row by row) beside the MFMA engine, after its dispatch.
 void launch_singles_gateup(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s);
