@@ -354,7 +354,7 @@ def main():
     wanted = [] if args.secondary == "none" else args.secondary.split(",")
 
     # ------------------------------------------------------------- decode
-    def decode_timeline(dl, xs, ys, n):
+    def decode_timeline(dl, xs, ys, n, bf16):
         """n one-token forwards queued back to back (as in the timed loop),
         each with its own timeline buffer; per role and stamp, the median
         over forwards of the median over the role's workgroups of the stamp's
@@ -369,12 +369,20 @@ def main():
                        trace={"decode_stamps": st[i]}, sync=False)
         sync()
         a = st.cpu().numpy()
-        names = {"logit": ("start", "logits stored", "stores complete", "counted in"),
-                 "shared": ("start", None, None, "rows dotted", "counted in"),
-                 "routed": ("start", "input staged", "experts selected", "rows dotted",
-                            "counted in"),
-                 "down": ("start", "experts selected", None, "hidden values ready",
-                          "rows dotted", "output written")}
+        if bf16:  # row-dot engine: down workgroups wait for the hidden rows
+            names = {"logit": ("start", "logits stored", "stores complete", "counted in"),
+                     "shared": ("start", None, None, "rows dotted", "counted in"),
+                     "routed": ("start", "input staged", "experts selected", "rows dotted",
+                                "counted in"),
+                     "output": ("start", "experts selected", None, "hidden values ready",
+                                "rows dotted", "output written")}
+        else:  # split-K engine: combine workgroups read the down partials
+            names = {"logit": ("start", "logits stored", "stores complete", "counted in"),
+                     "shared": ("start", None, None, "rows dotted", "partials stored"),
+                     "routed": ("start", "input staged", "experts selected", "rows dotted",
+                                "partials stored"),
+                     "output": ("start", "experts selected", "probe partial in",
+                                "partials read", "partials summed", "output written")}
         out, spans, r0 = {}, [], 0
         t0 = a[:, :, 0].min(axis=1)
         for f in range(n):
@@ -449,7 +457,7 @@ def main():
         gpu_ms = sum(v[1] for v in ph.values()) / steps
         timeline = None
         if T == 1 and args.decode_timeline > 0:
-            timeline = decode_timeline(dl, xs, ys, args.decode_timeline)
+            timeline = decode_timeline(dl, xs, ys, args.decode_timeline, quant == um.QUANT_NONE)
         for l in dl:
             l.close()
         torch.cuda.empty_cache()

@@ -153,11 +153,15 @@ typedef struct uocr_w8a8_trace {
  * I * n_shared_experts). Rows in launch order and their stamps:
  *   ceil(E/8) router-logit workgroups: 0 start, 1 logits stored, 2 stores
  *     complete, 3 counted in;
- *   S/32 shared gate/up workgroups: 0 start, 3 rows dotted, 4 counted in;
+ *   S/32 shared gate/up workgroups: 0 start, 3 rows dotted, 4 counted in
+ *     (BF16 layers) or down partials stored (INT8 overlays);
  *   k*I/32 routed gate/up workgroups: 0 start, 1 input staged, 2 experts
- *     selected, 3 rows dotted, 4 counted in;
- *   H/8 down workgroups: 0 start, 1 experts selected, 3 every hidden value
- *     ready, 4 rows dotted, 5 output written.
+ *     selected, 3 rows dotted, 4 as the shared ones;
+ *   H/8 output workgroups. BF16 layers (down workgroups): 0 start, 1
+ *     experts selected, 3 every hidden value ready, 4 rows dotted, 5 output
+ *     written. INT8 overlays (combine workgroups, which read the gate/up
+ *     workgroups' down partials): 0 start, 1 experts selected, 2 probe
+ *     partial in, 3 every partial read, 4 partials summed, 5 output written.
  * Other stamps are left untouched. Other engines ignore the member. */
 #define UOCR_DECODE_STAMPS 8
 #define UOCR_DECODE_STAMP_ROWS(E, S, k, I, H) \
@@ -265,10 +269,11 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * scratch is a static device array of UOCR_STATIC_SCRATCH_BYTES per GPU
  * (held until the process ends) instead of a context's reservation, and it
  * calls no allocating routine. Its first UOCR_STATIC_RESERVED_BYTES hold
- * the device flag and the one-token engine's synchronisation words;
+ * the device flag and the one-token engine's synchronisation words and
+ * down partials (a fill kernel, not a memset, resets them at every call);
  * forwards whose uocr_moe_scratch_bytes exceeds UOCR_STATIC_SCRATCH_BYTES -
  * UOCR_STATIC_RESERVED_BYTES fail with Resource (at the model shape: up to
- * 115 tokens). Every call on one GPU shares that GPU's
+ * 126 tokens). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU race, so serialise them (one
  * stream, or events). Enqueued on `stream` (a hipStream_t; NULL: the null
  * stream) and returns once queued. Device-side errors (non-finite
@@ -276,8 +281,8 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * whose workgroups did not all run: Resource) are written as a status code
  * to *device_status (a device int32 the call first clears; NULL: an
  * internal flag nobody reads). No trace, no phase timers. */
-#define UOCR_STATIC_SCRATCH_BYTES (16u << 20)
-#define UOCR_STATIC_RESERVED_BYTES (256u + (64u << 10))
+#define UOCR_STATIC_SCRATCH_BYTES (20u << 20)
+#define UOCR_STATIC_RESERVED_BYTES (256u + (64u << 10) + (5u << 19))
 int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t T, float* y,
                             uint32_t flags, int32_t* device_status, void* stream);
 /* The post-attention half of Decoder::layer (src/decoder/mod.rs:351-363)

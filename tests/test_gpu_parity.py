@@ -458,11 +458,11 @@ def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
 
 def test_decode_wait_bound(ctx, full_int8):
     """The one-token engine's cross-workgroup waits are bounded. With the
-    bound at 0 polls, the down workgroups' wait for the hidden rows cannot
-    be satisfied at its first poll (those rows come microseconds later):
-    the forward reports Resource and the launch still ends. The words it
-    leaves set are cleared with the error, so the same context at the
-    default bound gives the right result again, twice in a row."""
+    bound at 0 polls, the combine workgroups' waits for the logits and for
+    the down partials cannot all be satisfied at their first poll: the
+    forward reports Resource and the launch still ends. The words and
+    partials it leaves set are reset with the error, so the same context
+    at the default bound gives the right result again, twice in a row."""
     case = full_int8
     x = syn.activations(1, 1280, seed=9100)
     ref, _ = oracle_ref(case, x)
@@ -484,8 +484,10 @@ def test_decode_wait_bound(ctx, full_int8):
 
 # Stamps each role of the one-token engine writes, in the order it passes
 # them (uocr_moe_trace::decode_stamps).
-DECODE_STAMPS_SET = {"logit": (0, 1, 2, 3), "shared": (0, 3, 4), "routed": (0, 1, 2, 3, 4),
-                     "down": (0, 1, 3, 4, 5)}
+DECODE_STAMPS_SET = {"logit": (0, 1, 2, 3), "shared": (0, 3, 4), "routed": (0, 1, 2, 3, 4)}
+# The output workgroups: down workgroups (BF16 layers), combine workgroups
+# (INT8 overlays).
+DECODE_OUTPUT_STAMPS = {"bf16": (0, 1, 3, 4, 5), "int8": (0, 1, 2, 3, 4, 5)}
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
@@ -498,7 +500,7 @@ def test_decode_timeline_stamps(ctx, full_bf16, full_int8, kind):
     case = {"bf16": full_bf16, "int8": full_int8}[kind]
     rows = um.decode_stamp_rows(FULL["hidden"], FULL["inter"], FULL["experts"], FULL["shared"],
                                 case.top_k)
-    assert rows == {"logit": 8, "shared": 56, "routed": 168, "down": 160}
+    assert rows == {"logit": 8, "shared": 56, "routed": 168, "output": 160}
     n = sum(rows.values())
     x = syn.activations(1, 1280, seed=9300)
     xd = dev(x)
@@ -513,7 +515,7 @@ def test_decode_timeline_stamps(ctx, full_bf16, full_int8, kind):
     r0 = 0
     for role in um.DECODE_ROLES:
         blk = a[r0:r0 + rows[role]]
-        idx = DECODE_STAMPS_SET[role]
+        idx = DECODE_STAMPS_SET[role] if role != "output" else DECODE_OUTPUT_STAMPS[kind]
         unset = [j for j in range(um.DECODE_STAMPS) if j not in idx]
         assert (blk[:, list(idx)] > 0).all(), role
         assert (blk[:, unset] == -1).all(), role

@@ -72,9 +72,11 @@ static const char* const kPhaseNames[kPhases] = {"router", "topk",    "dispatch"
 
 // The context's flag allocation: the device error flag at byte 0, the
 // decode engine's cross-workgroup words (zeroed once, zero again after
-// every launch) from byte kSyncOffset.
+// every launch) from byte kSyncOffset, then its down partials (all bits
+// set once, and again after every launch) from byte kPartOffset.
 constexpr size_t kSyncOffset = 256;
-constexpr size_t kFlagBytes = kSyncOffset + uocr::kDecodeSyncBytes;
+constexpr size_t kPartOffset = kSyncOffset + uocr::kDecodeSyncBytes;
+constexpr size_t kFlagBytes = kPartOffset + uocr::kDecodePartBytes;
 
 struct uocr_gpu_ctx {
   int device = 0;
@@ -223,12 +225,14 @@ struct Exec {
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   int* sync = nullptr;  // the decode engine's cross-workgroup words (zero between launches)
+  float* part = nullptr;  // the decode engine's down partials (all bits set between launches)
   int wait_limit = -1;  // the decode engine's wait bound in polls (< 0: its default)
 };
 
 Exec exec_of(uocr_gpu_ctx* ctx) {
   Exec ex{ctx->scratch, ctx->scratch_limit, ctx->stream, ctx->err, ctx};
   ex.sync = reinterpret_cast<int*>(reinterpret_cast<char*>(ctx->err) + kSyncOffset);
+  ex.part = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->err) + kPartOffset);
   ex.wait_limit = ctx->wait_limit;
   if (ctx->timing_mask == 0) {
     ex.side = ctx->side;
@@ -263,6 +267,7 @@ Scratch carve(const Exec& ex, const ScratchPlan& p) {
   s.router_part = reinterpret_cast<float*>(b + p.router_part);
   s.err = ex.err;
   s.sync = ex.sync;
+  s.part = ex.part;
   s.wait_limit = ex.wait_limit;
   return s;
 }
@@ -339,9 +344,12 @@ int read_and_clear_error(uocr_gpu_ctx* ctx) {
   HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
   int e = *ctx->err_host;
   if (e != 0) {
-    // The decode engine's words too: a wait that gave up (Resource) can
-    // leave a flag that its producer set later.
-    HIP_TRY(hipMemsetAsync(ctx->err, 0, kFlagBytes, ctx->stream), "clear device error flag");
+    // The decode engine's words and partials too: a wait that gave up
+    // (Resource) can leave a flag or a partial that its producer set later.
+    HIP_TRY(hipMemsetAsync(ctx->err, 0, kPartOffset, ctx->stream), "clear device error flag");
+    HIP_TRY(hipMemsetAsync(reinterpret_cast<char*>(ctx->err) + kPartOffset, 0xff,
+                           uocr::kDecodePartBytes, ctx->stream),
+            "reset the decode partials");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "synchronize");
     return fail(e, e == UOCR_ERR_NUMERICAL  ? "nonfinite numerical input on device"
                    : e == UOCR_ERR_RESOURCE ? "a one-token launch's cross-workgroup wait reached its bound"
@@ -452,7 +460,8 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
     return fail(UOCR_ERR_RESOURCE, "token count too large for one forward (%zu)", T);
   if (engine == Engine::Decode) {
     // One token: one launch, its workgroups ordered by the words at S.sync.
-    if (!S.sync) return fail(UOCR_ERR_UNSUPPORTED, "decode engine without its sync words");
+    if (!S.sync || !S.part)
+      return fail(UOCR_ERR_UNSUPPORTED, "decode engine without its sync words");
     phase_begin(ctx, kDecode);
     uocr::launch_decode(L, S, residual, y, st);
     phase_end(ctx);
@@ -646,13 +655,18 @@ static_assert(kStaticFlagBytes == UOCR_STATIC_RESERVED_BYTES, "static reservatio
 std::mutex g_static_mu;
 char* g_static_base[kMaxStaticDevices] = {};
 
-// Clears the error flag and the decode engine's words at the start of each
-// static forward (256 threads, 16 bytes each per pass).
-__global__ void clear_flag_kernel(int* flag, int* sync) {
-  if (threadIdx.x == 0) *flag = 0;
+// Clears the error flag and the decode engine's words, and sets every bit
+// of its partials, at the start of each static forward (16 bytes per
+// thread and pass over the grid).
+__global__ void clear_flag_kernel(int* flag, int* sync, float* part) {
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  if (tid == 0) *flag = 0;
   uint4* w = reinterpret_cast<uint4*>(sync);
-  for (size_t i = threadIdx.x; i < uocr::kDecodeSyncBytes / 16; i += blockDim.x)
-    w[i] = make_uint4(0, 0, 0, 0);
+  for (size_t i = tid; i < uocr::kDecodeSyncBytes / 16; i += stride) w[i] = make_uint4(0, 0, 0, 0);
+  uint4* p = reinterpret_cast<uint4*>(part);
+  const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u);
+  for (size_t i = tid; i < uocr::kDecodePartBytes / 16; i += stride) p[i] = ones;
 }
 
 // The device address of this device's array (the device must be current).
@@ -698,7 +712,9 @@ int uocr_gpu_ctx_create(int device, size_t scratch_limit, uocr_gpu_ctx** out) {
   if (e == hipSuccess) e = hipMalloc(&ctx->scratch, scratch_limit);
   if (e == hipSuccess) e = hipMalloc(&ctx->err, kFlagBytes);
   if (e == hipSuccess) e = hipHostMalloc(&ctx->err_host, sizeof(int));
-  if (e == hipSuccess) e = hipMemset(ctx->err, 0, kFlagBytes);
+  if (e == hipSuccess) e = hipMemset(ctx->err, 0, kPartOffset);
+  if (e == hipSuccess)
+    e = hipMemset(reinterpret_cast<char*>(ctx->err) + kPartOffset, 0xff, uocr::kDecodePartBytes);
   if (e != hipSuccess) {
     uocr_gpu_ctx_destroy(ctx);
     return hip_fail(e, "context allocation");
@@ -900,7 +916,8 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   DeviceLayer& L = layer->dev;
   const size_t H = L.H, I = L.I, S = L.S, E = L.E;
   const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
-  void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr, *q13k = nullptr, *q2k = nullptr;
+  void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr, *q13k = nullptr, *q2k = nullptr,
+       *s2k = nullptr;
   std::vector<void*> fresh;
   auto alloc = [&](size_t bytes, void** p) -> hipError_t {
     hipError_t e = hipMalloc(p, bytes);
@@ -917,6 +934,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2);
   if (e == hipSuccess) e = alloc(n13, &q13k);
   if (e == hipSuccess) e = alloc(n2, &q2k);
+  if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2k);
   if (e != hipSuccess) return release(hip_fail(e, "INT8 allocation"));
   const hipMemcpyKind kind = kind_of(where);
   hipStream_t st = ctx->stream;
@@ -953,6 +971,12 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   uocr::launch_panelize(q2, q2k, 1, (int)H, (int)I, (int)E, st);
   uocr::launch_panelize(static_cast<char*>(q2) + E * H * I, static_cast<char*>(q2k) + E * H * I, 1,
                         (int)H, (int)S, 1, st);
+  // The one-token engine's block-major down scales.
+  uocr::launch_transpose_f32(static_cast<const float*>(s2), static_cast<float*>(s2k), (int)H,
+                             (int)(I / 32), (int)E, st);
+  uocr::launch_transpose_f32(static_cast<const float*>(s2) + E * H * (I / 32),
+                             static_cast<float*>(s2k) + E * H * (I / 32), (int)H, (int)(S / 32), 1,
+                             st);
   // Validate the uploaded values on the device.
   HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), st), "clear flag");
   hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q13, n13,
@@ -965,7 +989,8 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
                                                  : "INT8 scales must be finite and nonnegative"));
   }
   // Replace any previous overlay.
-  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2, (void*)L.q13k, (void*)L.q2k}) {
+  for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2, (void*)L.q13k, (void*)L.q2k,
+                  (void*)L.s2k}) {
     if (!p) continue;
     for (auto it = layer->allocations.begin(); it != layer->allocations.end(); ++it)
       if (*it == p) {
@@ -975,13 +1000,14 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     (void)hipFree(p);
   }
   for (void* p : fresh) layer->allocations.push_back(p);
-  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + n2 / 32 * 4;
+  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + 2 * (n2 / 32 * 4);
   L.q13 = static_cast<const int8_t*>(q13);
   L.s13 = static_cast<const float*>(s13);
   L.q2 = static_cast<const int8_t*>(q2);
   L.s2 = static_cast<const float*>(s2);
   L.q13k = static_cast<const int8_t*>(q13k);
   L.q2k = static_cast<const int8_t*>(q2k);
+  L.s2k = static_cast<const float*>(s2k);
   L.quant_mode = mode;
   layer->quant_mode = mode;
   return UOCR_OK;
@@ -1053,9 +1079,12 @@ int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t 
   int* err = device_status ? reinterpret_cast<int*>(device_status) : reinterpret_cast<int*>(base);
   // A fill kernel, not a memset, so that graph capture records a kernel node.
   int* sync = reinterpret_cast<int*>(base + kSyncOffset);
-  hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(256), 0, st, err, sync);
+  float* part = reinterpret_cast<float*>(base + kPartOffset);
+  hipLaunchKernelGGL(clear_flag_kernel, dim3(uocr::kDecodePartBytes / 16 / 256), dim3(256), 0, st,
+                     err, sync, part);
   Exec ex{base + kStaticFlagBytes, have, st, err, nullptr};
   ex.sync = sync;
+  ex.part = part;
   return enqueue_experts(ex, layer, x, T, nullptr, y, flags, nullptr, false);
 }
 

@@ -849,6 +849,25 @@ __global__ __launch_bounds__(256) void panelize_kernel(const uint4* __restrict__
   out[i] = in[m * per_matrix + n * (size_t)(K / 32) * cpb + kb * cpb + c];
 }
 
+__global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ in,
+                                                            float* __restrict__ out, int rows,
+                                                            int cols, size_t total) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const size_t per = (size_t)rows * cols;
+  const size_t m = i / per, rest = i % per;
+  const size_t r = rest / cols, c = rest % cols;
+  out[m * per + c * rows + r] = in[i];
+}
+
+void launch_transpose_f32(const float* in, float* out, int rows, int cols, int groups,
+                          hipStream_t s) {
+  if (rows <= 0 || cols <= 0 || groups <= 0) return;
+  const size_t total = (size_t)groups * rows * cols;
+  hipLaunchKernelGGL(transpose_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     in, out, rows, cols, total);
+}
+
 void launch_panelize(const void* in, void* out, int elem_bytes, int N, int K, int groups,
                      hipStream_t s) {
   if (N <= 0 || K <= 0 || groups <= 0) return;

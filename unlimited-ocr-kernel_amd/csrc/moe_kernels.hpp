@@ -38,6 +38,10 @@ struct DeviceLayer {
   const uint16_t* w2k;
   const int8_t* q13k;
   const int8_t* q2k;
+  // The one-token engine's copy of s2 block-major: each group's [H, W/32]
+  // scales as [W/32][H] (same group offsets), so one 32-block's scales of
+  // every output feature are one contiguous run.
+  const float* s2k;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
   __host__ __device__ size_t n13() const { return ((size_t)E * 2 * I + 2 * (size_t)S) * H; }
@@ -91,6 +95,7 @@ struct Scratch {
   float* q8s;       // int8 mode: their block scales [T*H/32 + (T*K*I + T*S)/32]
   int* err;         // device error flag
   int* sync;        // kDecodeSyncBytes: the decode engine's counts and flags (zero between launches)
+  float* part;      // kDecodePartBytes: the decode engine's down partials (0xffffffff between launches)
   int wait_limit;   // the decode engine's wait bound in polls (< 0: its default)
   Q8Trace q8;       // W8A8 trace (tests), all null by default
   // The decode engine's timeline: kDecodeStamps real-time stamps per
@@ -195,6 +200,10 @@ constexpr int kMfmaQ8BM = 64;  // INT8 weights: 64-row tiles, 64 x 512 items
 void mfma_init_attributes();
 // out = `groups` row-major [N, K] matrices (elem_bytes 1 or 2, K % 32 == 0,
 // matrix g at g * N * K) as k-blocked panels [K/32][N][32].
+// out = in transposed per matrix: `groups` row-major f32 [rows, cols]
+// matrices to [cols, rows] (the block-major down scales).
+void launch_transpose_f32(const float* in, float* out, int rows, int cols, int groups,
+                          hipStream_t s);
 void launch_panelize(const void* in, void* out, int elem_bytes, int N, int K, int groups,
                      hipStream_t s);
 
@@ -220,19 +229,31 @@ void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, i
 constexpr int kGemvChunk = 16;
 
 // decode.hip: one-token expert engine, one launch (router logits, the
-// shared and the routed gate/up, routed and shared down + ordered combine
-// into out), ordered inside by the kDecodeSyncBytes at S.sync, which must
-// be zero when it starts and are zero again when it ends.
+// shared and the routed gate/up with their shares of the down projection,
+// ordered combine into out), ordered inside by the kDecodeSyncBytes at
+// S.sync, which must be zero when it starts and are zero again when it
+// ends, and handing its down partials over through the kDecodePartBytes at
+// S.part, which must hold 0xffffffff in every byte when it starts and do
+// again when it ends.
 constexpr size_t kDecodeSyncBytes = 64 << 10;
+// Partials: (S/32 + K I/32) per output feature, at most (2048/32 + 8 *
+// 1024/32) x 2048 features, 4 bytes each.
+constexpr size_t kDecodePartBytes = (size_t)(2048 / 32 + 8 * 1024 / 32) * 2048 * 4;
 // The split router's per-chunk counts (<= 128 chunks, one word per 64 bytes)
 // live in the same zero-between-launches region, past the decode engine's
 // words (at most 1 + 16 + 2 * 256 lines).
 constexpr size_t kRouterSyncWord = 10240;
 static_assert((kRouterSyncWord + 128 * 16) * 4 <= kDecodeSyncBytes, "router counts fit");
 static_assert((1 + 16 + 2 * 256) * 16 <= kRouterSyncWord, "after the decode words");
+// By the layer's kind: BF16 layers take the row-dot engine (decode_rows.hip:
+// down rows on workgroups of their own, hidden values handed over through
+// the sync words), INT8 overlays the split-K engine (decode.hip).
 bool decode_supported(const DeviceLayer& L);
 void launch_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
                    hipStream_t s);
+bool rows_decode_supported(const DeviceLayer& L);
+void launch_rows_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                        hipStream_t s);
 
 // combine.hip
 // RMSNorm output of rows: the normalised rows (out, [T, H]) and optionally

@@ -127,14 +127,16 @@ class Trace(ctypes.Structure):
 # DECODE_STAMPS uint64 stamps of the device's 100 MHz real-time counter, one
 # row per workgroup of its launch in this order.
 DECODE_STAMPS = 8
-DECODE_ROLES = ("logit", "shared", "routed", "down")
+# "output": the H/8 workgroups that write the token's output row — down
+# workgroups on BF16 layers, combine workgroups on INT8 overlays.
+DECODE_ROLES = ("logit", "shared", "routed", "output")
 
 
 def decode_stamp_rows(hidden: int, inter: int, experts: int, shared: int, top_k: int) -> dict:
     """Workgroup rows per role of the one-token engine's launch
     (UOCR_DECODE_STAMP_ROWS), in launch order."""
     return {"logit": (experts + 7) // 8, "shared": inter * shared // 32,
-            "routed": top_k * (inter // 32), "down": hidden // 8}
+            "routed": top_k * (inter // 32), "output": hidden // 8}
 
 
 def _load():
@@ -355,8 +357,9 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
               ctypes.byref(tr) if tr is not None else None))
 
 
-STATIC_SCRATCH_BYTES = 16 << 20
-STATIC_RESERVED_BYTES = 256 + (64 << 10)  # the device flag and the decode engine's words
+STATIC_SCRATCH_BYTES = 20 << 20
+# The device flag, the decode engine's words and its down partials.
+STATIC_RESERVED_BYTES = 256 + (64 << 10) + (5 << 19)
 
 
 def forward_static(layer: MoeLayer, x, y, flags: int = 0, status=None, stream=None):
