@@ -14,8 +14,9 @@ against the oracle's 12-layer chain after timing.
 
 Secondary workloads (same JSON line, "secondary"): the same stack with
 BF16-rounded activations (the 2e-2 class), batch-1 decode with the
-INT8 block-32 overlay and with BF16 weights (rotating over 12 distinct layers
-so the 256 MB MALL cannot hold the working set), and the 1024-token prefill
+INT8 block-32 overlay (weight-only and W8A8) and with BF16 weights, and the
+INT8 16-token forward (rotating over 12 distinct layers so the 256 MB MALL
+cannot hold the working set), and the 1024-token prefill
 with Zipf(1.1) expert popularity in both activation precision classes, the
 INT8-overlay layer at 512 tokens with uniform routing (W8A8 under
 DynamicActivations, and weight-only), and
@@ -27,7 +28,7 @@ x86 path) on a bounded sample of the headline workload at 1, 8 and 16
 threads; on the batch-1 decode workloads at 8 and 16 threads (the
 reference's decode tasks); and on the 16-token INT8, the 1024-token Zipf and
 the 512-token INT8 (W8A8 and weight-only) workloads at 1, 8 and 16 threads.
-16 threads are one GPU's share of the host.
+16 threads are every logical CPU of the GPU's host.
 """
 import argparse
 import json
@@ -66,7 +67,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--secondary",
-                    default="decode_int8,decode_bf16,decode_int8_t16,prefill1024,"
+                    default="decode_int8,decode_bf16,decode_w8a8,decode_int8_t16,prefill1024,"
                             "prefill_w8a8_t512,prefill_int8_t512,prefill_w8a8_int8mfma_t512,"
                             "lm_head_bf16,lm_head_int8,lm_head_w8a8",
                     help="comma list of secondary workloads, or 'none'")
@@ -529,6 +530,7 @@ def main():
 
     for key, quant, T in (("decode_int8", um.QUANT_WEIGHTS_ONLY, 1),
                           ("decode_bf16", um.QUANT_NONE, 1),
+                          ("decode_w8a8", um.QUANT_DYNAMIC, 1),
                           ("decode_int8_t16", um.QUANT_WEIGHTS_ONLY, 16)):
         if key in wanted:
             secondary.append(decode(quant, T))

@@ -434,10 +434,12 @@ def test_w8a8_singles_beside_mfma_wide(ctx, shape, K, T, flags):
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
     """48 one-token forwards queued back to back (one synchronisation at the
-    end), each against the oracle. The decode engine's single launch orders
-    its workgroups through counts and flags that every launch must leave
-    at zero: a word left set would let the next launch read logits or
-    hidden values before they are written."""
+    end), each against the oracle. Each one-token engine's single launch
+    orders its workgroups through counts and flags (row-dot engine) or
+    partial slots holding a sentinel until written (split-K engine) that
+    every launch must leave as it found them: a word left set would let the
+    next launch read logits, hidden values or partials before they are
+    written."""
     case = {"bf16": full_bf16, "int8": full_int8}[kind]
     xs = [syn.activations(1, 1280, seed=7000 + i) for i in range(48)]
     xd = [dev(x) for x in xs]
@@ -456,14 +458,17 @@ def test_decode_back_to_back(ctx, full_bf16, full_int8, kind):
     say(f"  {kind}: 48 queued one-token forwards, worst normwise {worst:.3e}")
 
 
-def test_decode_wait_bound(ctx, full_int8):
-    """The one-token engine's cross-workgroup waits are bounded. With the
-    bound at 0 polls, the combine workgroups' waits for the logits and for
-    the down partials cannot all be satisfied at their first poll: the
-    forward reports Resource and the launch still ends. The words and
-    partials it leaves set are reset with the error, so the same context
-    at the default bound gives the right result again, twice in a row."""
-    case = full_int8
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_decode_wait_bound(ctx, full_bf16, full_int8, kind):
+    """The one-token engines' cross-workgroup waits are bounded. With the
+    bound at 0 polls, the waits for the logits and for the hidden values
+    (row-dot engine, BF16) or the down partials (split-K engine, INT8)
+    cannot all be satisfied at their first poll: the forward reports
+    Resource and the launch still ends. The words and partials it leaves
+    set are reset with the error, so the same context at the default bound
+    gives the right result again, twice in a row."""
+    case = {"bf16": full_bf16, "int8": full_int8}[kind]
+    say(f"decode wait bound 0, {kind}")
     x = syn.activations(1, 1280, seed=9100)
     ref, _ = oracle_ref(case, x)
     c2 = um.Context(0, 64 << 20)

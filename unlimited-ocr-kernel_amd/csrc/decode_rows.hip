@@ -513,7 +513,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
 constexpr int kBlockWaves = kUpWaves > kMaxK + 2 ? kUpWaves : kMaxK + 2;
 
 template <int KIND, int KH, bool ST>
-__global__ __launch_bounds__(64 * kBlockWaves) void decode_kernel(DeviceLayer L, Scratch S,
+__global__ __launch_bounds__(64 * kBlockWaves) void rows_decode_kernel(DeviceLayer L, Scratch S,
                                                                   const float* residual, float* out) {
   __shared__ __align__(16) DecodeSmem sm;
   // Wave-uniform (scalar) so the per-wave buffer bases stay scalar.
@@ -541,9 +541,9 @@ void launch_kind(const DeviceLayer& L, const Scratch& S, const float* residual, 
   const DecodeGrid G(L);
   const int waves = L.K + 2 > kUpWaves ? L.K + 2 : kUpWaves;
   if (S.stamps)
-    decode_kernel<KIND, KH, true><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+    rows_decode_kernel<KIND, KH, true><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
   else
-    decode_kernel<KIND, KH, false><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+    rows_decode_kernel<KIND, KH, false><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
 }
 
 }  // namespace
