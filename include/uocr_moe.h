@@ -269,8 +269,8 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * scratch is a static device array of UOCR_STATIC_SCRATCH_BYTES per GPU
  * (held until the process ends) instead of a context's reservation, and it
  * calls no allocating routine. Its first UOCR_STATIC_RESERVED_BYTES hold
- * the device flag and the one-token engine's synchronisation words and
- * down partials (a fill kernel, not a memset, resets them at every call);
+ * the device flag and the one-token engines' synchronisation words, down
+ * partials and logit copies (a fill kernel, not a memset, resets them at every call);
  * forwards whose uocr_moe_scratch_bytes exceeds UOCR_STATIC_SCRATCH_BYTES -
  * UOCR_STATIC_RESERVED_BYTES fail with Resource (at the model shape: up to
  * 126 tokens). Every call on one GPU shares that GPU's
@@ -282,7 +282,7 @@ int uocr_moe_forward(uocr_gpu_ctx* ctx, const uocr_moe_layer* layer, const float
  * to *device_status (a device int32 the call first clears; NULL: an
  * internal flag nobody reads). No trace, no phase timers. */
 #define UOCR_STATIC_SCRATCH_BYTES (20u << 20)
-#define UOCR_STATIC_RESERVED_BYTES (256u + (64u << 10) + (5u << 19))
+#define UOCR_STATIC_RESERVED_BYTES (256u + (64u << 10) + (328u << 13))
 int uocr_moe_forward_static(const uocr_moe_layer* layer, const float* x, size_t T, float* y,
                             uint32_t flags, int32_t* device_status, void* stream);
 /* The post-attention half of Decoder::layer (src/decoder/mod.rs:351-363)

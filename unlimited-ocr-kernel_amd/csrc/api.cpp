@@ -517,8 +517,9 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       HIP_TRY(hipEventRecord(ex.join, ex.side), "join event");
     }
     if (T <= (size_t)uocr::kGemvChunk && !mfma && !int8) {
-      // Few tokens: logits with every token staged once, then one
-      // workgroup routes them and builds the dispatch.
+      // Few tokens: one launch; the last of its logit workgroups routes
+      // every token and builds the dispatch (counted in a word at S.sync).
+      if (!S.sync) return fail(UOCR_ERR_UNSUPPORTED, "small-batch router without its sync word");
       phase_begin(ctx, kRouter);
       uocr::launch_small_route(S.xn, L, S, Ti, st);
       phase_end(ctx);

@@ -4,12 +4,13 @@
 // dots it with the tile's activation rows staged in LDS. The grid is one
 // unit per workgroup, shared-expert units first (they need nothing from
 // the dispatch), then the slices of each routed tile; workgroups are kept
-// small (36 KiB of LDS, <= 128 or 168 VGPRs) so that four or three share a CU and
+// small (19 KiB of LDS, <= 128 or 168 VGPRs) so that several share a CU and
 // their chains of dependent loads overlap. Used for 2 <= T <= 16, and for
 // the single-row W8A8 groups of INT8 layers at any T.
 //
-// Also the fence-free small-batch router (2 <= T <= 16): logits, then one
-// workgroup that routes every token and builds the dispatch.
+// Also the fence-free small-batch router (2 <= T <= 16): one launch whose
+// logit workgroups count themselves in; the last one routes every token
+// and builds the dispatch.
 //
 // Arithmetic: Decoder::projection / feed_forward (src/decoder/mod.rs:
 // 99-122) per row; INT8 weight-only as q * x summed per 16-byte chunk and
@@ -28,7 +29,10 @@ namespace {
 
 constexpr int kTileRows = kGemvChunk;  // tokens per row tile
 constexpr int kDotTok = 4;             // tokens per register batch of the dot
-constexpr int kStage = 9216;           // FP32 activations staged per workgroup (36 KiB)
+// FP32 activations staged per workgroup (16 KiB: three 1280-wide rows per
+// pass). 36 KiB (seven rows) allowed four workgroups per CU; at 16 KiB the
+// VGPRs set the limit, and the 16-token INT8 forward went 76.7 -> 75.3 us.
+constexpr int kStage = 4096;
 constexpr int kWideK = 2048;           // widest reduction dimension (H, S)
 constexpr int kSegK = 1024;            // widest down-projection segment in registers
 // Shared-expert tiles take 8 rows: their units dot every weight with each
@@ -195,7 +199,7 @@ __device__ __forceinline__ void tile_dot(const DeviceLayer& L, const Scratch& S,
       stage_tile(sm, 0, 1, cols, ld, row_of);
       // The zero columns quantise to zero blocks, so every block a segment
       // can reach is defined.
-      if (threadIdx.x < 64) quantize_lds(sm.x, ld, sm.xq, sm.xs, lane, S.err);
+      quantize_lds_waves(sm.x, ld, sm.xq, sm.xs, threadIdx.x >> 6, blockDim.x >> 6, lane, S.err);
       __syncthreads();
       float r0, r1;
       dot_rows_as<kW8A8>(P, K, sm.x, sm.xq, sm.xs, r0, r1, xb_off, sums);
@@ -390,63 +394,33 @@ __attribute__((amdgpu_waves_per_eu(3))) void singles_down_kernel(DeviceLayer L, 
 
 // ------------------------------------------------------------- small router
 
-// Logits for T <= 16 tokens: one wave per (8 router rows, 2 tokens), so
-// the 2·H·E·T flops spread over E/8 · T/2 workgroups; the router rows are
-// read from L2 by every token pair.
+// Routing of T <= 16 tokens in one launch. Workgroup (b, p) dots router
+// rows 8b .. 8b+7 with tokens 2p, 2p+1 on its first wave (so the 2·H·E·T
+// flops spread over E/8 · T/2 workgroups, and the router rows come from L2
+// after the first touch) and stores the logits device-coherently. Once its
+// stores are complete it counts itself in one of 8 sub-counts (workgroup
+// id mod 8); the one completing a sub-count counts that in a top count and
+// zeroes the sub-count; the one completing the top count zeroes it and,
+// with all 16 waves, routes and dispatches every token, reading the logits
+// device-coherently (no word takes more than 8 counts). Wave t routes token
+// t (moe::route, src/decoder/moe.rs:7-30), then the dispatch of
+// Decoder::experts (src/decoder/mod.rs:127-141): per expert, its tokens in
+// ascending order; one row tile per active expert and one for the shared
+// expert.
 constexpr int kRouterTok = 2;
-
-template <int KH>
-__global__ __launch_bounds__(64) void small_router_kernel(const float* __restrict__ x,
-                                                          DeviceLayer L, Scratch S, int T) {
-  __shared__ __align__(16) float xl[kRouterTok * KH];
-  const int lane = threadIdx.x;
-  const int ra = 8 * blockIdx.x + (lane >> 4), rb = ra + 4;
-  const int t0 = kRouterTok * blockIdx.y;
-  const int nt = min(kRouterTok, T - t0);
-  RowPair<kBF16, KH> P;
-  issue_rows(P, L.router, nullptr, L.E, L.H, ra, rb);
-  RowStage<kRouterTok * KH> X;
-  load_row(X, x + (size_t)t0 * L.H, nt * L.H, lane);
-  store_row(X, xl, nt * L.H, lane);
-  __syncthreads();
-  auto run = [&](auto ntc) {
-    constexpr int NT = decltype(ntc)::value;
-    float a0[NT], a1[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
-    dot_rows_multi(P, L.H, xl, 0, L.H, a0, a1);
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const float v0 = row16_sum(a0[t]), v1 = row16_sum(a1[t]);
-      if ((lane & 15) == 0) {
-        if (ra < L.E) S.logits[(size_t)(t0 + t) * L.E + ra] = v0;
-        if (rb < L.E) S.logits[(size_t)(t0 + t) * L.E + rb] = v1;
-      }
-    }
-  };
-  static_assert(kRouterTok == 2, "one case per token count");
-  if (nt == 2)
-    run(std::integral_constant<int, 2>{});
-  else
-    run(std::integral_constant<int, 1>{});
-}
-
-// One workgroup of 16 waves: wave t routes token t (moe::route,
-// src/decoder/moe.rs:7-30), then the dispatch of Decoder::experts
-// (src/decoder/mod.rs:127-141): per expert, its tokens in ascending order;
-// one row tile per active expert and one for the shared expert.
 constexpr int kRouteWaves = 16;
 
-__global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(DeviceLayer L,
-                                                                               Scratch S, int T) {
+__device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scratch& S, int T,
+                                               int wave, int lane) {
   __shared__ unsigned long long masks[kRouteWaves];
   __shared__ int count[64];
   __shared__ int start[65];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = L.E, K = L.K;
   const bool mine = wave < T;
   // Waves past T route a neutral row (their result is not used).
-  const float v = mine && lane < E ? S.logits[(size_t)wave * E + lane] : 0.0f;
+  const float v = mine && lane < E ? __hip_atomic_load(S.logits + (size_t)wave * E + lane,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0.0f;
   const WaveSel r = route_wave_sel(v, E, K);
   const float w = route_weight(r, L.normalize, L.scale);
   if (mine && !r.ok && lane == 0) raise_error(S.err, kErrNumerical);
@@ -498,6 +472,69 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_dispatch_kernel(
       S.counters[1] = n_active;
     }
   }
+}
+
+template <int KH>
+__global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const float* __restrict__ x,
+                                                                       DeviceLayer L, Scratch S,
+                                                                       int T) {
+  __shared__ __align__(16) float xl[kRouterTok * KH];
+  __shared__ int last;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave == 0) {
+    const int ra = 8 * blockIdx.x + (lane >> 4), rb = ra + 4;
+    const int t0 = kRouterTok * blockIdx.y;
+    const int nt = min(kRouterTok, T - t0);
+    RowPair<kBF16, KH> P;
+    issue_rows(P, L.router, nullptr, L.E, L.H, ra, rb);
+    RowStage<kRouterTok * KH> X;
+    load_row(X, x + (size_t)t0 * L.H, nt * L.H, lane);
+    store_row(X, xl, nt * L.H, lane);  // read back by this wave only
+    auto run = [&](auto ntc) {
+      constexpr int NT = decltype(ntc)::value;
+      float a0[NT], a1[NT];
+#pragma unroll
+      for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
+      dot_rows_multi(P, L.H, xl, 0, L.H, a0, a1);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const float v0 = row16_sum(a0[t]), v1 = row16_sum(a1[t]);
+        if ((lane & 15) == 0) {
+          float* row = S.logits + (size_t)(t0 + t) * L.E;
+          if (ra < L.E) __hip_atomic_store(row + ra, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (rb < L.E) __hip_atomic_store(row + rb, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    };
+    static_assert(kRouterTok == 2, "one case per token count");
+    if (nt == 2)
+      run(std::integral_constant<int, 2>{});
+    else
+      run(std::integral_constant<int, 1>{});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logit stores are complete
+    if (lane == 0) {
+      const int n = (int)(gridDim.x * gridDim.y);
+      const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+      const int i = id % 8;
+      int* sub = S.sync + kSmallRouteWord + 16 * i;
+      int* top = S.sync + kSmallRouteWord + 16 * 8;
+      int done = 0;
+      if (__hip_atomic_fetch_add(sub, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          (n - 1 - i) / 8) {
+        __hip_atomic_store(sub, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int n_sub = n < 8 ? n : 8;
+        if (__hip_atomic_fetch_add(top, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            n_sub - 1) {
+          __hip_atomic_store(top, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          done = 1;
+        }
+      }
+      last = done;
+    }
+  }
+  __syncthreads();
+  if (!last) return;
+  route_dispatch(L, S, T, wave, lane);
 }
 
 // Routed tiles a dispatch can list: one per active group when every group
@@ -583,10 +620,9 @@ void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, 
                         hipStream_t s) {
   const dim3 grid((L.E + 7) / 8, (T + kRouterTok - 1) / kRouterTok);
   if (L.H <= 1280)
-    small_router_kernel<1280><<<grid, dim3(64), 0, s>>>(x, L, S, T);
+    small_route_kernel<1280><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T);
   else
-    small_router_kernel<kWideK><<<grid, dim3(64), 0, s>>>(x, L, S, T);
-  small_route_dispatch_kernel<<<dim3(1), dim3(64 * kRouteWaves), 0, s>>>(L, S, T);
+    small_route_kernel<kWideK><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T);
 }
 
 }  // namespace uocr

@@ -55,6 +55,17 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_move<0x140>(v);  // row_mirror
   return v;
 }
+// Largest value over each 32-lane half of the wave: the row maximum as
+// above, then the two rows of a half exchanged by a swizzle (lane ^ 16).
+// Every lane of the wave must be active.
+__device__ __forceinline__ float half_wave_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10.
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f)));
+}
 
 __device__ __forceinline__ void raise_error(int* err, int code) {
   if (err) atomicMax(err, code);

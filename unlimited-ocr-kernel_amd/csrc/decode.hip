@@ -3,13 +3,14 @@
 // the bytes of the active experts' weights and by the latency of the steps
 // that depend on each other (router logits -> selection -> expert rows ->
 // output). One launch, four kinds of workgroup by id:
-//   logit     ceil(E/8) workgroups, one wave each: 8 router logits, which
-//             give the combine workgroups the routing weights
+//   logit     ceil(E/8) workgroups: 8 router logits (one wave), stored
+//             into every routed workgroup's copy (all waves) and for the
+//             combine workgroups, which take the routing weights from them
 //   shared    S/32 workgroups: 32 hidden values of the shared expert (no
 //             routing needed), then their share of its down projection
-//   routed    K (I/32) workgroups: all E router logits (from L2: the
-//             router is 160 KiB), select, 32 hidden values of the expert of
-//             their slot, then their share of its down projection
+//   routed    K (I/32) workgroups: wait for their copy of the E logits,
+//             select, 32 hidden values of the expert of their slot, then
+//             their share of its down projection
 //   combine   H/8 workgroups: wait for the logits, select, then read the
 //             down partials of 8 output features, sum each expert's in
 //             block order, and the ordered combine.
@@ -20,27 +21,35 @@
 // partials cross workgroups, once: no hidden value is re-read by another
 // workgroup.
 //
-// Cross-workgroup data. The logits: the logit workgroups store them
-// device-coherently, wait for the stores, count themselves in one word;
-// the last one sets one flag line per combine workgroup and zeroes the
-// count; a combine workgroup polls its own line and zeroes it. The
-// partials: a region of 4-byte values (Scratch::part), each written by
+// Cross-workgroup data. The logits, for the routed workgroups: one copy
+// (64 words of Scratch::part, the sentinel 0xffffffff between launches)
+// per routed workgroup, written device-coherently by the logit workgroups
+// (8 words each), polled by its routed workgroup until no word is the
+// sentinel, and set back to the sentinel by it. The logits, for the
+// combine workgroups: the logit workgroups store them device-coherently,
+// wait for the stores, count themselves in one word; the last one sets
+// one flag line per combine workgroup and zeroes the count; a combine
+// workgroup polls its own line and zeroes it. The partials: a region of
+// 4-byte values (Scratch::part), each written by
 // exactly one gate/up workgroup and read by exactly one combine workgroup,
 // that holds the sentinel 0xffffffff between launches. A producer stores
 // its value device-coherently (a value with the sentinel's bits becomes
-// the quiet NaN 0x7fc00000), then sets its done word (which it zeroed at
-// its start); the consumer polls the done words (one small run) until all
-// are set, then reads its values with device-coherent loads until none is
-// the sentinel, then writes the sentinel back. The done words only pace
-// the polling (a stale one costs a few more data polls, never a value):
-// what orders the data is the sentinel check. So no word is counted into
-// by more than the 8 logit workgroups, the partials are in their
-// launch-start state again when the launch ends (also under graph replay:
-// nothing depends on a launch counter), and a consumer sees each value as
-// soon as its store lands. Why this shape: an agent-scope release / acquire fence per wave
-// (an L2 write-back or invalidate each) made a call take 160 us instead of
-// 17, and hundreds of waves counting into and polling one word took 80 us
-// (accesses to one line serialise where the XCDs meet). Workgroups wait
+// the quiet NaN 0x7fc00000); the consumer polls one probe of its run (the
+// last routed producer's first values) until it is no longer the
+// sentinel, then reads all its values with device-coherent loads until
+// none is the sentinel, then writes the sentinel back. The probe only
+// paces the polling: what orders the data is the sentinel check. So no
+// word is counted into by more than the 8 logit workgroups, the partials
+// are in their launch-start state again when the launch ends (also under
+// graph replay: nothing depends on a launch counter), and a consumer sees
+// each value as soon as its store lands. Why this shape: an agent-scope
+// release / acquire fence per wave (an L2 write-back or invalidate each)
+// made a call take 160 us instead of 17, and hundreds of waves counting
+// into and polling one word took 80 us (accesses to one line serialise
+// where the XCDs meet). The routed workgroups used to compute all E
+// logits themselves from the router in L2 (160 KiB per workgroup): they
+// selected at 4.6 us, against 4.3 us polling their copy (INT8 14.9 ->
+// 14.5 us per token, W8A8 15.5 -> 14.9 us). Workgroups wait
 // only on workgroups with smaller ids (logit < gate/up < combine). The
 // dispatcher starts a launch's workgroups in id order, so every workgroup
 // waited on has started, and none of those waits itself on a later one;
@@ -89,6 +98,13 @@ constexpr int kSpinLimit = 1 << 20;
 constexpr int kLine = 16;         // sync words per 64-byte line
 constexpr int kErrResource = 6;  // uocr_status Resource
 constexpr uint32_t kSentinel = 0xffffffffu;
+// The routed workgroups' logit copies (64 words each) follow the partials.
+constexpr size_t kCopyBase = (size_t)kMaxParts * kWide;
+static_assert((kCopyBase + (size_t)kMaxK * kNarrow / 32 * 64) * 4 <= kDecodePartBytes, "copies");
+__device__ __forceinline__ uint32_t publish_bits(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  return bits == kSentinel ? 0x7fc00000u : bits;
+}
 
 
 // Row of w13 holding gate value k (up value k is 32 rows further).
@@ -252,45 +268,49 @@ __device__ __forceinline__ WaveSel select_token(const DeviceLayer& L, const Scra
   return route_wave_sel(v, L.E, L.K);
 }
 
-// Stages the activation row (wave 0) into LDS, quantised per 32-block for
-// W8A8; the caller's loads stay in flight meanwhile.
-template <int KIND, int KH>
-__device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
-                                        int wave, int lane) {
-  if (wave == 0) {
-    RowStage<KH> X;
-    load_row(X, S.xn, L.H, lane);
-    store_row(X, sm.xl, L.H, lane);
-  }
-  __syncthreads();
-  if constexpr (KIND == kW8A8) {
-    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
-    __syncthreads();
-  }
-}
-
 // Logit workgroup b: router rows 8b + q and 8b + q + 4 (q = lane / 16; BF16
-// router, FP32 x; rows past E read as zero) dotted with x by one wave.
+// router, FP32 x; rows past E read as zero) dotted with x by wave 0; every
+// wave then stores the 8 logits (rows below E) into its share of the
+// routed workgroups' copies, and wave 0 stores them for the combine
+// workgroups, then counts in.
 template <int KH, bool ST>
 __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
-                           const SyncMap& M, const DecodeGrid& G, int b, int lane) {
+                           const SyncMap& M, const DecodeGrid& G, int b, int wave, int lane) {
   const int q = lane >> 4;
   const int ra = kLogitsPerWg * b + q, rb = ra + 4;
   stamp<ST>(S, 0);
-  RowPair<kBF16, KH> R;
-  issue_rows(R, L.router, nullptr, L.E, L.H, ra, rb);
-  RowStage<KH> X;
-  load_row(X, S.xn, L.H, lane);
-  store_row(X, sm.xl, L.H, lane);  // read back by this wave only
-  float r0, r1;
-  dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
+  float r0 = 0.0f, r1 = 0.0f;
+  if (wave == 0) {
+    RowPair<kBF16, KH> R;
+    issue_rows(R, L.router, nullptr, L.E, L.H, ra, rb);
+    RowStage<KH> X;
+    load_row(X, S.xn, L.H, lane);
+    store_row(X, sm.xl, L.H, lane);  // read back by this wave only
+    dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
+    if ((lane & 15) == 0) {
+      sm.logits[q] = r0;
+      sm.logits[q + 4] = r1;
+    }
+  }
+  __syncthreads();
+  {
+    // Every wave: row 8b + (lane & 7) into routed copies 8 wave + lane / 8,
+    // + 64, ...
+    const int j = lane & 7, row = kLogitsPerWg * b + j;
+    const uint32_t v = publish_bits(sm.logits[j]);
+    uint32_t* copies = reinterpret_cast<uint32_t*>(S.part) + kCopyBase;
+    if (row < L.E)
+      for (int i = 8 * wave + (lane >> 3); i < G.n_routed; i += 64)
+        part_store(copies + (size_t)i * 64 + row, v);
+  }
+  if (wave != 0) return;
   if ((lane & 15) == 0) {
     if (ra < L.E) shared_store(S.logits + ra, r0);
     if (rb < L.E) shared_store(S.logits + rb, r1);
   }
   stamp<ST>(S, 1);
   // Counted once the logits are stored; the last logit workgroup releases
-  // every workgroup waiting for them.
+  // every combine workgroup waiting for them.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   stamp<ST>(S, 2);
   int last = 0;
@@ -464,7 +484,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
     if (wave == 0) store_row(X, sm.xl, L.H, lane);
     __syncthreads();
     if constexpr (KIND == kW8A8) {
-      if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
+      quantize_lds_waves(sm.xl, L.H, sm.xq, sm.xs, wave, kUpWaves, lane, S.err);
       __syncthreads();
     }
     BlockSumOut bs;
@@ -488,29 +508,35 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int rb = b - n_shared;
   const int slot = rb / per_expert;
   const int c = rb - slot * per_expert;
-  // Router rows 8 wave + q and 8 wave + q + 4 (BF16 router, FP32 x; rows
-  // past E read as zero), the logits into LDS; x is issued first, so it is
-  // staged while the router rows are still in flight. Same rows and the
-  // same dot as the logit workgroups: the same logits, bit for bit.
-  {
+  // Wave 1 stages x while wave 0 polls this workgroup's copy of the logits
+  // (bounded; a word still the sentinel after a wait that gave up reads as
+  // 0, so the forward reports Resource rather than the sentinel's NaN). The
+  // copy goes back to the sentinel at the end of the role.
+  uint32_t* copy = reinterpret_cast<uint32_t*>(S.part) + kCopyBase + (size_t)rb * 64;
+  if (wave == 1) {
     RowStage<KH> X;
-    if (wave == 0) load_row(X, S.xn, L.H, lane);
-    RowPair<kBF16, KH> R;
-    issue_rows(R, L.router, nullptr, L.E, L.H, 8 * wave + q, 8 * wave + q + 4);
-    if (wave == 0) store_row(X, sm.xl, L.H, lane);
-    __syncthreads();
-    stamp<ST>(S, 1);
-    float r0, r1;
-    dot_rows(R, L.H, sm.xl, nullptr, nullptr, r0, r1);
-    if ((lane & 15) == 0) {
-      sm.logits[8 * wave + q] = r0;
-      sm.logits[8 * wave + q + 4] = r1;
-    }
+    load_row(X, S.xn, L.H, lane);
+    store_row(X, sm.xl, L.H, lane);
   }
-  if constexpr (KIND == kW8A8) {
-    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
+  if (wave == 0) {
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(copy, (uint32_t)L.E * 4u);
+    const int bound = wait_bound(S);
+    uint32_t v = 0u;
+    for (int it = 0;; it++) {
+      v = __builtin_amdgcn_raw_buffer_load_b32(cr, lane < L.E ? (uint32_t)lane * 4u : kOut, 0,
+                                               kCoherent);
+      if (__ballot(lane < L.E && v == kSentinel) == 0ull) break;
+      if (it >= bound) {
+        if (lane == 0) raise_error(S.err, kErrResource);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      asm volatile("" ::: "memory");  // the next poll reloads
+    }
+    sm.logits[lane] = lane < L.E && v != kSentinel ? __uint_as_float(v) : 0.0f;
   }
   __syncthreads();
+  stamp<ST>(S, 1);
   // Wave 0 selects the token's experts for the workgroup.
   if (wave == 0) {
     const WaveSel r = route_wave_sel(sm.logits[lane], L.E, L.K);
@@ -523,6 +549,12 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int ra = gate_row(k);
   RowPair<KIND, KH> P;
   issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
+  // W8A8: x quantised per 32-block while the rows are in flight (the
+  // barrier waits for LDS traffic only).
+  if constexpr (KIND == kW8A8) {
+    quantize_lds_waves(sm.xl, L.H, sm.xq, sm.xs, wave, kUpWaves, lane, S.err);
+    __syncthreads();
+  }
   // One token: the dispatched position of a slot is the slot itself.
   BlockSumOut bs;
   if (KIND == kW8A8 && S.q8.gateup) {
@@ -540,6 +572,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   int32_t* tr = KIND == kW8A8 && S.q8.down ? S.q8.down + (size_t)slot * L.H * nbI + c : nullptr;
   down_partial(D, L, S, sm, b, np, tr, nbI);
   finish_block(S.gu + (size_t)slot * L.I + (size_t)c * kHidPerWg, h, wave, lane);
+  if (wave == 0 && lane < L.E) part_store(copy + lane, kSentinel);  // read once, above
   // The first routed workgroup writes the routing and the one-token
   // dispatch last (its stores are off the path to the partials).
   if (rb == 0 && wave == 0) {
@@ -727,7 +760,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DeviceLayer L, Scratch
   }
   int b = blockIdx.x;
   if (b < G.n_logit) {
-    if (wave == 0) logit_role<KH, ST>(L, S, sm.up, M, G, b, lane);
+    logit_role<KH, ST>(L, S, sm.up, M, G, b, wave, lane);
   } else if ((b -= G.n_logit) < G.n_up()) {
     gateup_role<KIND, KH, ST>(L, S, sm.up, G, b, wave, lane);
   } else {

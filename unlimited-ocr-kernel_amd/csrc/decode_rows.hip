@@ -47,11 +47,7 @@
 // read as zero without a memory access), all issued before the first use.
 //
 // Arithmetic is that of Decoder::projection / feed_forward for one row
-// (src/decoder/mod.rs:99-122): BF16 widened exactly; INT8 weight-only as
-// the rounded product w * scale (src/cpu/quantized.rs:119-131); W8A8 for
-// DynamicActivations (one row is always a single-row group, :103-104) with
-// the row quantised per 32-block and exact i32 block sums (:155-236).
-// Routing is moe::route (src/decoder/moe.rs:7-30) on logits from
+// (src/decoder/mod.rs:99-122): BF16 weights widened exactly. Routing is moe::route (src/decoder/moe.rs:7-30) on logits from
 // ops::linear (src/cpu/ops.rs:9-59); the combine follows src/decoder/mod.rs:185-194.
 #include "common.hpp"
 #include "moe_kernels.hpp"
@@ -80,37 +76,21 @@ __device__ __forceinline__ int gate_row(int k) { return (k >> 5) * 64 + (k & 31)
 
 __device__ __forceinline__ int clamp_group(int g, int n) { return g < 0 ? 0 : (g >= n ? n - 1 : g); }
 
-template <int KIND>
 __device__ __forceinline__ const void* w13_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? (const void*)(L.w13 + L.w13_offset(g))
-                       : (const void*)(L.q13 + L.w13_offset(g));
+  return L.w13 + L.w13_offset(g);
 }
-template <int KIND>
-__device__ __forceinline__ const float* s13_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? nullptr : L.s13 + L.s13_offset(g);
-}
-template <int KIND>
-__device__ __forceinline__ const float* s2_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? nullptr : L.s2 + L.s2_offset(g);
-}
-template <int KIND>
 __device__ __forceinline__ const void* w2_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? (const void*)(L.w2 + L.w2_offset(g))
-                       : (const void*)(L.q2 + L.w2_offset(g));
+  return L.w2 + L.w2_offset(g);
 }
 
 struct GateUpSmem {
   float xl[kWide];
-  int8_t xq[kWide];
-  float xs[kWide / kQBlock];
   float logits[64];
   unsigned long long mask;
 };
 
 struct DownSmem {
   float hl[kMaxK + 2][kNarrow];
-  int8_t hq[kMaxK + 2][kNarrow];
-  float hs[kMaxK + 2][kNarrow / kQBlock];
   float yl[kMaxK + 2][8];
   float pw[kMaxK];
   unsigned long long mask;
@@ -253,9 +233,9 @@ __device__ __forceinline__ void wait_line(int* line, int n, const Scratch& S) {
   asm volatile("" ::: "memory");
 }
 
-// Stages the activation row (wave 0) into LDS, quantised per 32-block for
-// W8A8; the caller's loads stay in flight meanwhile.
-template <int KIND, int KH>
+// Stages the activation row (wave 0) into LDS; the caller's loads stay in
+// flight meanwhile.
+template <int KH>
 __device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
                                         int wave, int lane) {
   if (wave == 0) {
@@ -264,10 +244,6 @@ __device__ __forceinline__ void stage_x(const DeviceLayer& L, const Scratch& S, 
     store_row(X, sm.xl, L.H, lane);
   }
   __syncthreads();
-  if constexpr (KIND == kW8A8) {
-    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
-    __syncthreads();
-  }
 }
 
 // Logit workgroup b: router rows 8b + q and 8b + q + 4 (q = lane / 16; BF16
@@ -310,7 +286,7 @@ __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& s
 // also writes the routing and the one-token dispatch (ids, weights,
 // offsets, permutation, row tiles). Each wave counts itself done once its
 // hidden values are stored.
-template <int KIND, int KH, bool ST>
+template <int KH, bool ST>
 __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& sm,
                             const SyncMap& M, const DecodeGrid& G, int b, int wave, int lane) {
   const int q = lane >> 4;
@@ -320,18 +296,11 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   if (b < n_shared) {
     const int k = b * kHidPerWg + 4 * wave + q;
     const int ra = gate_row(k);
-    RowPair<KIND, KH> P;
-    issue_rows(P, w13_of<KIND>(L, L.E), s13_of<KIND>(L, L.E), 2 * L.S, L.H, ra, ra + 32);
-    stage_x<KIND, KH>(L, S, sm, wave, lane);
-    BlockSumOut bs;
-    if (KIND == kW8A8 && S.q8.s_gateup) {
-      const int nb = L.H / kQBlock;
-      bs.a = S.q8.s_gateup + (size_t)k * nb;
-      bs.b = S.q8.s_gateup + (size_t)(L.S + k) * nb;
-      bs.na = bs.nb = nb;
-    }
+    RowPair<kBF16, KH> P;
+    issue_rows(P, w13_of(L, L.E), nullptr, 2 * L.S, L.H, ra, ra + 32);
+    stage_x<KH>(L, S, sm, wave, lane);
     float r0, r1;
-    dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
+    dot_rows(P, L.H, sm.xl, nullptr, nullptr, r0, r1);
     stamp<ST>(S, 3);
     if ((lane & 15) == 0) shared_store(S.gu + (size_t)L.K * L.I + k, silu(r0) * r1);
     count_gateup(M, G, b, wave, lane);
@@ -358,9 +327,6 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
       sm.logits[8 * wave + q] = r0;
       sm.logits[8 * wave + q + 4] = r1;
     }
-  }
-  if constexpr (KIND == kW8A8) {
-    if (wave == 0) quantize_lds(sm.xl, L.H, sm.xq, sm.xs, lane, S.err);
   }
   __syncthreads();
   // Wave 0 selects the token's experts and publishes the selection; the
@@ -400,18 +366,10 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int g = clamp_group(__builtin_amdgcn_readfirstlane(slot_expert(sm.mask, slot)), L.E);
   const int k = kHidPerWg * (rb - slot * per_expert) + 4 * wave + q;
   const int ra = gate_row(k);
-  RowPair<KIND, KH> P;
-  issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
-  // One token: the dispatched position of a slot is the slot itself.
-  BlockSumOut bs;
-  if (KIND == kW8A8 && S.q8.gateup) {
-    const int nb = L.H / kQBlock;
-    bs.a = S.q8.gateup + ((size_t)slot * 2 * L.I + k) * nb;
-    bs.b = S.q8.gateup + ((size_t)slot * 2 * L.I + L.I + k) * nb;
-    bs.na = bs.nb = nb;
-  }
+  RowPair<kBF16, KH> P;
+  issue_rows(P, w13_of(L, g), nullptr, 2 * L.I, L.H, ra, ra + 32);
   float r0, r1;
-  dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
+  dot_rows(P, L.H, sm.xl, nullptr, nullptr, r0, r1);
   stamp<ST>(S, 3);
   if ((lane & 15) == 0) shared_store(S.gu + (size_t)slot * L.I + k, silu(r0) * r1);
   count_gateup(M, G, b, wave, lane);
@@ -423,7 +381,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
 // shared expert's reduction (S/2 columns each); then the ordered combine
 // of the 8 features: out = (residual +) ((y_s0 + y_s1) + p_0 y_0 + p_1 y_1
 // + ...), mul then add.
-template <int KIND, bool ST>
+template <bool ST>
 __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, const SyncMap& M,
                           const DecodeGrid& G, int b, const float* residual, float* out, int wave,
                           int lane) {
@@ -435,10 +393,9 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   // This wave's hidden row: an expert's I values, or half the shared S.
   const int n = routed ? L.I : half;
   // The shared expert's rows need no routing: issued first.
-  RowPair<KIND, kNarrow> P;
+  RowPair<kBF16, kNarrow> P;
   if (!routed)
-    issue_rows_cols(P, w2_of<KIND>(L, L.E), s2_of<KIND>(L, L.E), L.H, L.S, (wave - L.K) * half, n,
-                    f0 + q, f0 + q + 4);
+    issue_rows_cols(P, w2_of(L, L.E), nullptr, L.H, L.S, (wave - L.K) * half, n, f0 + q, f0 + q + 4);
   // Wave 0 selects; every routed wave needs its slot's expert, the combine
   // the routing weights in ascending slot order.
   if (wave == 0) {
@@ -457,18 +414,17 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
     // (~6 us after the selection), while the routed gate/up rows, read from
     // HBM at the same time, are on the critical path: issued at once, they
     // took a third of HBM from them. They wait for the time those rows take
-    // at the HBM peak (80 KB per 10 ns tick) less 0.44 us — 1.45 us INT8,
-    // 2.9 us BF16 at the model shape, measured best of 1.0-5.0 us (per
-    // token 16.1 -> 15.8 us INT8, 18.4 -> 17.9 us BF16); issuing them after
-    // the hidden values were in cost 0.8 us instead. A wait on the
-    // real-time counter always ends.
-    const long long up_bytes = (long long)L.K * 2 * L.I * L.H * (KIND == kBF16 ? 16 : 9) / 8;
+    // at the HBM peak (80 KB per 10 ns tick) less 0.44 us — 2.9 us at the
+    // model shape, measured best of 1.0-5.0 us (per token 18.4 -> 17.9 us);
+    // issuing them after the hidden values were in cost 0.8 us instead. A
+    // wait on the real-time counter always ends.
+    const long long up_bytes = (long long)L.K * 2 * L.I * L.H * 2;
     const long long ticks = up_bytes / 81920 - 44;
     if (ticks > 0) {
       const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)ticks;
       while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(2);
     }
-    issue_rows_cols(P, w2_of<KIND>(L, g), s2_of<KIND>(L, g), L.H, L.I, 0, n, f0 + q, f0 + q + 4);
+    issue_rows_cols(P, w2_of(L, g), nullptr, L.H, L.I, 0, n, f0 + q, f0 + q + 4);
   }
   const float res_f = residual ? residual[f0 + (lane & 7)] : 0.0f;
   // The hidden rows are whole once every gate/up workgroup has counted
@@ -481,18 +437,8 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
   RowStage<kNarrow> Hr;
   load_row<kNarrow, kCoherent>(Hr, hrow, n, lane);
   store_row(Hr, sm.hl[wave], n, lane);  // each wave reads back its own row only
-  if constexpr (KIND == kW8A8) quantize_lds(sm.hl[wave], n, sm.hq[wave], sm.hs[wave], lane, S.err);
-  BlockSumOut bs;
-  if (KIND == kW8A8 && (routed ? S.q8.down : S.q8.s_down)) {
-    const int nb = L.width(g) / kQBlock;
-    int32_t* row = routed ? S.q8.down + ((size_t)wave * L.H + f0 + q) * nb
-                          : S.q8.s_down + (size_t)(f0 + q) * nb + (wave - L.K) * (half / kQBlock);
-    bs.a = row;
-    bs.b = row + (size_t)4 * nb;
-    bs.na = bs.nb = n / kQBlock;
-  }
   float r0, r1;
-  dot_rows(P, n, sm.hl[wave], sm.hq[wave], sm.hs[wave], r0, r1, bs);
+  dot_rows(P, n, sm.hl[wave], nullptr, nullptr, r0, r1);
   stamp<ST>(S, 4);
   if ((lane & 15) == 0) {
     sm.yl[wave][q] = r0;
@@ -512,7 +458,7 @@ __device__ void down_role(const DeviceLayer& L, const Scratch& S, DownSmem& sm, 
 
 constexpr int kBlockWaves = kUpWaves > kMaxK + 2 ? kUpWaves : kMaxK + 2;
 
-template <int KIND, int KH, bool ST>
+template <int KH, bool ST>
 __global__ __launch_bounds__(64 * kBlockWaves) void rows_decode_kernel(DeviceLayer L, Scratch S,
                                                                   const float* residual, float* out) {
   __shared__ __align__(16) DecodeSmem sm;
@@ -528,28 +474,28 @@ __global__ __launch_bounds__(64 * kBlockWaves) void rows_decode_kernel(DeviceLay
   }
   b -= G.n_logit;
   if (b < G.n_up()) {
-    if (wave < kUpWaves) gateup_role<KIND, KH, ST>(L, S, sm.up, M, G, b, wave, lane);
+    if (wave < kUpWaves) gateup_role<KH, ST>(L, S, sm.up, M, G, b, wave, lane);
     return;
   }
   b -= G.n_up();
-  if (wave < L.K + 2) down_role<KIND, ST>(L, S, sm.down, M, G, b, residual, out, wave, lane);
+  if (wave < L.K + 2) down_role<ST>(L, S, sm.down, M, G, b, residual, out, wave, lane);
 }
 
-template <int KIND, int KH>
-void launch_kind(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
-                 hipStream_t s) {
+template <int KH>
+void launch_width(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
+                  hipStream_t s) {
   const DecodeGrid G(L);
   const int waves = L.K + 2 > kUpWaves ? L.K + 2 : kUpWaves;
   if (S.stamps)
-    rows_decode_kernel<KIND, KH, true><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+    rows_decode_kernel<KH, true><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
   else
-    rows_decode_kernel<KIND, KH, false><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
+    rows_decode_kernel<KH, false><<<dim3(G.blocks()), dim3(64 * waves), 0, s>>>(L, S, residual, out);
 }
 
 }  // namespace
 
 bool rows_decode_supported(const DeviceLayer& L) {
-  // Gate/up rows reduce over H (<= 2048), 32 hidden values per workgroup;
+  // BF16 weights only (INT8 overlays take the split-K engine). Gate/up rows reduce over H (<= 2048), 32 hidden values per workgroup;
   // the down workgroups reduce over I (<= 1024, one wave per routed expert)
   // and the two halves of S (<= 2048, each a whole number of 32-blocks);
   // routing is one wave over E <= 64 logits.
@@ -561,17 +507,17 @@ bool rows_decode_supported(const DeviceLayer& L) {
   static_assert(kSubCounts <= kLine, "a down workgroup's sub-set flags share one line");
   static_assert(kLogitsPerWg == 8 && kHidPerWg == 32,
                 "the timeline's row count (UOCR_DECODE_STAMP_ROWS) follows these widths");
-  return L.H <= kWide && L.S <= kWide && L.I <= kNarrow && L.K >= 1 && L.K <= kMaxK &&
-         L.E <= 64 && L.H % 8 == 0 && L.I % kHidPerWg == 0 && L.S % kHidPerWg == 0 &&
-         L.S % 64 == 0;
+  return L.quant_mode == 0 && L.H <= kWide && L.S <= kWide && L.I <= kNarrow && L.K >= 1 &&
+         L.K <= kMaxK && L.E <= 64 && L.H % 8 == 0 && L.I % kHidPerWg == 0 &&
+         L.S % kHidPerWg == 0 && L.S % 64 == 0;
 }
 
 void launch_rows_decode(const DeviceLayer& L, const Scratch& S, const float* residual, float* out,
                         hipStream_t s) {
   if (L.H <= 1280)
-    launch_kind<kBF16, 1280>(L, S, residual, out, s);
+    launch_width<1280>(L, S, residual, out, s);
   else
-    launch_kind<kBF16, kWide>(L, S, residual, out, s);
+    launch_width<kWide>(L, S, residual, out, s);
 }
 
 }  // namespace uocr

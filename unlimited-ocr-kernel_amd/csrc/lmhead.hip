@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kRowThreads) void lm_head_kernel(const float* __res
   norm_row(row, H, head.norm_w, head.eps, xl, nullptr, nullptr, blockIdx.x == 0 ? err : nullptr);
   __syncthreads();
   if constexpr (KIND == kW8A8) {
-    if (wave == 0) quantize_lds(xl, H, xq, xs, lane, blockIdx.x == 0 ? err : nullptr);
+    quantize_lds_waves(xl, H, xq, xs, wave, kRowThreads / 64, lane, blockIdx.x == 0 ? err : nullptr);
     __syncthreads();
   }
   if (r0 >= head.V) return;  // no barrier follows

@@ -163,6 +163,9 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
 // (W8A8 row by row) beside the MFMA engine, after its dispatch.
 void launch_singles_gateup(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s);
 void launch_singles_down(const DeviceLayer& L, const Scratch& S, int T, hipStream_t s);
+// Router logits, routing and dispatch of T <= 16 tokens in one launch
+// (its workgroups counted in the words from kSmallRouteWord of S.sync,
+// which are zero between launches).
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
                         hipStream_t s);
 
@@ -232,19 +235,24 @@ constexpr int kGemvChunk = 16;
 // shared and the routed gate/up with their shares of the down projection,
 // ordered combine into out), ordered inside by the kDecodeSyncBytes at
 // S.sync, which must be zero when it starts and are zero again when it
-// ends, and handing its down partials over through the kDecodePartBytes at
-// S.part, which must hold 0xffffffff in every byte when it starts and do
-// again when it ends.
+// ends, and handing its logits and down partials over through the
+// kDecodePartBytes at S.part, which must hold 0xffffffff in every byte
+// when it starts and do again when it ends.
 constexpr size_t kDecodeSyncBytes = 64 << 10;
 // Partials: (S/32 + K I/32) per output feature, at most (2048/32 + 8 *
-// 1024/32) x 2048 features, 4 bytes each.
-constexpr size_t kDecodePartBytes = (size_t)(2048 / 32 + 8 * 1024 / 32) * 2048 * 4;
+// 1024/32) x 2048 features, 4 bytes each; then a 64-word copy of the
+// router logits per routed gate/up workgroup (at most 8 * 1024/32 = 256).
+constexpr size_t kDecodePartBytes = (size_t)(2048 / 32 + 8 * 1024 / 32 + 8) * 2048 * 4;
 // The split router's per-chunk counts (<= 128 chunks, one word per 64 bytes)
 // live in the same zero-between-launches region, past the decode engine's
 // words (at most 1 + 16 + 2 * 256 lines).
 constexpr size_t kRouterSyncWord = 10240;
 static_assert((kRouterSyncWord + 128 * 16) * 4 <= kDecodeSyncBytes, "router counts fit");
 static_assert((1 + 16 + 2 * 256) * 16 <= kRouterSyncWord, "after the decode words");
+// The small-batch router's counts of logit workgroups done (8 sub-count
+// lines and a top line, past the split router's counts).
+constexpr size_t kSmallRouteWord = kRouterSyncWord + 128 * 16;
+static_assert((kSmallRouteWord + 9 * 16) * 4 <= kDecodeSyncBytes, "small router counts fit");
 // By the layer's kind: BF16 layers take the row-dot engine (decode_rows.hip:
 // down rows on workgroups of their own, hidden values handed over through
 // the sync words), INT8 overlays the split-K engine (decode.hip).

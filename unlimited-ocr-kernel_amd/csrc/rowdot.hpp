@@ -29,26 +29,52 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // Quantise an FP32 row held in LDS per 32-block (Int8Matrix::quantize,
-// src/cpu/quantized.rs:43-74) with the 64 lanes of one wave; non-finite
-// input or an underflowing scale raises Numerical.
-__device__ inline void quantize_lds(const float* xl, int K, int8_t* xq, float* xs, int lane, int* err) {
-  for (int b = lane; b < K / kQBlock; b += 64) {
-    const float* v = xl + b * kQBlock;
-    float maximum = 0.0f;
-    bool bad = false;
-    for (int i = 0; i < kQBlock; i++) {
-      bad |= !isfinite(v[i]);
-      maximum = fmaxf(maximum, fabsf(v[i]));
+// src/cpu/quantized.rs:43-74) with waves `wave` of `nw`: a wave takes two
+// blocks per step, one value per lane, and four steps at once (independent
+// chains, so their latencies overlap); the block maximum comes from lane
+// moves (the maximum of absolute values is the same in any order, so the
+// scale and the rounded values are those of the serial loop). Non-finite
+// input or an underflowing scale raises Numerical. Every lane of each
+// calling wave must call it.
+__device__ inline void quantize_lds_waves(const float* xl, int K, int8_t* xq, float* xs, int wave,
+                                          int nw, int lane, int* err) {
+  constexpr int kU = 4;
+  const int nb = K / kQBlock;
+  const int half = lane >> 5, i = lane & 31;
+  const int step = 2 * nw;
+  for (int b0 = 2 * wave; b0 < nb; b0 += step * kU) {
+    float v[kU], m[kU];
+    unsigned long long nonfinite[kU];
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int b = b0 + step * u + half;
+      v[u] = b < nb ? xl[b * kQBlock + i] : 0.0f;
     }
-    const float scale = maximum / 127.0f;
-    if (bad || (maximum > 0.0f && scale == 0.0f)) raise_error(err, kErrNumerical);
-    xs[b] = scale;
-    for (int i = 0; i < kQBlock; i++) {
-      int q = 0;
-      if (scale != 0.0f) q = (int)fminf(fmaxf(rintf(v[i] / scale), -127.0f), 127.0f);
-      xq[b * kQBlock + i] = (int8_t)q;
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      nonfinite[u] = __ballot(!isfinite(v[u]));
+      m[u] = half_wave_max(fabsf(v[u]));
+    }
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int b = b0 + step * u + half;
+      const float scale = m[u] / 127.0f;
+      if (b < nb) {
+        if (i == 0) {
+          const bool bad = ((half ? nonfinite[u] >> 32 : nonfinite[u]) & 0xffffffffull) != 0;
+          if (bad || (m[u] > 0.0f && scale == 0.0f)) raise_error(err, kErrNumerical);
+          xs[b] = scale;
+        }
+        int q = 0;
+        if (scale != 0.0f) q = (int)fminf(fmaxf(rintf(v[u] / scale), -127.0f), 127.0f);
+        xq[b * kQBlock + i] = (int8_t)q;
+      }
     }
   }
+}
+// The same with one wave.
+__device__ inline void quantize_lds(const float* xl, int K, int8_t* xq, float* xs, int lane, int* err) {
+  quantize_lds_waves(xl, K, xq, xs, 0, 1, lane, err);
 }
 
 // 16-byte weight chunks of two rows, ra and rb, of a row-major [rows, K]
@@ -196,13 +222,19 @@ __device__ __forceinline__ void dot_rows_as(const RowPair<KIND, KMAX>& P, int K,
       pb = __builtin_amdgcn_sdot4((int)vb.y, yv.y, pb, false);
       pb = __builtin_amdgcn_sdot4((int)vb.z, yv.z, pb, false);
       pb = __builtin_amdgcn_sdot4((int)vb.w, yv.w, pb, false);
-      // Chunks 2b and 2b+1 (lanes j, j^1) form block b: exact i32 sum.
-      const int ia = pa + __shfl_xor(pa, 1);
-      const int ib = pb + __shfl_xor(pb, 1);
-      if ((j & 1) == 0) {
-        const int b = c >> 1;
-        a0 += (float)ia * P.sa[m] * xs[b];
-        a1 += (float)ib * P.sb[m] * xs[(xb_off >> 5) + b];
+      // Chunks 2b and 2b+1 (lanes j, j^1) form block b: exact i32 sum (the
+      // partner's value by a DPP quad swap, no LDS round trip). Even lanes
+      // add the block's scaled sum, odd lanes add zero: their partial sums
+      // stay +0, as if they had skipped the block.
+      const int ia = pa + __builtin_amdgcn_mov_dpp(pa, 0xB1, 0xf, 0xf, false);
+      const int ib = pb + __builtin_amdgcn_mov_dpp(pb, 0xB1, 0xf, 0xf, false);
+      const bool even = (j & 1) == 0;
+      const int b = c >> 1;
+      const float fa = (float)ia * P.sa[m] * xs[b];
+      const float fb = (float)ib * P.sb[m] * xs[(xb_off >> 5) + b];
+      a0 += even ? fa : 0.0f;
+      a1 += even ? fb : 0.0f;
+      if (even) {
         if (sums.a && b < sums.na) sums.a[b] = ia;
         if (sums.b && b < sums.nb) sums.b[b] = ib;
       }

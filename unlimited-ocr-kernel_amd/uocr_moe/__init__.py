@@ -359,7 +359,7 @@ def forward(ctx: Context, layer: MoeLayer, x, y, flags: int = 0, trace: dict | N
 
 STATIC_SCRATCH_BYTES = 20 << 20
 # The device flag, the decode engine's words and its down partials.
-STATIC_RESERVED_BYTES = 256 + (64 << 10) + (5 << 19)
+STATIC_RESERVED_BYTES = 256 + (64 << 10) + (328 << 13)
 
 
 def forward_static(layer: MoeLayer, x, y, flags: int = 0, status=None, stream=None):
