@@ -380,7 +380,7 @@ def main():
         else:  # split-K engine: combine workgroups read the down partials
             names = {"logit": ("start", "logits stored", "stores complete", "counted in"),
                      "shared": ("start", None, None, "rows dotted", "partials stored"),
-                     "routed": ("start", "input staged", "experts selected", "rows dotted",
+                     "routed": ("start", "logits and input in", "experts selected", "rows dotted",
                                 "partials stored"),
                      "output": ("start", "experts selected", "probe partial in",
                                 "partials read", "partials summed", "output written")}

@@ -155,7 +155,8 @@ typedef struct uocr_w8a8_trace {
  *     complete, 3 counted in;
  *   S/32 shared gate/up workgroups: 0 start, 3 rows dotted, 4 counted in
  *     (BF16 layers) or down partials stored (INT8 overlays);
- *   k*I/32 routed gate/up workgroups: 0 start, 1 input staged, 2 experts
+ *   k*I/32 routed gate/up workgroups: 0 start, 1 input staged (INT8
+ *     overlays: and the workgroup's copy of the logits in), 2 experts
  *     selected, 3 rows dotted, 4 as the shared ones;
  *   H/8 output workgroups. BF16 layers (down workgroups): 0 start, 1
  *     experts selected, 3 every hidden value ready, 4 rows dotted, 5 output

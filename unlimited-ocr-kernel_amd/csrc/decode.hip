@@ -75,6 +75,7 @@
 #include "common.hpp"
 #include "moe_kernels.hpp"
 #include "routing.hpp"
+#include "logit_copies.hpp"
 #include "rowdot.hpp"
 
 namespace uocr {
@@ -97,14 +98,8 @@ static_assert((size_t)kMaxParts * kWide * 4 <= kDecodePartBytes, "partial region
 constexpr int kSpinLimit = 1 << 20;
 constexpr int kLine = 16;         // sync words per 64-byte line
 constexpr int kErrResource = 6;  // uocr_status Resource
-constexpr uint32_t kSentinel = 0xffffffffu;
-// The routed workgroups' logit copies (64 words each) follow the partials.
-constexpr size_t kCopyBase = (size_t)kMaxParts * kWide;
-static_assert((kCopyBase + (size_t)kMaxK * kNarrow / 32 * 64) * 4 <= kDecodePartBytes, "copies");
-__device__ __forceinline__ uint32_t publish_bits(float v) {
-  const uint32_t bits = __float_as_uint(v);
-  return bits == kSentinel ? 0x7fc00000u : bits;
-}
+constexpr uint32_t kSentinel = kSlotSentinel;
+static_assert((size_t)kMaxParts * kWide <= kDecodeCopyWord, "partials before the logit copies");
 
 
 // Row of w13 holding gate value k (up value k is 32 rows further).
@@ -165,9 +160,6 @@ __device__ __forceinline__ void shared_store(float* p, float v) {
 }
 __device__ __forceinline__ float shared_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void part_store(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 constexpr int kCoherent = 16;  // buffer-load cache policy: sc1 (device coherent)
 
@@ -293,16 +285,7 @@ __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& s
     }
   }
   __syncthreads();
-  {
-    // Every wave: row 8b + (lane & 7) into routed copies 8 wave + lane / 8,
-    // + 64, ...
-    const int j = lane & 7, row = kLogitsPerWg * b + j;
-    const uint32_t v = publish_bits(sm.logits[j]);
-    uint32_t* copies = reinterpret_cast<uint32_t*>(S.part) + kCopyBase;
-    if (row < L.E)
-      for (int i = 8 * wave + (lane >> 3); i < G.n_routed; i += 64)
-        part_store(copies + (size_t)i * 64 + row, v);
-  }
+  publish_logits(S.part, sm.logits, b, L.E, G.n_routed, wave, kUpWaves, lane);
   if (wave != 0) return;
   if ((lane & 15) == 0) {
     if (ra < L.E) shared_store(S.logits + ra, r0);
@@ -426,7 +409,7 @@ __device__ __forceinline__ void down_partial(const DownBlock<KIND, KH>& D, const
     }
     uint32_t bits = __float_as_uint(y);
     if (bits == kSentinel) bits = 0x7fc00000u;
-    part_store(part + ((size_t)(f / kFeatPerWg) * np + p) * kFeatPerWg + f % kFeatPerWg, bits);
+    slot_store(part + ((size_t)(f / kFeatPerWg) * np + p) * kFeatPerWg + f % kFeatPerWg, bits);
   }
 }
 
@@ -467,10 +450,10 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int n_shared = L.S / kHidPerWg;
   const int per_expert = L.I / kHidPerWg;
   const int np = G.n_up();
-  // The down block is issued once the gate/up rows are dotted: issued
-  // with them, it took HBM from them (the routed rows are on the critical
-  // path: selection to rows dotted 3.4 -> 4.4 us, INT8) and held registers
-  // beside them.
+  // The down block: issued once the gate/up rows are dotted, except in a
+  // routed W8A8 workgroup (issued behind the rows; see there). Issued with
+  // the rows, it took HBM from them (the routed rows are on the critical
+  // path: selection to rows dotted 3.4 -> 4.4 us, INT8).
   DownBlock<KIND, KH> D;
   stamp<ST>(S, 0);
   if (b < n_shared) {
@@ -509,32 +492,13 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int slot = rb / per_expert;
   const int c = rb - slot * per_expert;
   // Wave 1 stages x while wave 0 polls this workgroup's copy of the logits
-  // (bounded; a word still the sentinel after a wait that gave up reads as
-  // 0, so the forward reports Resource rather than the sentinel's NaN). The
-  // copy goes back to the sentinel at the end of the role.
-  uint32_t* copy = reinterpret_cast<uint32_t*>(S.part) + kCopyBase + (size_t)rb * 64;
+  // (set back to the sentinel at the end of the role).
   if (wave == 1) {
     RowStage<KH> X;
     load_row(X, S.xn, L.H, lane);
     store_row(X, sm.xl, L.H, lane);
   }
-  if (wave == 0) {
-    const __amdgpu_buffer_rsrc_t cr = make_rsrc(copy, (uint32_t)L.E * 4u);
-    const int bound = wait_bound(S);
-    uint32_t v = 0u;
-    for (int it = 0;; it++) {
-      v = __builtin_amdgcn_raw_buffer_load_b32(cr, lane < L.E ? (uint32_t)lane * 4u : kOut, 0,
-                                               kCoherent);
-      if (__ballot(lane < L.E && v == kSentinel) == 0ull) break;
-      if (it >= bound) {
-        if (lane == 0) raise_error(S.err, kErrResource);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-      asm volatile("" ::: "memory");  // the next poll reloads
-    }
-    sm.logits[lane] = lane < L.E && v != kSentinel ? __uint_as_float(v) : 0.0f;
-  }
+  if (wave == 0) sm.logits[lane] = poll_logits(S.part, rb, L.E, wait_bound(S), S.err, lane);
   __syncthreads();
   stamp<ST>(S, 1);
   // Wave 0 selects the token's experts for the workgroup.
@@ -550,10 +514,15 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   RowPair<KIND, KH> P;
   issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
   // W8A8: x quantised per 32-block while the rows are in flight (the
-  // barrier waits for LDS traffic only).
+  // barrier waits for LDS traffic only), and the down block issued behind
+  // them: its dot (v_dot4 block sums) is slower than the weight-only one,
+  // and with the block in flight during it the token took 14.75 against
+  // 15.1 us. Weight-only issues the block after the dot (issued here, it
+  // took HBM from the gate/up rows: 14.5 -> 15.1 us).
   if constexpr (KIND == kW8A8) {
     quantize_lds_waves(sm.xl, L.H, sm.xq, sm.xs, wave, kUpWaves, lane, S.err);
     __syncthreads();
+    issue_down_block(D, L, g, c);
   }
   // One token: the dispatched position of a slot is the slot itself.
   BlockSumOut bs;
@@ -565,14 +534,14 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   }
   float r0, r1;
   dot_rows(P, L.H, sm.xl, sm.xq, sm.xs, r0, r1, bs);
-  issue_down_block(D, L, g, c);
+  if constexpr (KIND != kW8A8) issue_down_block(D, L, g, c);
   stamp<ST>(S, 3);
   const float h = hidden_block<KIND>(S, sm, r0, r1, wave, lane);
   const int nbI = L.I / kQBlock;
   int32_t* tr = KIND == kW8A8 && S.q8.down ? S.q8.down + (size_t)slot * L.H * nbI + c : nullptr;
   down_partial(D, L, S, sm, b, np, tr, nbI);
   finish_block(S.gu + (size_t)slot * L.I + (size_t)c * kHidPerWg, h, wave, lane);
-  if (wave == 0 && lane < L.E) part_store(copy + lane, kSentinel);  // read once, above
+  if (wave == 0) release_logits(S.part, rb, L.E, lane);
   // The first routed workgroup writes the routing and the one-token
   // dispatch last (its stores are off the path to the partials).
   if (rb == 0 && wave == 0) {
