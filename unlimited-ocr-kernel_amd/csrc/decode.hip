@@ -60,7 +60,7 @@
 // read as zero without a memory access), all issued before the first use.
 //
 // Arithmetic is that of Decoder::projection / feed_forward for one row
-// (src/decoder/mod.rs:99-122): BF16 widened exactly; INT8 weight-only as
+// (src/decoder/mod.rs:99-122): INT8 weight-only as
 // q * x summed per 16-byte chunk (gate/up) or per 32-block (down) and scaled
 // once by the block scale (the reference rounds w = q * scale first,
 // src/cpu/quantized.rs:119-131); W8A8 for DynamicActivations (one row is
@@ -107,25 +107,19 @@ __device__ __forceinline__ int gate_row(int k) { return (k >> 5) * 64 + (k & 31)
 
 __device__ __forceinline__ int clamp_group(int g, int n) { return g < 0 ? 0 : (g >= n ? n - 1 : g); }
 
-template <int KIND>
+// Group g's INT8 gate/up rows and their scales; its down matrix as k-blocked
+// panels ([W/32][H][32]) and their scales block-major ([W/32][H]).
 __device__ __forceinline__ const void* w13_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? (const void*)(L.w13 + L.w13_offset(g))
-                       : (const void*)(L.q13 + L.w13_offset(g));
+  return L.q13 + L.w13_offset(g);
 }
-template <int KIND>
 __device__ __forceinline__ const float* s13_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? nullptr : L.s13 + L.s13_offset(g);
+  return L.s13 + L.s13_offset(g);
 }
-// Group g's down matrix as k-blocked panels ([W/32][H][32]) and its scales
-// block-major ([W/32][H]).
-template <int KIND>
 __device__ __forceinline__ const void* w2k_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? (const void*)(L.w2k + L.w2_offset(g))
-                       : (const void*)(L.q2k + L.w2_offset(g));
+  return L.q2k + L.w2_offset(g);
 }
-template <int KIND>
 __device__ __forceinline__ const float* s2k_of(const DeviceLayer& L, int g) {
-  return KIND == kBF16 ? nullptr : L.s2k + L.s2_offset(g);
+  return L.s2k + L.s2_offset(g);
 }
 
 struct GateUpSmem {
@@ -306,12 +300,13 @@ __device__ void logit_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& s
 }
 
 // Block c of group g's down matrix for one 32-value hidden block: output
-// features f = tid + 512 r (r < kF), each the block's 32 consecutive panel
-// elements (16-byte loads), and its block scale (INT8 kinds).
+// features f = tid + 512 r (r < kF), each the block's 32 consecutive int8
+// panel elements (two 16-byte loads), and its block scale.
 template <int KIND, int KH>
 struct DownBlock {
+  static_assert(KIND != kBF16, "INT8 overlays only");
   static constexpr int kF = (KH + kThreads - 1) / kThreads;  // features per thread
-  static constexpr int kV = KIND == kBF16 ? 4 : 2;          // 16-byte loads per feature
+  static constexpr int kV = 2;                                // 16-byte loads per feature
   u32x4 w[kF][kV];
   float s[kF];
 };
@@ -320,27 +315,24 @@ template <int KIND, int KH>
 __device__ __forceinline__ void issue_down_block(DownBlock<KIND, KH>& D, const DeviceLayer& L,
                                                  int g, int c) {
   using DB = DownBlock<KIND, KH>;
-  constexpr uint32_t kEb = KIND == kBF16 ? 2 : 1;
   const int W = L.width(g);
   const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w2k_of<KIND>(L, g), (uint32_t)W * L.H * kEb);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w2k_of(L, g), (uint32_t)W * L.H);
 #pragma unroll
   for (int r = 0; r < DB::kF; r++) {
     const int f = tid + kThreads * r;
-    const uint32_t off = f < L.H ? ((uint32_t)c * L.H + f) * kQBlock * kEb : kOut;
+    const uint32_t off = f < L.H ? ((uint32_t)c * L.H + f) * kQBlock : kOut;
 #pragma unroll
     for (int v = 0; v < DB::kV; v++)
       D.w[r][v] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16u * v, 0, 0);
   }
-  if constexpr (KIND != kBF16) {
-    const int nb = W / kQBlock;
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(s2k_of<KIND>(L, g), (uint32_t)L.H * nb * 4u);
+  const int nb = W / kQBlock;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(s2k_of(L, g), (uint32_t)L.H * nb * 4u);
 #pragma unroll
-    for (int r = 0; r < DB::kF; r++) {
-      const int f = tid + kThreads * r;
-      D.s[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-          sr, f < L.H ? ((uint32_t)c * L.H + f) * 4u : kOut, 0, 0));
-    }
+  for (int r = 0; r < DB::kF; r++) {
+    const int f = tid + kThreads * r;
+    D.s[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        sr, f < L.H ? ((uint32_t)c * L.H + f) * 4u : kOut, 0, 0));
   }
 }
 
@@ -377,17 +369,7 @@ __device__ __forceinline__ void down_partial(const DownBlock<KIND, KH>& D, const
     const int f = tid + kThreads * r;
     if (f >= L.H) break;
     float y;
-    if constexpr (KIND == kBF16) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int v = 0; v < DB::kV; v++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          acc = fmaf(bf16_lo(D.w[r][v][i]), hv[8 * v + 2 * i], acc);
-          acc = fmaf(bf16_hi(D.w[r][v][i]), hv[8 * v + 2 * i + 1], acc);
-        }
-      y = acc;
-    } else if constexpr (KIND == kInt8) {
+    if constexpr (KIND == kInt8) {
       // The block's 32 q * h products accumulate first (exact integers
       // times h), then one multiply by the block scale.
       float acc = 0.0f;
@@ -463,7 +445,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
     RowStage<KH> X;
     if (wave == 0) load_row(X, S.xn, L.H, lane);
     RowPair<KIND, KH> P;
-    issue_rows(P, w13_of<KIND>(L, L.E), s13_of<KIND>(L, L.E), 2 * L.S, L.H, ra, ra + 32);
+    issue_rows(P, w13_of(L, L.E), s13_of(L, L.E), 2 * L.S, L.H, ra, ra + 32);
     if (wave == 0) store_row(X, sm.xl, L.H, lane);
     __syncthreads();
     if constexpr (KIND == kW8A8) {
@@ -512,7 +494,7 @@ __device__ void gateup_role(const DeviceLayer& L, const Scratch& S, GateUpSmem& 
   const int k = kHidPerWg * c + 4 * wave + q;
   const int ra = gate_row(k);
   RowPair<KIND, KH> P;
-  issue_rows(P, w13_of<KIND>(L, g), s13_of<KIND>(L, g), 2 * L.I, L.H, ra, ra + 32);
+  issue_rows(P, w13_of(L, g), s13_of(L, g), 2 * L.I, L.H, ra, ra + 32);
   // W8A8: x quantised per 32-block while the rows are in flight (the
   // barrier waits for LDS traffic only), and the down block issued behind
   // them: its dot (v_dot4 block sums) is slower than the weight-only one,
