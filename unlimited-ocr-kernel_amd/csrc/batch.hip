@@ -395,7 +395,7 @@ __attribute__((amdgpu_waves_per_eu(3))) void singles_down_kernel(DeviceLayer L, 
 // ------------------------------------------------------------- small router
 
 // Routing of T <= 16 tokens in one launch. Workgroup (b, p) dots router
-// rows 8b .. 8b+7 with tokens 2p, 2p+1 on its first wave (so the 2·H·E·T
+// rows 8b .. 8b+7 with tokens 2p, 2p+1 on its first two waves (so the 2·H·E·T
 // flops spread over E/8 · T/2 workgroups, and the router rows come from L2
 // after the first touch) and stores the logits device-coherently. Once its
 // stores are complete it counts itself in one of 8 sub-counts (workgroup
@@ -478,40 +478,31 @@ template <int KH>
 __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const float* __restrict__ x,
                                                                        DeviceLayer L, Scratch S,
                                                                        int T) {
-  __shared__ __align__(16) float xl[kRouterTok * KH];
+  __shared__ __align__(16) float xl[kRouterTok][KH];
   __shared__ int last;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (wave == 0) {
+  // Waves 0 and 1: tokens 2p and 2p + 1 (one token per wave keeps the
+  // router rows and the token row within the 128 VGPRs of a 16-wave
+  // workgroup).
+  const int t = kRouterTok * blockIdx.y + wave;
+  if (wave < kRouterTok && t < T) {
     const int ra = 8 * blockIdx.x + (lane >> 4), rb = ra + 4;
-    const int t0 = kRouterTok * blockIdx.y;
-    const int nt = min(kRouterTok, T - t0);
     RowPair<kBF16, KH> P;
     issue_rows(P, L.router, nullptr, L.E, L.H, ra, rb);
-    RowStage<kRouterTok * KH> X;
-    load_row(X, x + (size_t)t0 * L.H, nt * L.H, lane);
-    store_row(X, xl, nt * L.H, lane);  // read back by this wave only
-    auto run = [&](auto ntc) {
-      constexpr int NT = decltype(ntc)::value;
-      float a0[NT], a1[NT];
-#pragma unroll
-      for (int t = 0; t < NT; t++) a0[t] = a1[t] = 0.0f;
-      dot_rows_multi(P, L.H, xl, 0, L.H, a0, a1);
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const float v0 = row16_sum(a0[t]), v1 = row16_sum(a1[t]);
-        if ((lane & 15) == 0) {
-          float* row = S.logits + (size_t)(t0 + t) * L.E;
-          if (ra < L.E) __hip_atomic_store(row + ra, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (rb < L.E) __hip_atomic_store(row + rb, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    };
-    static_assert(kRouterTok == 2, "one case per token count");
-    if (nt == 2)
-      run(std::integral_constant<int, 2>{});
-    else
-      run(std::integral_constant<int, 1>{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logit stores are complete
+    RowStage<KH> X;
+    load_row(X, x + (size_t)t * L.H, L.H, lane);
+    store_row(X, xl[wave], L.H, lane);  // read back by this wave only
+    float v0, v1;
+    dot_rows(P, L.H, xl[wave], nullptr, nullptr, v0, v1);
+    if ((lane & 15) == 0) {
+      float* row = S.logits + (size_t)t * L.E;
+      if (ra < L.E) __hip_atomic_store(row + ra, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (rb < L.E) __hip_atomic_store(row + rb, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's logit stores are complete
+  __syncthreads();
+  if (wave == 0) {
     if (lane == 0) {
       const int n = (int)(gridDim.x * gridDim.y);
       const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
