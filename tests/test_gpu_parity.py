@@ -880,6 +880,33 @@ def test_block_stack(ctx, T, quant):
         assert err <= tol, err
 
 
+@pytest.mark.parametrize("H", [128, 1280, 1536, 2048])
+@pytest.mark.parametrize("T", [8, 40])
+def test_fused_norm_bits(ctx, H, T):
+    """The next layer's RMSNorm fused into a combine gives the standalone
+    norm's bits: a 2-layer block forward equals two 1-layer block forwards
+    (each with a standalone first norm), bit for bit, at widths that take
+    the one-row-per-wave form (<= 1280) and the one-row-per-workgroup form."""
+    shape = dict(hidden=H, inter=64, experts=16, shared=2)
+    layers = []
+    for l in range(2):
+        c = Case(ctx, shape, 4, seed=1500 + 11 * l + H, normalize=True)
+        nw = (0.75 + 0.5 * np.sin(np.arange(H) * (0.2 + 0.1 * l))).astype(np.float32)
+        c.w["norm_weight"] = orc.f32_to_bf16(nw).view(np.uint16)
+        cfg = um.config(H, shape["inter"], shape["experts"], shape["shared"], 4, normalize=True)
+        c.layer = um.MoeLayer(ctx, cfg, c.w, um.MEMORY_HOST)
+        layers.append(c.layer)
+    say(f"fused norm bits H={H} T={T}")
+    x = dev(syn.activations(T, H, seed=77 + T))
+    both = torch.empty_like(x)
+    um.block_forward(ctx, layers, x, both)
+    one = torch.empty_like(x)
+    two = torch.empty_like(x)
+    um.block_forward(ctx, layers[:1], x, one)
+    um.block_forward(ctx, layers[1:], one, two)
+    assert np.array_equal(both.cpu().numpy().view(np.uint32), two.cpu().numpy().view(np.uint32))
+
+
 # ------------------------------------------------------ vocabulary projection
 
 @pytest.mark.parametrize("V,H", [(1000, 1280), (4099, 1280), (517, 2048), (300, 192),

@@ -281,6 +281,7 @@ void launch_combine(const Scratch& S, const float* residual, int T, int H, int K
 // Rows of width <= 2048 (multiple of 4) take the fused norm (planes too);
 // wider rows a plain one (no planes).
 bool row_norm_fusable(int width);
+bool row_norm_wave(int width);
 void launch_rms_norm(const float* x, int rows, int width, const RowNorm& nn, int* err,
                      hipStream_t s);
 
