@@ -40,6 +40,13 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// bf16(a) in the low half, bf16(b) in the high half (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
 // Split FP32 activations [rows, K] into bf16 hi and lo planes, k-blocked
 // ([K/32][rows][32], as the GEMM reads them).
 __global__ void split_planes_kernel(const float* __restrict__ x, int rows, int K,
@@ -519,20 +526,24 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
         char* rowp = hst + (uint32_t)wn * (TM * 64) + row * 64 + 8 * fc;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          uint32_t hb[4], lb[4];
+          float h[4];
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const float gv = acc[mi][0][4 * j + i];
-            const float h = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][1][4 * j + i];
-            hb[i] = bf16_bits(h);
-            if constexpr (SPLIT) lb[i] = bf16_bits(h - __uint_as_float(hb[i] << 16));
+            h[i] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[mi][1][4 * j + i];
           }
+          // Two values per conversion (round to nearest even, as one at a
+          // time): hi, then lo = bf16(h - hi) from hi's halves.
+          const uint32_t hb01 = bf16_pair(h[0], h[1]), hb23 = bf16_pair(h[2], h[3]);
           const int pos = 16 * (j ^ hsw(row));
-          *reinterpret_cast<uint2*>(rowp + pos) =
-              make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-          if constexpr (SPLIT)
-            *reinterpret_cast<uint2*>(rowp + kPlaneB + pos) =
-                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+          *reinterpret_cast<uint2*>(rowp + pos) = make_uint2(hb01, hb23);
+          if constexpr (SPLIT) {
+            const uint32_t lb01 = bf16_pair(h[0] - __uint_as_float(hb01 << 16),
+                                            h[1] - __uint_as_float(hb01 & 0xffff0000u));
+            const uint32_t lb23 = bf16_pair(h[2] - __uint_as_float(hb23 << 16),
+                                            h[3] - __uint_as_float(hb23 & 0xffff0000u));
+            *reinterpret_cast<uint2*>(rowp + kPlaneB + pos) = make_uint2(lb01, lb23);
+          }
         }
       }
     }
