@@ -4,8 +4,10 @@
 // the INT8 overlay weight-only, or W8A8 when the mode is DynamicActivations
 // (the projected row is always a single row there).
 //
-// One launch: every workgroup normalises the row itself (a few KB, the same
-// reduction as the standalone norm, so the same bits) into LDS, then its
+// One launch: every workgroup normalises the row itself (a few KB; the
+// workgroup form of the norm's fixed-order reduction, which the standalone
+// norm takes above 1280 wide — up to 1280 it reduces per wave, so the two
+// agree to rounding there) into LDS, then its
 // four waves stream their 32 rows each of the [V, H] matrix, eight rows per
 // pass (16 lanes per row), with the next pass's loads issued before the
 // current pass is dotted. The bound is HBM: V * H * (2 | 1 + 4/32) bytes.

@@ -18,7 +18,7 @@ constexpr int kRowThreads = 256, kRowChunks = 2;
 // out = v * scale * w. Non-finite row or weight -> Numerical (:382-389).
 // The sum runs per thread over its chunks (x, y, z, w in turn), then over
 // the wave and the four waves in order, so the standalone and the fused
-// norms give the same bits. Writes the normalised row and, when hi is set,
+// norms of a row wider than kWaveRowWidth give the same bits. Writes the normalised row and, when hi is set,
 // its bf16 planes (hi = bf16(v), lo = bf16(v - hi) when lo is set): row t
 // of `rows` into planes laid out [width/32][rows][32], as the MFMA engine
 // reads them (hi / lo are the planes' bases).
