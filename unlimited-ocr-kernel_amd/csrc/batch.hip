@@ -6,7 +6,9 @@
 // the dispatch), then the slices of each routed tile; workgroups are kept
 // small (19 KiB of LDS, <= 128 or 168 VGPRs) so that several share a CU and
 // their chains of dependent loads overlap. Used for 2 <= T <= 16, and for
-// the single-row W8A8 groups of INT8 layers at any T.
+// the single-row W8A8 groups of INT8 layers at any T. In INT8 weight-only
+// layers the shared expert's units run as MFMA tiles of 16 tokens instead
+// (the routed units keep the dot).
 //
 // Also the fence-free small-batch router (2 <= T <= 16): one launch whose
 // logit workgroups count themselves in; the last one routes every token
@@ -14,7 +16,8 @@
 //
 // Arithmetic: Decoder::projection / feed_forward (src/decoder/mod.rs:
 // 99-122) per row; INT8 weight-only as q * x summed per 16-byte chunk and
-// scaled by the chunk's block scale; W8A8 only for DynamicActivations
+// scaled by the chunk's block scale (MFMA units: per 32-block, with the
+// activations as bf16 hi + lo planes); W8A8 only for DynamicActivations
 // groups of a single row (:103-104).
 #include <type_traits>
 
@@ -61,8 +64,9 @@ struct Unit {
 };
 
 // Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
-// holds rows [ts * kSharedRows, ...) of the shared group), then ur slices of
-// each routed tile of the dispatch list.
+// holds rows [ts * SH, ...) of the shared group), then ur slices of each
+// routed tile of the dispatch list.
+template <int SH = kSharedRows>
 __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
                                           int nsh, int us, int ur, Unit& u) {
   int b = blockIdx.x;
@@ -70,10 +74,10 @@ __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S
     const int ts = b / us;
     u.g = L.E;
     u.routed = false;
-    u.r0 = ts * kSharedRows;
+    u.r0 = ts * SH;
     u.slice = b - ts * us;
     u.group_rows = T;
-    u.n = min(kSharedRows, T - u.r0);
+    u.n = min(SH, T - u.r0);
     return u.n > 0;
   }
   b -= nsh * us;
@@ -378,6 +382,209 @@ __attribute__((amdgpu_waves_per_eu(3))) void batch_down_kernel(
     down_body<KIND, true, DYN>(L, S, sm, u);
 }
 
+// MFMA form of the shared expert's units in INT8 weight-only layers: a tile
+// of up to 16 tokens times two sets of 16 weight rows (gate and up rows of
+// 16 hidden values, or 32 down rows), as v_mfma_f32_16x16x32_bf16 products.
+// A = the tokens' bf16 planes (hi, then lo: FP32-class; k-blocked
+// [K/32][rows][32]); B = 16 rows of one 32-block from the k-blocked int8
+// panels, each int8 exact in bf16; one partial per block and row set,
+// folded into the accumulator with the rows' block scales
+// (Decoder::projection, src/decoder/mod.rs:99-112, with the scale applied
+// per 32-block). Wave w takes the w-th quarter of the blocks; the four
+// partial tiles meet in LDS, summed in wave order. The MFMA costs the same
+// for 1 or 16 tokens, so the shared tiles take 16 rows; routed tiles
+// (about two tokens each) stay on the dot, where the 16-row A operand's
+// loads cost more than the MFMA saves (the 16-token forward's gate/up launch
+// took 50.7 instead of 35.2 us with every unit in MFMA form).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kMfmaSharedRows = 16;
+constexpr int kMfmaWaves = 4;
+constexpr int kPartLd = 20;  // floats per row of a partial tile (16 tokens + pad, 16-byte aligned)
+
+struct MfmaUnitSmem {
+  float part[kMfmaWaves][2][16][kPartLd];  // [wave][row set][row][token]
+};
+union SharedSmem {
+  BatchSmem b;
+  MfmaUnitSmem m;
+};
+
+// Eight int8 weights as bf16 (the f32 of a small integer has a zero low
+// half, so its bf16 is the high half).
+__device__ __forceinline__ bf16x8 widen_q8(u32x2 q) {
+  uint32_t hp[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t word = j < 2 ? q.x : q.y;
+    const int s0 = 16 * (j & 1);
+    const float w0 = (float)(int8_t)((word >> s0) & 0xffu);
+    const float w1 = (float)(int8_t)((word >> (s0 + 8)) & 0xffu);
+    hp[j] = __builtin_amdgcn_perm(__float_as_uint(w1), __float_as_uint(w0), 0x07060302u);
+  }
+  return __builtin_bit_cast(bf16x8, u32x4{hp[0], hp[1], hp[2], hp[3]});
+}
+
+// Rows ra and rb (this lane's column of each row set) of a k-blocked int8
+// panel [K/32][rows][32] with row-major block scales [rows][K/32], dotted
+// with plane row xrow of the planes (hi at `planes`, lo prows * K elements
+// later, k-blocked [K/32][prows][32]): acc_a / acc_b hold this wave's blocks'
+// sums for tokens 4 (lane / 16) .. + 3. Rows outside [0, rows) read as zero.
+template <int KMAX>
+__device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* scales, int rows,
+                                              int K, int ra, int rb, const uint16_t* planes,
+                                              int prows, int xrow, f32x4& acc_a, f32x4& acc_b) {
+  const int wave = threadIdx.x >> 6, grp = (threadIdx.x >> 4) & 3;
+  const int nblk = K / kQBlock;
+  constexpr int kBW = KMAX / kQBlock / kMfmaWaves;  // blocks per wave, at most
+  const int per = (nblk + kMfmaWaves - 1) / kMfmaWaves;
+  const int kb0 = wave * per;
+  // Weights and scales first (they need only the group).
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(panel, (uint32_t)rows * (uint32_t)K);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(scales, (uint32_t)rows * (uint32_t)nblk * 4u);
+  u32x2 qa[kBW], qb[kBW];
+  float sa[kBW], sb[kBW];
+#pragma unroll
+  for (int i = 0; i < kBW; i++) {
+    const int kb = kb0 + i;
+    const bool ok = i < per && kb < nblk;
+    const uint32_t at = (uint32_t)kb * rows;
+    qa[i] = __builtin_amdgcn_raw_buffer_load_b64(
+        wr, ok && ra < rows ? ((at + ra) * 32u + 8u * grp) : kOut, 0, 0);
+    qb[i] = __builtin_amdgcn_raw_buffer_load_b64(
+        wr, ok && rb < rows ? ((at + rb) * 32u + 8u * grp) : kOut, 0, 0);
+    sa[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        sr, ok && ra < rows ? ((uint32_t)ra * nblk + kb) * 4u : kOut, 0, 0));
+    sb[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        sr, ok && rb < rows ? ((uint32_t)rb * nblk + kb) * 4u : kOut, 0, 0));
+  }
+  const uint32_t plane = (uint32_t)prows * (uint32_t)K;  // elements per plane
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(planes, plane * 4u);
+  acc_a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  acc_b = acc_a;
+#pragma unroll
+  for (int i = 0; i < kBW; i++) {
+    const int kb = kb0 + i;
+    const bool ok = i < per && kb < nblk;
+    const uint32_t at = ((uint32_t)kb * prows + xrow) * 64u + 16u * grp;
+    const bf16x8 xh = __builtin_bit_cast(
+        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOut, 0, 0));
+    const bf16x8 xl = __builtin_bit_cast(
+        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at + plane * 2u : kOut, 0, 0));
+    const bf16x8 wa = widen_q8(qa[i]), wb = widen_q8(qb[i]);
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wa, z, 0, 0, 0);
+    pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wa, pa, 0, 0, 0);
+    f32x4 pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, z, 0, 0, 0);
+    pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, pb, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      acc_a[r] = __builtin_fmaf(pa[r], sa[i], acc_a[r]);
+      acc_b[r] = __builtin_fmaf(pb[r], sb[i], acc_b[r]);
+    }
+  }
+}
+
+// Sums the four waves' partial tiles in wave order: thread (c = tid % 16,
+// t = tid / 16) receives row c of each set for token t.
+__device__ __forceinline__ void mfma_reduce(MfmaUnitSmem& sm, const f32x4& acc_a,
+                                            const f32x4& acc_b, float& a, float& b) {
+  const int wave = threadIdx.x >> 6, col = threadIdx.x & 15, grp = (threadIdx.x >> 4) & 3;
+  *reinterpret_cast<f32x4*>(&sm.part[wave][0][col][4 * grp]) = acc_a;
+  *reinterpret_cast<f32x4*>(&sm.part[wave][1][col][4 * grp]) = acc_b;
+  __syncthreads();
+  const int c = threadIdx.x & 15, t = threadIdx.x >> 4;
+  a = sm.part[0][0][c][t];
+  b = sm.part[0][1][c][t];
+#pragma unroll
+  for (int w = 1; w < kMfmaWaves; w++) {
+    a += sm.part[w][0][c][t];
+    b += sm.part[w][1][c][t];
+  }
+}
+
+// bf16 planes of the shared expert's hidden rows ([S/32][T][32], hi then
+// lo), in the bytes the routed engine's gate/up/down leave free.
+__device__ __forceinline__ uint16_t* shared_hidden_planes(const Scratch& S) {
+  return reinterpret_cast<uint16_t*>(S.gu);
+}
+
+// Shared gate/up unit: 16 hidden values k0 .. k0 + 15 for the tile's
+// tokens; h = silu(gate) * up (src/decoder/mod.rs:114-122) goes to the
+// hidden planes.
+template <int KH>
+__device__ __forceinline__ void shared_gateup_mfma(const DeviceLayer& L, const Scratch& S,
+                                                   MfmaUnitSmem& sm, const Unit& u, int T) {
+  const int W = L.S, col = threadIdx.x & 15;
+  const int k0 = 16 * u.slice;
+  const int ra = gate_row(k0) + col;
+  f32x4 ag, au;
+  mfma_rows_dot<KH>(L.q13k + L.w13_offset(L.E), L.s13 + L.s13_offset(L.E), 2 * W, L.H, ra, ra + 32,
+                    S.xb, T, u.r0 + min(col, u.n - 1), ag, au);
+  float g, up;
+  mfma_reduce(sm, ag, au, g, up);
+  const int c = threadIdx.x & 15, t = threadIdx.x >> 4, k = k0 + c;
+  if (t < u.n && k < W) {
+    const float h = silu(g) * up;
+    const uint16_t hb = __builtin_bit_cast(uint16_t, (__bf16)h);
+    const uint16_t lb = __builtin_bit_cast(uint16_t, (__bf16)(h - __uint_as_float((uint32_t)hb << 16)));
+    uint16_t* hp = shared_hidden_planes(S);
+    const size_t p = ((size_t)(k / 32) * T + u.r0 + t) * 32 + k % 32;
+    hp[p] = hb;
+    hp[(size_t)T * W + p] = lb;
+  }
+}
+
+// Shared down unit: output features 32 slice .. + 31 for the tile's tokens.
+__device__ __forceinline__ void shared_down_mfma(const DeviceLayer& L, const Scratch& S,
+                                                 MfmaUnitSmem& sm, const Unit& u, int T) {
+  const int W = L.S, col = threadIdx.x & 15;
+  const int n0 = 32 * u.slice;
+  f32x4 aa, ab;
+  mfma_rows_dot<kWideK>(L.q2k + L.w2_offset(L.E), L.s2 + L.s2_offset(L.E), L.H, W, n0 + col,
+                        n0 + 16 + col, shared_hidden_planes(S), T, u.r0 + min(col, u.n - 1), aa, ab);
+  float ya, yb;
+  mfma_reduce(sm, aa, ab, ya, yb);
+  const int c = threadIdx.x & 15, t = threadIdx.x >> 4;
+  if (t < u.n) {
+    float* yout = S.ys + (size_t)(u.r0 + t) * L.H;
+    if (n0 + c < L.H) yout[n0 + c] = ya;
+    if (n0 + 16 + c < L.H) yout[n0 + 16 + c] = yb;
+  }
+}
+
+// INT8 weight-only gate/up and down with the shared expert's units in MFMA
+// form (the first nsh * us workgroups) and the routed units on the dot.
+template <int KH>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 4 : 3))) void batch_gateup_ms_kernel(
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
+  __shared__ __align__(16) SharedSmem sm;
+  Unit u;
+  if (!load_unit<kMfmaSharedRows>(L, S, T, mchunk, nsh, (L.S + 15) / 16, (L.I + 15) / 16, u))
+    return;
+  if (u.routed)
+    gateup_body<kInt8, KH, false>(L, S, sm.b, u);
+  else
+    shared_gateup_mfma<KH>(L, S, sm.m, u, T);
+}
+
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(3))) void batch_down_ms_kernel(
+    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
+  __shared__ __align__(16) SharedSmem sm;
+  Unit u;
+  if (!load_unit<kMfmaSharedRows>(L, S, T, mchunk, nsh, L.H / 32, down_units(L.H, L.I), u))
+    return;
+  if (!u.routed)
+    shared_down_mfma(L, S, sm.m, u, T);
+  else if (L.I <= kSegK)
+    down_body<kInt8, false, false>(L, S, sm.b, u);
+  else
+    down_body<kInt8, true, false>(L, S, sm.b, u);
+}
+
 // Down of the single-row W8A8 groups; HALVES as down_body (routed width
 // beyond kSegK).
 template <bool HALVES>
@@ -474,10 +681,11 @@ __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scrat
   }
 }
 
+// planes: where the x planes go (null: not written).
 template <int KH>
 __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const float* __restrict__ x,
                                                                        DeviceLayer L, Scratch S,
-                                                                       int T) {
+                                                                       int T, uint16_t* planes) {
   __shared__ __align__(16) float xl[kRouterTok][KH];
   __shared__ int last;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -492,6 +700,25 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const flo
     RowStage<KH> X;
     load_row(X, x + (size_t)t * L.H, L.H, lane);
     store_row(X, xl[wave], L.H, lane);  // read back by this wave only
+    if (planes && blockIdx.x == 0) {
+      // The token's bf16 planes (hi = bf16(x), lo = bf16(x - hi)),
+      // k-blocked [H/32][T][32], for the MFMA gate/up units.
+#pragma unroll
+      for (int i = 0; i < RowStage<KH>::kV; i++) {
+        const int e = 4 * (lane + 64 * i);
+        if (e >= L.H) continue;
+        const size_t p = ((size_t)(e / 32) * T + t) * 32 + e % 32;
+        uint32_t h[2], l[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const float a = __uint_as_float(X.v[i][2 * j]), b = __uint_as_float(X.v[i][2 * j + 1]);
+          h[j] = bf16_pair(a, b);
+          l[j] = bf16_pair(a - __uint_as_float(h[j] << 16), b - __uint_as_float(h[j] & 0xffff0000u));
+        }
+        *reinterpret_cast<uint2*>(planes + p) = make_uint2(h[0], h[1]);
+        *reinterpret_cast<uint2*>(planes + (size_t)T * L.H + p) = make_uint2(l[0], l[1]);
+      }
+    }
     float v0, v1;
     dot_rows(P, L.H, xl[wave], nullptr, nullptr, v0, v1);
     if ((lane & 15) == 0) {
@@ -544,6 +771,16 @@ dim3 singles_grid(const DeviceLayer& L, int T, int ur) {
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, hipStream_t s, bool shared_only) {
+  if (KIND == kInt8 && batch_mfma_shared(L)) {
+    const int nsh = (T + kMfmaSharedRows - 1) / kMfmaSharedRows;
+    const int units = nsh * ((L.S + 15) / 16) +
+                      (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16));
+    if (L.H <= 1280)
+      batch_gateup_ms_kernel<1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh);
+    else
+      batch_gateup_ms_kernel<kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh);
+    return;
+  }
   const int nsh = (T + kSharedRows - 1) / kSharedRows;
   const int units = nsh * ((L.S + 15) / 16) +
                     (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16));
@@ -562,6 +799,10 @@ void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles
 }
 
 }  // namespace
+
+bool batch_mfma_shared(const DeviceLayer& L) {
+  return L.quant_mode == kQuantWeightsOnly && L.S % 32 == 0 && L.S > 0;
+}
 
 bool batch_supported(const DeviceLayer& L) {
   // Down rows are held as one segment up to kSegK or as two halves.
@@ -599,6 +840,13 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
   const int units = nsh * down_units(L.H, L.S) +
                     (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
   const dim3 grid(units), block(256);
+  if (batch_mfma_shared(L)) {
+    const int nsh16 = (T + kMfmaSharedRows - 1) / kMfmaSharedRows;
+    const int units16 = nsh16 * (L.H / 32) +
+                        (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
+    batch_down_ms_kernel<<<dim3(units16), block, 0, s>>>(L, S, T, mchunk, nsh16);
+    return;
+  }
   if (L.quant_mode == 0)
     batch_down_kernel<kBF16, false><<<grid, block, 0, s>>>(L, S, T, mchunk, nsh);
   else if (L.quant_mode == kQuantDynamic)
@@ -610,10 +858,11 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
                         hipStream_t s) {
   const dim3 grid((L.E + 7) / 8, (T + kRouterTok - 1) / kRouterTok);
+  uint16_t* planes = batch_mfma_shared(L) ? S.xb : nullptr;
   if (L.H <= 1280)
-    small_route_kernel<1280><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T);
+    small_route_kernel<1280><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, planes);
   else
-    small_route_kernel<kWideK><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T);
+    small_route_kernel<kWideK><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, planes);
 }
 
 }  // namespace uocr

@@ -40,13 +40,6 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// bf16(a) in the low half, bf16(b) in the high half (one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
-}
-
 // Split FP32 activations [rows, K] into bf16 hi and lo planes, k-blocked
 // ([K/32][rows][32], as the GEMM reads them).
 __global__ void split_planes_kernel(const float* __restrict__ x, int rows, int K,
