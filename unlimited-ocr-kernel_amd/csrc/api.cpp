@@ -607,13 +607,7 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       if (overlap) HIP_TRY(hipStreamWaitEvent(st, ex.join, 0), "join wait");
     } else {
       // (The W8A8 trace's hidden rows of single-row groups are written by
-      // the gate/up units themselves.) MFMA units read the input's planes,
-      // which only the small router writes.
-      if (T > (size_t)uocr::kGemvChunk && uocr::batch_mfma_shared(L)) {
-        phase_begin(ctx, kSplit);
-        uocr::launch_split_planes(S.xn, Ti, L.H, S.xb, S.xb + T * L.H, st);
-        phase_end(ctx);
-      }
+      // the gate/up units themselves.)
       phase_begin(ctx, kGateUp);
       uocr::launch_batch_gateup(L, S, Ti, tiles_bound, bm, st);
       phase_end(ctx);

@@ -12,12 +12,13 @@
 //
 // Also the fence-free small-batch router (2 <= T <= 16): one launch whose
 // logit workgroups count themselves in; the last one routes every token
-// and builds the dispatch.
+// and builds the dispatch. In INT8 weight-only layers its launch also runs
+// the shared expert's gate/up units.
 //
 // Arithmetic: Decoder::projection / feed_forward (src/decoder/mod.rs:
 // 99-122) per row; INT8 weight-only as q * x summed per 16-byte chunk and
 // scaled by the chunk's block scale (MFMA units: per 32-block, with the
-// activations as bf16 hi + lo planes); W8A8 only for DynamicActivations
+// activations as bf16 hi + lo parts); W8A8 only for DynamicActivations
 // groups of a single row (:103-104).
 #include <type_traits>
 
@@ -63,24 +64,8 @@ struct Unit {
   bool routed;
 };
 
-// Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
-// holds rows [ts * SH, ...) of the shared group), then ur slices of each
-// routed tile of the dispatch list.
-template <int SH = kSharedRows>
-__device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
-                                          int nsh, int us, int ur, Unit& u) {
-  int b = blockIdx.x;
-  if (b < nsh * us) {
-    const int ts = b / us;
-    u.g = L.E;
-    u.routed = false;
-    u.r0 = ts * SH;
-    u.slice = b - ts * us;
-    u.group_rows = T;
-    u.n = min(SH, T - u.r0);
-    return u.n > 0;
-  }
-  b -= nsh * us;
+// Routed unit b: ur slices of each routed tile of the dispatch list.
+__device__ __forceinline__ bool routed_unit(const Scratch& S, int mchunk, int ur, int b, Unit& u) {
   const int i = b / ur;
   // Both loads in flight together; i stays inside the list's allocation.
   const int routed_tiles = S.counters[1];
@@ -93,6 +78,25 @@ __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S
   u.group_rows = S.offsets[g + 1] - S.offsets[g];
   u.n = min(mchunk, u.group_rows - r0);
   return u.n > 0;
+}
+
+// Unit blockIdx.x: the nsh shared tiles' us slices each come first (tile ts
+// holds rows [ts * kSharedRows, ...) of the shared group), then the routed
+// units.
+__device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S, int T, int mchunk,
+                                          int nsh, int us, int ur, Unit& u) {
+  const int b = blockIdx.x;
+  if (b < nsh * us) {
+    const int ts = b / us;
+    u.g = L.E;
+    u.routed = false;
+    u.r0 = ts * kSharedRows;
+    u.slice = b - ts * us;
+    u.group_rows = T;
+    u.n = min(kSharedRows, T - u.r0);
+    return u.n > 0;
+  }
+  return routed_unit(S, mchunk, ur, b - nsh * us, u);
 }
 
 // The single-row pass (the W8A8 rows the MFMA engine leaves to this engine
@@ -383,19 +387,27 @@ __attribute__((amdgpu_waves_per_eu(3))) void batch_down_kernel(
 }
 
 // MFMA form of the shared expert's units in INT8 weight-only layers: a tile
-// of up to 16 tokens times two sets of 16 weight rows (gate and up rows of
-// 16 hidden values, or 32 down rows), as v_mfma_f32_16x16x32_bf16 products.
-// A = the tokens' bf16 planes (hi, then lo: FP32-class; k-blocked
-// [K/32][rows][32]); B = 16 rows of one 32-block from the k-blocked int8
-// panels, each int8 exact in bf16; one partial per block and row set,
-// folded into the accumulator with the rows' block scales
-// (Decoder::projection, src/decoder/mod.rs:99-112, with the scale applied
-// per 32-block). Wave w takes the w-th quarter of the blocks; the four
-// partial tiles meet in LDS, summed in wave order. The MFMA costs the same
-// for 1 or 16 tokens, so the shared tiles take 16 rows; routed tiles
-// (about two tokens each) stay on the dot, where the 16-row A operand's
-// loads cost more than the MFMA saves (the 16-token forward's gate/up launch
-// took 50.7 instead of 35.2 us with every unit in MFMA form).
+// of up to 16 tokens times one or two sets of 16 weight rows (gate and up
+// rows of 16 hidden values, or 16 or 32 down rows), as
+// v_mfma_f32_16x16x32_bf16 products. A = the tokens' activations as bf16
+// hi and lo parts (FP32-class: the input rows split as they are loaded, the
+// hidden rows handed over as k-blocked [K/32][rows][32] planes); B = 16 rows
+// of one 32-block from the k-blocked int8 panels, each int8 exact in bf16;
+// one partial per block and row set, folded into the accumulator with the
+// rows' block scales (Decoder::projection, src/decoder/mod.rs:99-112, with
+// the scale applied per 32-block). Wave w of the unit's four takes the w-th
+// quarter of the blocks; the four partial tiles meet in LDS, summed in wave
+// order. The MFMA costs the same for 1 or 16 tokens, so the shared tiles
+// take 16 rows; routed tiles (about two tokens each) stay on the dot, where
+// a 16-row A operand's loads cost more than the MFMA saves (the 16-token
+// forward's gate/up launch took 50.7 instead of 35.2 us with every unit in
+// MFMA form).
+//
+// Where they run (2 <= T <= 16, hidden width <= 1280): the shared gate/up
+// units in the router's launch, beside its logit workgroups (they need no
+// routing), and the shared down units at the head of the gate/up launch;
+// the down launch then holds routed units only. Otherwise the shared units
+// head the gate/up and down launches.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -426,16 +438,19 @@ __device__ __forceinline__ bf16x8 widen_q8(u32x2 q) {
   return __builtin_bit_cast(bf16x8, u32x4{hp[0], hp[1], hp[2], hp[3]});
 }
 
-// Rows ra and rb (this lane's column of each row set) of a k-blocked int8
-// panel [K/32][rows][32] with row-major block scales [rows][K/32], dotted
-// with plane row xrow of the planes (hi at `planes`, lo prows * K elements
-// later, k-blocked [K/32][prows][32]): acc_a / acc_b hold this wave's blocks'
-// sums for tokens 4 (lane / 16) .. + 3. Rows outside [0, rows) read as zero.
-template <int KMAX>
+// Rows ra (and, with NSET = 2, rb) -- this lane's column of each row set --
+// of a k-blocked int8 panel [K/32][rows][32] with row-major block scales
+// [rows][K/32], dotted with activation row xrow: with F32X, FP32 rows
+// [prows][K] split into bf16 hi and lo parts here; otherwise bf16 planes
+// (hi at `act`, lo prows * K elements later, k-blocked [K/32][prows][32]).
+// acc_a / acc_b hold this wave's blocks' sums for tokens 4 (lane / 16) ..
+// + 3. Rows outside [0, rows) read as zero. Lanes are numbered within the
+// unit's four waves (threadIdx.x mod 256).
+template <int KMAX, int NSET, bool F32X>
 __device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* scales, int rows,
-                                              int K, int ra, int rb, const uint16_t* planes,
-                                              int prows, int xrow, f32x4& acc_a, f32x4& acc_b) {
-  const int wave = threadIdx.x >> 6, grp = (threadIdx.x >> 4) & 3;
+                                              int K, int ra, int rb, const void* act, int prows,
+                                              int xrow, f32x4& acc_a, f32x4& acc_b) {
+  const int wave = (threadIdx.x >> 6) & 3, grp = (threadIdx.x >> 4) & 3;
   const int nblk = K / kQBlock;
   constexpr int kBW = KMAX / kQBlock / kMfmaWaves;  // blocks per wave, at most
   const int per = (nblk + kMfmaWaves - 1) / kMfmaWaves;
@@ -443,8 +458,8 @@ __device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* 
   // Weights and scales first (they need only the group).
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(panel, (uint32_t)rows * (uint32_t)K);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(scales, (uint32_t)rows * (uint32_t)nblk * 4u);
-  u32x2 qa[kBW], qb[kBW];
-  float sa[kBW], sb[kBW];
+  u32x2 qa[kBW], qb[NSET == 2 ? kBW : 1];
+  float sa[kBW], sb[NSET == 2 ? kBW : 1];
 #pragma unroll
   for (int i = 0; i < kBW; i++) {
     const int kb = kb0 + i;
@@ -452,49 +467,70 @@ __device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* 
     const uint32_t at = (uint32_t)kb * rows;
     qa[i] = __builtin_amdgcn_raw_buffer_load_b64(
         wr, ok && ra < rows ? ((at + ra) * 32u + 8u * grp) : kOut, 0, 0);
-    qb[i] = __builtin_amdgcn_raw_buffer_load_b64(
-        wr, ok && rb < rows ? ((at + rb) * 32u + 8u * grp) : kOut, 0, 0);
     sa[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         sr, ok && ra < rows ? ((uint32_t)ra * nblk + kb) * 4u : kOut, 0, 0));
-    sb[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        sr, ok && rb < rows ? ((uint32_t)rb * nblk + kb) * 4u : kOut, 0, 0));
+    if constexpr (NSET == 2) {
+      qb[i] = __builtin_amdgcn_raw_buffer_load_b64(
+          wr, ok && rb < rows ? ((at + rb) * 32u + 8u * grp) : kOut, 0, 0);
+      sb[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          sr, ok && rb < rows ? ((uint32_t)rb * nblk + kb) * 4u : kOut, 0, 0));
+    }
   }
-  const uint32_t plane = (uint32_t)prows * (uint32_t)K;  // elements per plane
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(planes, plane * 4u);
+  const uint32_t plane = (uint32_t)prows * (uint32_t)K;  // elements per plane or per row set
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(act, plane * 4u);
   acc_a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   acc_b = acc_a;
 #pragma unroll
   for (int i = 0; i < kBW; i++) {
     const int kb = kb0 + i;
     const bool ok = i < per && kb < nblk;
-    const uint32_t at = ((uint32_t)kb * prows + xrow) * 64u + 16u * grp;
-    const bf16x8 xh = __builtin_bit_cast(
-        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOut, 0, 0));
-    const bf16x8 xl = __builtin_bit_cast(
-        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at + plane * 2u : kOut, 0, 0));
-    const bf16x8 wa = widen_q8(qa[i]), wb = widen_q8(qb[i]);
+    bf16x8 xh, xl;
+    if constexpr (F32X) {
+      const uint32_t at = ((uint32_t)xrow * K + (uint32_t)kb * 32u + 8u * grp) * 4u;
+      const u32x4 f0 = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOut, 0, 0);
+      const u32x4 f1 = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at + 16u : kOut, 0, 0);
+      const uint32_t f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float a = __uint_as_float(f[2 * j]), b = __uint_as_float(f[2 * j + 1]);
+        h[j] = bf16_pair(a, b);
+        l[j] = bf16_pair(a - bf16_lo(h[j]), b - bf16_hi(h[j]));
+      }
+      xh = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+      xl = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
+    } else {
+      const uint32_t at = ((uint32_t)kb * prows + xrow) * 64u + 16u * grp;
+      xh = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOut, 0, 0));
+      xl = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at + plane * 2u : kOut, 0, 0));
+    }
     const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bf16x8 wa = widen_q8(qa[i]);
     f32x4 pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wa, z, 0, 0, 0);
     pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wa, pa, 0, 0, 0);
-    f32x4 pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, z, 0, 0, 0);
-    pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, pb, 0, 0, 0);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      acc_a[r] = __builtin_fmaf(pa[r], sa[i], acc_a[r]);
-      acc_b[r] = __builtin_fmaf(pb[r], sb[i], acc_b[r]);
+    for (int r = 0; r < 4; r++) acc_a[r] = __builtin_fmaf(pa[r], sa[i], acc_a[r]);
+    if constexpr (NSET == 2) {
+      const bf16x8 wb = widen_q8(qb[i]);
+      f32x4 pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, z, 0, 0, 0);
+      pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, pb, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc_b[r] = __builtin_fmaf(pb[r], sb[i], acc_b[r]);
     }
   }
 }
 
-// Sums the four waves' partial tiles in wave order: thread (c = tid % 16,
-// t = tid / 16) receives row c of each set for token t.
+// Sums the unit's four waves' partial tiles in wave order (one barrier for
+// the whole workgroup): thread (c = tid % 16, t = tid / 16 % 16) receives
+// row c of each set for token t.
 __device__ __forceinline__ void mfma_reduce(MfmaUnitSmem& sm, const f32x4& acc_a,
                                             const f32x4& acc_b, float& a, float& b) {
-  const int wave = threadIdx.x >> 6, col = threadIdx.x & 15, grp = (threadIdx.x >> 4) & 3;
+  const int wave = (threadIdx.x >> 6) & 3, col = threadIdx.x & 15, grp = (threadIdx.x >> 4) & 3;
   *reinterpret_cast<f32x4*>(&sm.part[wave][0][col][4 * grp]) = acc_a;
   *reinterpret_cast<f32x4*>(&sm.part[wave][1][col][4 * grp]) = acc_b;
   __syncthreads();
-  const int c = threadIdx.x & 15, t = threadIdx.x >> 4;
+  const int c = threadIdx.x & 15, t = (threadIdx.x >> 4) & 15;
   a = sm.part[0][0][c][t];
   b = sm.part[0][1][c][t];
 #pragma unroll
@@ -505,81 +541,106 @@ __device__ __forceinline__ void mfma_reduce(MfmaUnitSmem& sm, const f32x4& acc_a
 }
 
 // bf16 planes of the shared expert's hidden rows ([S/32][T][32], hi then
-// lo), in the bytes the routed engine's gate/up/down leave free.
+// lo), in bytes the small-batch engine leaves free.
 __device__ __forceinline__ uint16_t* shared_hidden_planes(const Scratch& S) {
   return reinterpret_cast<uint16_t*>(S.gu);
 }
 
-// Shared gate/up unit: 16 hidden values k0 .. k0 + 15 for the tile's
-// tokens; h = silu(gate) * up (src/decoder/mod.rs:114-122) goes to the
-// hidden planes.
+// Shared gate/up unit: hidden values 16 slice .. + 15 for tokens [r0, r0 + n)
+// of the input rows; h = silu(gate) * up (src/decoder/mod.rs:114-122) goes
+// to the hidden planes. A unit that is not `live` still takes part in the
+// workgroup's barrier and stores nothing.
 template <int KH>
 __device__ __forceinline__ void shared_gateup_mfma(const DeviceLayer& L, const Scratch& S,
-                                                   MfmaUnitSmem& sm, const Unit& u, int T) {
+                                                   MfmaUnitSmem& sm, int slice, int r0, int n,
+                                                   int T, bool live) {
   const int W = L.S, col = threadIdx.x & 15;
-  const int k0 = 16 * u.slice;
-  const int ra = gate_row(k0) + col;
+  const int k0 = 16 * slice;
+  const int ra = live ? gate_row(k0) + col : 2 * W;
   f32x4 ag, au;
-  mfma_rows_dot<KH>(L.q13k + L.w13_offset(L.E), L.s13 + L.s13_offset(L.E), 2 * W, L.H, ra, ra + 32,
-                    S.xb, T, u.r0 + min(col, u.n - 1), ag, au);
+  mfma_rows_dot<KH, 2, true>(L.q13k + L.w13_offset(L.E), L.s13 + L.s13_offset(L.E), 2 * W, L.H,
+                             ra, ra + 32, S.xn, T, r0 + min(col, n - 1), ag, au);
   float g, up;
   mfma_reduce(sm, ag, au, g, up);
-  const int c = threadIdx.x & 15, t = threadIdx.x >> 4, k = k0 + c;
-  if (t < u.n && k < W) {
+  const int c = threadIdx.x & 15, t = (threadIdx.x >> 4) & 15, k = k0 + c;
+  if (live && t < n && k < W) {
     const float h = silu(g) * up;
     const uint16_t hb = __builtin_bit_cast(uint16_t, (__bf16)h);
     const uint16_t lb = __builtin_bit_cast(uint16_t, (__bf16)(h - __uint_as_float((uint32_t)hb << 16)));
     uint16_t* hp = shared_hidden_planes(S);
-    const size_t p = ((size_t)(k / 32) * T + u.r0 + t) * 32 + k % 32;
+    const size_t p = ((size_t)(k / 32) * T + r0 + t) * 32 + k % 32;
     hp[p] = hb;
     hp[(size_t)T * W + p] = lb;
   }
 }
 
-// Shared down unit: output features 32 slice .. + 31 for the tile's tokens.
+// Shared down unit: output features 16 NSET slice .. for tokens [r0, r0 + n).
+template <int NSET>
 __device__ __forceinline__ void shared_down_mfma(const DeviceLayer& L, const Scratch& S,
-                                                 MfmaUnitSmem& sm, const Unit& u, int T) {
+                                                 MfmaUnitSmem& sm, int slice, int r0, int n, int T) {
   const int W = L.S, col = threadIdx.x & 15;
-  const int n0 = 32 * u.slice;
+  const int n0 = 16 * NSET * slice;
   f32x4 aa, ab;
-  mfma_rows_dot<kWideK>(L.q2k + L.w2_offset(L.E), L.s2 + L.s2_offset(L.E), L.H, W, n0 + col,
-                        n0 + 16 + col, shared_hidden_planes(S), T, u.r0 + min(col, u.n - 1), aa, ab);
+  mfma_rows_dot<kWideK, NSET, false>(L.q2k + L.w2_offset(L.E), L.s2 + L.s2_offset(L.E), L.H, W,
+                                     n0 + col, n0 + 16 + col, shared_hidden_planes(S), T,
+                                     r0 + min(col, n - 1), aa, ab);
   float ya, yb;
   mfma_reduce(sm, aa, ab, ya, yb);
-  const int c = threadIdx.x & 15, t = threadIdx.x >> 4;
-  if (t < u.n) {
-    float* yout = S.ys + (size_t)(u.r0 + t) * L.H;
+  const int c = threadIdx.x & 15, t = (threadIdx.x >> 4) & 15;
+  if (t < n) {
+    float* yout = S.ys + (size_t)(r0 + t) * L.H;
     if (n0 + c < L.H) yout[n0 + c] = ya;
-    if (n0 + 16 + c < L.H) yout[n0 + 16 + c] = yb;
+    if (NSET == 2 && n0 + 16 + c < L.H) yout[n0 + 16 + c] = yb;
   }
 }
 
-// INT8 weight-only gate/up and down with the shared expert's units in MFMA
-// form (the first nsh * us workgroups) and the routed units on the dot.
+// Whether the router's launch runs the shared gate/up units (then the
+// gate/up launch runs the shared down units, 16 rows each).
+__host__ __device__ inline bool shared_in_router(const DeviceLayer& L, int T) {
+  return L.quant_mode == kQuantWeightsOnly && L.S % 32 == 0 && L.S > 0 && L.H <= 1280 &&
+         T <= kTileRows;
+}
+
+// Gate/up launch of INT8 weight-only layers: sdn shared down units (16
+// rows of the one shared tile), then sgu shared gate/up units (16-token
+// tiles, (S + 15) / 16 per tile), then the routed units on the dot.
 template <int KH>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 4 : 3))) void batch_gateup_ms_kernel(
-    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
+    DeviceLayer L, Scratch S, int T, int mchunk, int sdn, int sgu) {
   __shared__ __align__(16) SharedSmem sm;
-  Unit u;
-  if (!load_unit<kMfmaSharedRows>(L, S, T, mchunk, nsh, (L.S + 15) / 16, (L.I + 15) / 16, u))
+  int b = blockIdx.x;
+  if (b < sdn) {
+    shared_down_mfma<1>(L, S, sm.m, b, 0, T, T);
     return;
-  if (u.routed)
-    gateup_body<kInt8, KH, false>(L, S, sm.b, u);
-  else
-    shared_gateup_mfma<KH>(L, S, sm.m, u, T);
+  }
+  b -= sdn;
+  if (b < sgu) {
+    const int us = (L.S + 15) / 16, ts = b / us;
+    const int r0 = ts * kMfmaSharedRows;
+    shared_gateup_mfma<KH>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T, true);
+    return;
+  }
+  Unit u;
+  if (routed_unit(S, mchunk, (L.I + 15) / 16, b - sgu, u)) gateup_body<kInt8, KH, false>(L, S, sm.b, u);
 }
 
+// Down launch of INT8 weight-only layers: sdn shared down units (32 rows of
+// one 16-token tile), then the routed units on the dot.
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(3))) void batch_down_ms_kernel(
-    DeviceLayer L, Scratch S, int T, int mchunk, int nsh) {
+__attribute__((amdgpu_waves_per_eu(3))) void batch_down_ms_kernel(DeviceLayer L, Scratch S, int T,
+                                                                 int mchunk, int sdn) {
   __shared__ __align__(16) SharedSmem sm;
-  Unit u;
-  if (!load_unit<kMfmaSharedRows>(L, S, T, mchunk, nsh, L.H / 32, down_units(L.H, L.I), u))
+  const int b = blockIdx.x;
+  if (b < sdn) {
+    const int us = L.H / 32, ts = b / us;
+    const int r0 = ts * kMfmaSharedRows;
+    shared_down_mfma<2>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T);
     return;
-  if (!u.routed)
-    shared_down_mfma(L, S, sm.m, u, T);
-  else if (L.I <= kSegK)
+  }
+  Unit u;
+  if (!routed_unit(S, mchunk, down_units(L.H, L.I), b - sdn, u)) return;
+  if (L.I <= kSegK)
     down_body<kInt8, false, false>(L, S, sm.b, u);
   else
     down_body<kInt8, true, false>(L, S, sm.b, u);
@@ -681,44 +742,43 @@ __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scrat
   }
 }
 
-// planes: where the x planes go (null: not written).
+// Workgroups [0, n_route): router column b = id % ceil(E / 8) (rows 8b ..
+// 8b + 7) for tokens 2p, 2p + 1 (p = id / ceil(E / 8)). Each workgroup from
+// n_route on runs one of the shared expert's gate/up units on its first
+// four waves (they need no routing and take no part in the count); one
+// unit per workgroup, so that the units' weight streams spread over as
+// many CUs (with four units per 16-wave workgroup, 28 CUs streamed the
+// shared rows and the launch took 22.8 instead of 8.9 us).
 template <int KH>
 __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const float* __restrict__ x,
                                                                        DeviceLayer L, Scratch S,
-                                                                       int T, uint16_t* planes) {
+                                                                       int T, int n_route) {
   __shared__ __align__(16) float xl[kRouterTok][KH];
+  __shared__ __align__(16) MfmaUnitSmem su;
   __shared__ int last;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int id = (int)blockIdx.x;
+  if (id >= n_route) {
+    if constexpr (KH <= 1280) {
+      if (wave < kMfmaWaves)
+        shared_gateup_mfma<KH>(L, S, su, id - n_route, 0, T, T, true);
+      else
+        __syncthreads();  // the unit's one barrier
+    }
+    return;
+  }
+  const int bx = (L.E + 7) / 8, col = id % bx, pair = id / bx;
   // Waves 0 and 1: tokens 2p and 2p + 1 (one token per wave keeps the
   // router rows and the token row within the 128 VGPRs of a 16-wave
   // workgroup).
-  const int t = kRouterTok * blockIdx.y + wave;
+  const int t = kRouterTok * pair + wave;
   if (wave < kRouterTok && t < T) {
-    const int ra = 8 * blockIdx.x + (lane >> 4), rb = ra + 4;
+    const int ra = 8 * col + (lane >> 4), rb = ra + 4;
     RowPair<kBF16, KH> P;
     issue_rows(P, L.router, nullptr, L.E, L.H, ra, rb);
     RowStage<KH> X;
     load_row(X, x + (size_t)t * L.H, L.H, lane);
     store_row(X, xl[wave], L.H, lane);  // read back by this wave only
-    if (planes && blockIdx.x == 0) {
-      // The token's bf16 planes (hi = bf16(x), lo = bf16(x - hi)),
-      // k-blocked [H/32][T][32], for the MFMA gate/up units.
-#pragma unroll
-      for (int i = 0; i < RowStage<KH>::kV; i++) {
-        const int e = 4 * (lane + 64 * i);
-        if (e >= L.H) continue;
-        const size_t p = ((size_t)(e / 32) * T + t) * 32 + e % 32;
-        uint32_t h[2], l[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const float a = __uint_as_float(X.v[i][2 * j]), b = __uint_as_float(X.v[i][2 * j + 1]);
-          h[j] = bf16_pair(a, b);
-          l[j] = bf16_pair(a - __uint_as_float(h[j] << 16), b - __uint_as_float(h[j] & 0xffff0000u));
-        }
-        *reinterpret_cast<uint2*>(planes + p) = make_uint2(h[0], h[1]);
-        *reinterpret_cast<uint2*>(planes + (size_t)T * L.H + p) = make_uint2(l[0], l[1]);
-      }
-    }
     float v0, v1;
     dot_rows(P, L.H, xl[wave], nullptr, nullptr, v0, v1);
     if ((lane & 15) == 0) {
@@ -731,8 +791,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const flo
   __syncthreads();
   if (wave == 0) {
     if (lane == 0) {
-      const int n = (int)(gridDim.x * gridDim.y);
-      const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+      const int n = n_route;
       const int i = id % 8;
       int* sub = S.sync + kSmallRouteWord + 16 * i;
       int* top = S.sync + kSmallRouteWord + 16 * 8;
@@ -772,13 +831,16 @@ template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, hipStream_t s, bool shared_only) {
   if (KIND == kInt8 && batch_mfma_shared(L)) {
+    const bool in_router = shared_in_router(L, T);
     const int nsh = (T + kMfmaSharedRows - 1) / kMfmaSharedRows;
-    const int units = nsh * ((L.S + 15) / 16) +
+    const int sdn = in_router ? L.H / 16 : 0;
+    const int sgu = in_router ? 0 : nsh * ((L.S + 15) / 16);
+    const int units = sdn + sgu +
                       (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16));
     if (L.H <= 1280)
-      batch_gateup_ms_kernel<1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh);
+      batch_gateup_ms_kernel<1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, sdn, sgu);
     else
-      batch_gateup_ms_kernel<kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, nsh);
+      batch_gateup_ms_kernel<kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, sdn, sgu);
     return;
   }
   const int nsh = (T + kSharedRows - 1) / kSharedRows;
@@ -841,10 +903,11 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
                     (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
   const dim3 grid(units), block(256);
   if (batch_mfma_shared(L)) {
-    const int nsh16 = (T + kMfmaSharedRows - 1) / kMfmaSharedRows;
-    const int units16 = nsh16 * (L.H / 32) +
-                        (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
-    batch_down_ms_kernel<<<dim3(units16), block, 0, s>>>(L, S, T, mchunk, nsh16);
+    const int sdn = shared_in_router(L, T) ? 0
+                                           : (T + kMfmaSharedRows - 1) / kMfmaSharedRows * (L.H / 32);
+    const int units16 = sdn + (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) *
+                                                     down_units(L.H, L.I));
+    batch_down_ms_kernel<<<dim3(units16), block, 0, s>>>(L, S, T, mchunk, sdn);
     return;
   }
   if (L.quant_mode == 0)
@@ -857,12 +920,13 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
 
 void launch_small_route(const float* x, const DeviceLayer& L, const Scratch& S, int T,
                         hipStream_t s) {
-  const dim3 grid((L.E + 7) / 8, (T + kRouterTok - 1) / kRouterTok);
-  uint16_t* planes = batch_mfma_shared(L) ? S.xb : nullptr;
+  const int n_route = (L.E + 7) / 8 * ((T + kRouterTok - 1) / kRouterTok);
+  const int sgu = shared_in_router(L, T) ? (L.S + 15) / 16 : 0;
+  const dim3 grid(n_route + sgu);
   if (L.H <= 1280)
-    small_route_kernel<1280><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, planes);
+    small_route_kernel<1280><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, n_route);
   else
-    small_route_kernel<kWideK><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, planes);
+    small_route_kernel<kWideK><<<grid, dim3(64 * kRouteWaves), 0, s>>>(x, L, S, T, n_route);
 }
 
 }  // namespace uocr

@@ -154,8 +154,8 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 // logits, then one workgroup that routes and builds the dispatch.
 bool batch_supported(const DeviceLayer& L);
 // Whether the small-batch engine's shared-expert units take the MFMA form
-// (INT8 weight-only layers): they read the input's bf16 planes, which the
-// small router writes (other routers leave them to a split launch).
+// (INT8 weight-only layers; up to 1280 hidden values and 16 tokens the
+// small router's launch also runs the shared gate/up units).
 bool batch_mfma_shared(const DeviceLayer& L);
 // shared_only: the shared expert's units only (the MFMA engine at one
 // token under DynamicActivations, where the shared group is a single row).
