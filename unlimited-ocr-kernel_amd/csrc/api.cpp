@@ -169,7 +169,7 @@ namespace {
 
 struct ScratchPlan {
   size_t logits, ids, w, offsets, perm_rows, perm_w, inv_pos, tiles, counters, chunk_counts,
-      h, hs, y, ys, xn, xb, gu, q8x, q8s, router_part, total;
+      tile_desc, h, hs, y, ys, xn, xb, gu, q8x, q8s, router_part, total;
 };
 
 ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
@@ -193,6 +193,7 @@ ScratchPlan plan_scratch(const uocr_moe_config& c, size_t T) {
   p.tiles = take((size_t)uocr::max_tiles((int)T, (int)K, (int)E, 1) * 2 * 4);
   p.counters = take(16);
   p.chunk_counts = take((T + 15) / 16 * 64 * 4);
+  p.tile_desc = take(T <= (size_t)uocr::kGemvChunk ? E * uocr::kTileDescInts * 4 : 0);
   p.h = take(T * K * I * 4);
   p.hs = take(T * S * 4);
   p.y = take(T * K * H * 4);
@@ -255,6 +256,7 @@ Scratch carve(const Exec& ex, const ScratchPlan& p) {
   s.tiles = reinterpret_cast<int*>(b + p.tiles);
   s.counters = reinterpret_cast<int*>(b + p.counters);
   s.chunk_counts = reinterpret_cast<int*>(b + p.chunk_counts);
+  s.tile_desc = nullptr;  // set where the small router writes them
   s.h = reinterpret_cast<float*>(b + p.h);
   s.hs = reinterpret_cast<float*>(b + p.hs);
   s.y = reinterpret_cast<float*>(b + p.y);
@@ -520,6 +522,7 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       // Few tokens: one launch; the last of its logit workgroups routes
       // every token and builds the dispatch (counted in a word at S.sync).
       if (!S.sync) return fail(UOCR_ERR_UNSUPPORTED, "small-batch router without its sync word");
+      S.tile_desc = reinterpret_cast<int*>(ex.scratch + plan.tile_desc);
       phase_begin(ctx, kRouter);
       uocr::launch_small_route(S.xn, L, S, Ti, st);
       phase_end(ctx);

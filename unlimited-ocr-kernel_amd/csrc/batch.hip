@@ -62,20 +62,41 @@ __host__ __device__ inline int down_units(int H, int W) { return W <= kSegK ? H 
 struct Unit {
   int g, r0, n, group_rows, slice;
   bool routed;
+  int base;          // first dispatched position (routed) or row (shared); < 0: read the offsets
+  const int* rows;   // the tile's tokens from its record (null: the permutation)
 };
 
-// Routed unit b: ur slices of each routed tile of the dispatch list.
+// Routed unit b: ur slices of each routed tile of the dispatch list. With
+// the small router's tile records, one load gives the group, its position
+// and rows, and the tokens (record i is written for every listed tile, and
+// i stays inside the records' allocation).
 __device__ __forceinline__ bool routed_unit(const Scratch& S, int mchunk, int ur, int b, Unit& u) {
   const int i = b / ur;
+  u.routed = true;
+  u.slice = b - i * ur;
+  if (S.tile_desc) {
+    const int* d = S.tile_desc + (size_t)i * kTileDescInts;
+    const int routed_tiles = S.counters[1];
+    const int g = d[0], base = d[1], rows = d[2];
+    if (i >= routed_tiles) return false;
+    u.g = g;
+    u.r0 = 0;
+    u.base = base;
+    u.rows = d + 4;
+    u.group_rows = rows;
+    u.n = min(mchunk, rows);
+    return u.n > 0;
+  }
   // Both loads in flight together; i stays inside the list's allocation.
   const int routed_tiles = S.counters[1];
   const int g = S.tiles[2 * i], r0 = S.tiles[2 * i + 1];
   if (i >= routed_tiles) return false;
   u.g = g;
   u.r0 = r0;
-  u.routed = true;
-  u.slice = b - i * ur;
-  u.group_rows = S.offsets[g + 1] - S.offsets[g];
+  const int first = S.offsets[g];
+  u.group_rows = S.offsets[g + 1] - first;
+  u.base = first + r0;
+  u.rows = nullptr;
   u.n = min(mchunk, u.group_rows - r0);
   return u.n > 0;
 }
@@ -91,6 +112,8 @@ __device__ __forceinline__ bool load_unit(const DeviceLayer& L, const Scratch& S
     u.g = L.E;
     u.routed = false;
     u.r0 = ts * kSharedRows;
+    u.base = u.r0;
+    u.rows = nullptr;
     u.slice = b - ts * us;
     u.group_rows = T;
     u.n = min(kSharedRows, T - u.r0);
@@ -123,6 +146,8 @@ __device__ __forceinline__ Unit single_unit(unsigned long long m, int ur, int b)
   u.n = 1;
   u.group_rows = 1;
   u.routed = true;
+  u.base = -1;
+  u.rows = nullptr;
   u.slice = b - j * ur;
   return u;
 }
@@ -260,9 +285,9 @@ __device__ __forceinline__ void gateup_body(const DeviceLayer& L, const Scratch&
   const int ra = gate_row(k);
   RowPair<KIND, KH> P;
   issue_rows(P, w13_of<KIND>(L, u.g), s13_of<KIND>(L, u.g), 2 * W, L.H, ra, ra + 32);
-  const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
+  const int base = u.base >= 0 ? u.base : S.offsets[u.g] + u.r0;
   auto row_of = [&](int t) {
-    const int row = u.routed ? S.perm_rows[base + t] : base + t;
+    const int row = u.rows ? u.rows[t] : u.routed ? S.perm_rows[base + t] : base + t;
     return S.xn + (size_t)row * L.H;
   };
   float* hout = SINGLE     ? S.gu + (size_t)base * L.I
@@ -335,7 +360,7 @@ __device__ __forceinline__ void down_body(const DeviceLayer& L, const Scratch& S
   const int rb = HALVES ? ra : ra + 4;
   RowPair<KIND, kSegK> P;
   issue_segs(P, w2_of<KIND>(L, u.g), s2_of<KIND>(L, u.g), L.H, W, ra, 0, rb, HALVES ? seg : 0, seg);
-  const int base = u.routed ? S.offsets[u.g] + u.r0 : u.r0;
+  const int base = u.base >= 0 ? u.base : S.offsets[u.g] + u.r0;
   const float* hin = SINGLE     ? S.gu + (size_t)base * L.I
                       : u.routed ? S.h + (size_t)base * L.I
                                  : S.hs + (size_t)base * L.S;
@@ -681,6 +706,7 @@ constexpr int kRouteWaves = 16;
 __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scratch& S, int T,
                                                int wave, int lane) {
   __shared__ unsigned long long masks[kRouteWaves];
+  __shared__ unsigned long long active_mask;
   __shared__ int count[64];
   __shared__ int start[65];
   const int E = L.E, K = L.K;
@@ -706,6 +732,8 @@ __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scrat
     }
     start[lane] = incl - count[lane];
     if (lane == 63) start[64] = incl;
+    const unsigned long long am = __ballot(count[lane] > 0);
+    if (lane == 0) active_mask = am;
   }
   __syncthreads();
   if (mine && ((r.mask >> lane) & 1ull)) {
@@ -719,6 +747,11 @@ __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scrat
     S.inv_pos[(size_t)wave * K + r.rank] = pos;
     S.perm_rows[pos] = wave;
     S.perm_w[pos] = w;
+    if (S.tile_desc) {
+      // The token's place in its group's record (one tile per active group).
+      const int slot = __popcll(active_mask & ((1ull << lane) - 1ull));
+      S.tile_desc[(size_t)slot * kTileDescInts + 4 + before] = wave;
+    }
   }
   if (wave == 0) {
     if (lane < E) S.offsets[lane] = start[lane];
@@ -731,6 +764,12 @@ __device__ __forceinline__ void route_dispatch(const DeviceLayer& L, const Scrat
     if (active) {
       S.tiles[2 * slot] = lane;
       S.tiles[2 * slot + 1] = 0;
+      if (S.tile_desc) {
+        int* d = S.tile_desc + (size_t)slot * kTileDescInts;
+        d[0] = lane;
+        d[1] = start[lane];
+        d[2] = count[lane];
+      }
     }
     const int n_active = __popcll(am);
     if (lane == 0) {

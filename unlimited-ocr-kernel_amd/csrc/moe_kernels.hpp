@@ -83,6 +83,11 @@ struct Scratch {
   int* tiles;       // [max_tiles*2] (group, first row) per row tile
   int* counters;    // [4]: row tiles, routed row tiles
   int* chunk_counts;  // [ceil(T/16), 64] per-chunk expert counts (router)
+  // Small router (T <= 16): one record of kTileDescInts per routed tile
+  // (group, first dispatched position, rows, one unused word, then the
+  // rows' tokens), so that a unit reads its tile with one load; null: none
+  // (units read the tile list, the expert offsets and the permutation).
+  int* tile_desc;
   float* h;         // [T*K, I] routed hidden in dispatched order
   float* hs;        // [T, S] shared hidden
   float* y;         // [T*K, H] routed expert outputs in dispatched order
@@ -104,6 +109,7 @@ struct Scratch {
 };
 
 int max_tiles(int T, int K, int E, int bm);
+constexpr int kTileDescInts = 32;  // one 128-byte line per record
 
 // route.hip
 void launch_router_logits(const float* x, const uint16_t* w, int T, int H, int E, float* logits,
