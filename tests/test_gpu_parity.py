@@ -414,6 +414,19 @@ def test_decode_edge_shapes(ctx, quant):
         check_layer(case, ctx, syn.activations(1, DECODE_EDGE["hidden"], seed=1300 + i))
 
 
+@pytest.mark.parametrize("T,flags", [(5, 0), (16, 0), (40, um.FLAG_FORCE_GEMV)])
+@pytest.mark.parametrize("quant", [orc.QUANT_NONE, orc.QUANT_WEIGHTS_ONLY, orc.QUANT_DYNAMIC])
+def test_small_batch_wide_hidden(ctx, quant, T, flags):
+    """The small-batch engine at a hidden width beyond 1280 (rows held in
+    its 2048-wide instantiations): in INT8 weight-only layers the shared
+    expert's MFMA units then head the gate/up and down launches instead of
+    running beside the router; T = 40 forces the engine past 16 tokens
+    (several 16-token shared tiles, the chunked dispatch)."""
+    case = Case(ctx, DECODE_EDGE, 8, seed=1600 + T, quant=quant)
+    say(f"small batch hidden 2048 quant={quant} T={T}")
+    check_layer(case, ctx, syn.activations(T, DECODE_EDGE["hidden"], seed=1700 + T), flags=flags)
+
+
 @pytest.mark.parametrize("shape,K,T,flags", [(DECODE_EDGE, 8, 17, 0),
                                              (WIDE, 2, 5, um.FLAG_FORCE_MFMA)],
                          ids=["hidden2048", "inter1088"])
