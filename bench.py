@@ -21,7 +21,9 @@ with Zipf(1.1) expert popularity in both activation precision classes, the
 INT8-overlay layer at 512 tokens with uniform routing (W8A8 under
 DynamicActivations, and weight-only), and
 the vocabulary projection (final RMSNorm + 129280 x 1280 lm_head) in BF16,
-INT8 weight-only and W8A8.
+INT8 weight-only and W8A8. On request only (--secondary): the 16-token
+forward with BF16 weights (decode_bf16_t16) and under DynamicActivations
+(decode_w8a8_t16).
 
 The CPU baseline is the C oracle (a restatement of the reference's scalar
 x86 path) on a bounded sample of the headline workload at 1, 8 and 16
@@ -531,7 +533,9 @@ def main():
     for key, quant, T in (("decode_int8", um.QUANT_WEIGHTS_ONLY, 1),
                           ("decode_bf16", um.QUANT_NONE, 1),
                           ("decode_w8a8", um.QUANT_DYNAMIC, 1),
-                          ("decode_int8_t16", um.QUANT_WEIGHTS_ONLY, 16)):
+                          ("decode_int8_t16", um.QUANT_WEIGHTS_ONLY, 16),
+                          ("decode_bf16_t16", um.QUANT_NONE, 16),
+                          ("decode_w8a8_t16", um.QUANT_DYNAMIC, 16)):
         if key in wanted:
             secondary.append(decode(quant, T))
 

@@ -411,28 +411,29 @@ __attribute__((amdgpu_waves_per_eu(3))) void batch_down_kernel(
     down_body<KIND, true, DYN>(L, S, sm, u);
 }
 
-// MFMA form of the shared expert's units in INT8 weight-only layers: a tile
-// of up to 16 tokens times one or two sets of 16 weight rows (gate and up
-// rows of 16 hidden values, or 16 or 32 down rows), as
-// v_mfma_f32_16x16x32_bf16 products. A = the tokens' activations as bf16
-// hi and lo parts (FP32-class: the input rows split as they are loaded, the
-// hidden rows handed over as k-blocked [K/32][rows][32] planes); B = 16 rows
-// of one 32-block from the k-blocked int8 panels, each int8 exact in bf16;
-// one partial per block and row set, folded into the accumulator with the
-// rows' block scales (Decoder::projection, src/decoder/mod.rs:99-112, with
-// the scale applied per 32-block). Wave w of the unit's four takes the w-th
-// quarter of the blocks; the four partial tiles meet in LDS, summed in wave
-// order. The MFMA costs the same for 1 or 16 tokens, so the shared tiles
-// take 16 rows; routed tiles (about two tokens each) stay on the dot, where
-// a 16-row A operand's loads cost more than the MFMA saves (the 16-token
-// forward's gate/up launch took 50.7 instead of 35.2 us with every unit in
-// MFMA form).
+// MFMA form of the shared expert's units: a tile of up to 16 tokens times
+// one or two sets of 16 weight rows (gate and up rows of 16 hidden values,
+// or 16 or 32 down rows), as v_mfma_f32_16x16x32_bf16 products. A = the
+// tokens' activations as bf16 hi and lo parts (FP32-class: the input rows
+// split as they are loaded, the hidden rows handed over as k-blocked
+// [K/32][rows][32] planes); B = 16 rows of one 32-block from the k-blocked
+// panels: BF16 weights as stored, or INT8 rows widened to bf16 (exact),
+// whose per-block partial is folded into the accumulator with the rows'
+// block scales (Decoder::projection, src/decoder/mod.rs:99-112, with the
+// scale applied per 32-block; under DynamicActivations the shared group
+// of T >= 2 rows is weight-only, :103-104). Wave w of the unit's four
+// takes the w-th quarter of the blocks; the four partial tiles meet in
+// LDS, summed in wave order. The MFMA costs the same for 1 or 16 tokens,
+// so the shared tiles take 16 rows; routed tiles (about two tokens each)
+// stay on the dot, where a 16-row A operand's loads cost more than the
+// MFMA saves (the 16-token INT8 forward's gate/up launch took 50.7 instead
+// of 35.2 us with every unit in MFMA form).
 //
 // Where they run (2 <= T <= 16, hidden width <= 1280): the shared gate/up
 // units in the router's launch, beside its logit workgroups (they need no
 // routing), and the shared down units at the head of the gate/up launch;
-// the down launch then holds routed units only. Otherwise the shared units
-// head the gate/up and down launches.
+// the down launch then holds routed units only. Otherwise (INT8 layers
+// only) the shared units head the gate/up and down launches.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -464,41 +465,51 @@ __device__ __forceinline__ bf16x8 widen_q8(u32x2 q) {
 }
 
 // Rows ra (and, with NSET = 2, rb) -- this lane's column of each row set --
-// of a k-blocked int8 panel [K/32][rows][32] with row-major block scales
-// [rows][K/32], dotted with activation row xrow: with F32X, FP32 rows
-// [prows][K] split into bf16 hi and lo parts here; otherwise bf16 planes
-// (hi at `act`, lo prows * K elements later, k-blocked [K/32][prows][32]).
-// acc_a / acc_b hold this wave's blocks' sums for tokens 4 (lane / 16) ..
-// + 3. Rows outside [0, rows) read as zero. Lanes are numbered within the
-// unit's four waves (threadIdx.x mod 256).
-template <int KMAX, int NSET, bool F32X>
-__device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* scales, int rows,
+// of a k-blocked panel [K/32][rows][32] (BF16, or INT8 with row-major block
+// scales [rows][K/32]), dotted with activation row xrow: with F32X, FP32
+// rows [prows][K] split into bf16 hi and lo parts here; otherwise bf16
+// planes (hi at `act`, lo prows * K elements later, k-blocked
+// [K/32][prows][32]). acc_a / acc_b hold this wave's blocks' sums for tokens
+// 4 (lane / 16) .. + 3. Rows outside [0, rows) read as zero. Lanes are
+// numbered within the unit's four waves (threadIdx.x mod 256).
+template <int KIND, int KMAX, int NSET, bool F32X>
+__device__ __forceinline__ void mfma_rows_dot(const void* panel, const float* scales, int rows,
                                               int K, int ra, int rb, const void* act, int prows,
                                               int xrow, f32x4& acc_a, f32x4& acc_b) {
+  constexpr bool kQ8 = KIND == kInt8;
   const int wave = (threadIdx.x >> 6) & 3, grp = (threadIdx.x >> 4) & 3;
   const int nblk = K / kQBlock;
   constexpr int kBW = KMAX / kQBlock / kMfmaWaves;  // blocks per wave, at most
+  constexpr int kB2 = NSET == 2 ? kBW : 1;
+  constexpr uint32_t kRowB = kQ8 ? 32u : 64u;       // bytes per row and block
   const int per = (nblk + kMfmaWaves - 1) / kMfmaWaves;
   const int kb0 = wave * per;
-  // Weights and scales first (they need only the group).
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(panel, (uint32_t)rows * (uint32_t)K);
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(scales, (uint32_t)rows * (uint32_t)nblk * 4u);
-  u32x2 qa[kBW], qb[NSET == 2 ? kBW : 1];
-  float sa[kBW], sb[NSET == 2 ? kBW : 1];
+  // Weights (and scales) first: they need only the group.
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(panel, (uint32_t)rows * (uint32_t)K * (kRowB / 32u));
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(kQ8 ? (const void*)scales : panel, kQ8 ? (uint32_t)rows * (uint32_t)nblk * 4u : 0u);
+  u32x2 qa[kQ8 ? kBW : 1], qb[kQ8 ? kB2 : 1];
+  u32x4 ha[kQ8 ? 1 : kBW], hb[kQ8 ? 1 : kB2];
+  float sa[kQ8 ? kBW : 1], sb[kQ8 ? kB2 : 1];
 #pragma unroll
   for (int i = 0; i < kBW; i++) {
     const int kb = kb0 + i;
     const bool ok = i < per && kb < nblk;
     const uint32_t at = (uint32_t)kb * rows;
-    qa[i] = __builtin_amdgcn_raw_buffer_load_b64(
-        wr, ok && ra < rows ? ((at + ra) * 32u + 8u * grp) : kOut, 0, 0);
-    sa[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        sr, ok && ra < rows ? ((uint32_t)ra * nblk + kb) * 4u : kOut, 0, 0));
-    if constexpr (NSET == 2) {
-      qb[i] = __builtin_amdgcn_raw_buffer_load_b64(
-          wr, ok && rb < rows ? ((at + rb) * 32u + 8u * grp) : kOut, 0, 0);
-      sb[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-          sr, ok && rb < rows ? ((uint32_t)rb * nblk + kb) * 4u : kOut, 0, 0));
+    const uint32_t oa = ok && ra < rows ? (at + ra) * kRowB + (kRowB / 4u) * grp : kOut;
+    const uint32_t ob = ok && rb < rows ? (at + rb) * kRowB + (kRowB / 4u) * grp : kOut;
+    if constexpr (kQ8) {
+      qa[i] = __builtin_amdgcn_raw_buffer_load_b64(wr, oa, 0, 0);
+      sa[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          sr, ok && ra < rows ? ((uint32_t)ra * nblk + kb) * 4u : kOut, 0, 0));
+      if constexpr (NSET == 2) {
+        qb[i] = __builtin_amdgcn_raw_buffer_load_b64(wr, ob, 0, 0);
+        sb[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            sr, ok && rb < rows ? ((uint32_t)rb * nblk + kb) * 4u : kOut, 0, 0));
+      }
+    } else {
+      ha[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, oa, 0, 0);
+      if constexpr (NSET == 2) hb[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, ob, 0, 0);
     }
   }
   const uint32_t plane = (uint32_t)prows * (uint32_t)K;  // elements per plane or per row set
@@ -530,18 +541,29 @@ __device__ __forceinline__ void mfma_rows_dot(const int8_t* panel, const float* 
       xl = __builtin_bit_cast(
           bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at + plane * 2u : kOut, 0, 0));
     }
-    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    const bf16x8 wa = widen_q8(qa[i]);
-    f32x4 pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wa, z, 0, 0, 0);
-    pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wa, pa, 0, 0, 0);
+    if constexpr (kQ8) {
+      const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+      const bf16x8 wa = widen_q8(qa[i]);
+      f32x4 pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wa, z, 0, 0, 0);
+      pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wa, pa, 0, 0, 0);
 #pragma unroll
-    for (int r = 0; r < 4; r++) acc_a[r] = __builtin_fmaf(pa[r], sa[i], acc_a[r]);
-    if constexpr (NSET == 2) {
-      const bf16x8 wb = widen_q8(qb[i]);
-      f32x4 pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, z, 0, 0, 0);
-      pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, pb, 0, 0, 0);
+      for (int r = 0; r < 4; r++) acc_a[r] = __builtin_fmaf(pa[r], sa[i], acc_a[r]);
+      if constexpr (NSET == 2) {
+        const bf16x8 wb = widen_q8(qb[i]);
+        f32x4 pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, z, 0, 0, 0);
+        pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, pb, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc_b[r] = __builtin_fmaf(pb[r], sb[i], acc_b[r]);
+        for (int r = 0; r < 4; r++) acc_b[r] = __builtin_fmaf(pb[r], sb[i], acc_b[r]);
+      }
+    } else {
+      const bf16x8 wa = __builtin_bit_cast(bf16x8, ha[i]);
+      acc_a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wa, acc_a, 0, 0, 0);
+      acc_a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wa, acc_a, 0, 0, 0);
+      if constexpr (NSET == 2) {
+        const bf16x8 wb = __builtin_bit_cast(bf16x8, hb[i]);
+        acc_b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb, acc_b, 0, 0, 0);
+        acc_b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb, acc_b, 0, 0, 0);
+      }
     }
   }
 }
@@ -575,7 +597,7 @@ __device__ __forceinline__ uint16_t* shared_hidden_planes(const Scratch& S) {
 // of the input rows; h = silu(gate) * up (src/decoder/mod.rs:114-122) goes
 // to the hidden planes. A unit that is not `live` still takes part in the
 // workgroup's barrier and stores nothing.
-template <int KH>
+template <int KIND, int KH>
 __device__ __forceinline__ void shared_gateup_mfma(const DeviceLayer& L, const Scratch& S,
                                                    MfmaUnitSmem& sm, int slice, int r0, int n,
                                                    int T, bool live) {
@@ -583,8 +605,10 @@ __device__ __forceinline__ void shared_gateup_mfma(const DeviceLayer& L, const S
   const int k0 = 16 * slice;
   const int ra = live ? gate_row(k0) + col : 2 * W;
   f32x4 ag, au;
-  mfma_rows_dot<KH, 2, true>(L.q13k + L.w13_offset(L.E), L.s13 + L.s13_offset(L.E), 2 * W, L.H,
-                             ra, ra + 32, S.xn, T, r0 + min(col, n - 1), ag, au);
+  const void* panel = KIND == kInt8 ? (const void*)(L.q13k + L.w13_offset(L.E))
+                                    : (const void*)(L.w13k + L.w13_offset(L.E));
+  mfma_rows_dot<KIND, KH, 2, true>(panel, KIND == kInt8 ? L.s13 + L.s13_offset(L.E) : nullptr,
+                                   2 * W, L.H, ra, ra + 32, S.xn, T, r0 + min(col, n - 1), ag, au);
   float g, up;
   mfma_reduce(sm, ag, au, g, up);
   const int c = threadIdx.x & 15, t = (threadIdx.x >> 4) & 15, k = k0 + c;
@@ -600,15 +624,17 @@ __device__ __forceinline__ void shared_gateup_mfma(const DeviceLayer& L, const S
 }
 
 // Shared down unit: output features 16 NSET slice .. for tokens [r0, r0 + n).
-template <int NSET>
+template <int KIND, int NSET>
 __device__ __forceinline__ void shared_down_mfma(const DeviceLayer& L, const Scratch& S,
                                                  MfmaUnitSmem& sm, int slice, int r0, int n, int T) {
   const int W = L.S, col = threadIdx.x & 15;
   const int n0 = 16 * NSET * slice;
   f32x4 aa, ab;
-  mfma_rows_dot<kWideK, NSET, false>(L.q2k + L.w2_offset(L.E), L.s2 + L.s2_offset(L.E), L.H, W,
-                                     n0 + col, n0 + 16 + col, shared_hidden_planes(S), T,
-                                     r0 + min(col, n - 1), aa, ab);
+  const void* panel = KIND == kInt8 ? (const void*)(L.q2k + L.w2_offset(L.E))
+                                    : (const void*)(L.w2k + L.w2_offset(L.E));
+  mfma_rows_dot<KIND, kWideK, NSET, false>(panel, KIND == kInt8 ? L.s2 + L.s2_offset(L.E) : nullptr,
+                                           L.H, W, n0 + col, n0 + 16 + col,
+                                           shared_hidden_planes(S), T, r0 + min(col, n - 1), aa, ab);
   float ya, yb;
   mfma_reduce(sm, aa, ab, ya, yb);
   const int c = threadIdx.x & 15, t = (threadIdx.x >> 4) & 15;
@@ -619,56 +645,71 @@ __device__ __forceinline__ void shared_down_mfma(const DeviceLayer& L, const Scr
   }
 }
 
+// Whether the shared expert's units take the MFMA form: weight-only math
+// on its group (not the single-row W8A8 group of a one-token forward under
+// DynamicActivations). BF16 weights: up to 1280 hidden values and 16
+// tokens (their two-set down units would not fit the registers beyond);
+// DynamicActivations: up to 1280 hidden values (the wider W8A8 gate/up
+// kernel has no registers to spare).
+__host__ __device__ inline bool mfma_shared(const DeviceLayer& L, int T) {
+  if (L.S <= 0 || L.S % 32 != 0) return false;
+  if (L.quant_mode == kQuantWeightsOnly) return true;
+  if (L.quant_mode == kQuantNone) return L.H <= 1280 && T <= kTileRows;
+  return L.H <= 1280 && T >= 2;  // DynamicActivations
+}
+
 // Whether the router's launch runs the shared gate/up units (then the
 // gate/up launch runs the shared down units, 16 rows each).
 __host__ __device__ inline bool shared_in_router(const DeviceLayer& L, int T) {
-  return L.quant_mode == kQuantWeightsOnly && L.S % 32 == 0 && L.S > 0 && L.H <= 1280 &&
-         T <= kTileRows;
+  return mfma_shared(L, T) && L.H <= 1280 && T <= kTileRows;
 }
 
-// Gate/up launch of INT8 weight-only layers: sdn shared down units (16
-// rows of the one shared tile), then sgu shared gate/up units (16-token
-// tiles, (S + 15) / 16 per tile), then the routed units on the dot.
-template <int KH>
+// Gate/up launch with MFMA shared units: sdn shared down units (16 rows of
+// the one shared tile), then sgu shared gate/up units (16-token tiles,
+// (S + 15) / 16 per tile), then the routed units on the dot.
+template <int KIND, int KH, bool DYN>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(KH <= 1280 ? 4 : 3))) void batch_gateup_ms_kernel(
+__attribute__((amdgpu_waves_per_eu(batch_waves<KIND, KH, DYN>()))) void batch_gateup_ms_kernel(
     DeviceLayer L, Scratch S, int T, int mchunk, int sdn, int sgu) {
   __shared__ __align__(16) SharedSmem sm;
   int b = blockIdx.x;
   if (b < sdn) {
-    shared_down_mfma<1>(L, S, sm.m, b, 0, T, T);
+    shared_down_mfma<KIND, 1>(L, S, sm.m, b, 0, T, T);
     return;
   }
   b -= sdn;
   if (b < sgu) {
     const int us = (L.S + 15) / 16, ts = b / us;
     const int r0 = ts * kMfmaSharedRows;
-    shared_gateup_mfma<KH>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T, true);
+    shared_gateup_mfma<KIND, KH>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T, true);
     return;
   }
   Unit u;
-  if (routed_unit(S, mchunk, (L.I + 15) / 16, b - sgu, u)) gateup_body<kInt8, KH, false>(L, S, sm.b, u);
+  if (routed_unit(S, mchunk, (L.I + 15) / 16, b - sgu, u)) gateup_body<KIND, KH, DYN>(L, S, sm.b, u);
 }
 
-// Down launch of INT8 weight-only layers: sdn shared down units (32 rows of
-// one 16-token tile), then the routed units on the dot.
+// Down launch with MFMA shared units: sdn shared down units (32 rows of one
+// 16-token tile; INT8 only), then the routed units on the dot.
+template <int KIND, bool DYN>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(3))) void batch_down_ms_kernel(DeviceLayer L, Scratch S, int T,
                                                                  int mchunk, int sdn) {
   __shared__ __align__(16) SharedSmem sm;
   const int b = blockIdx.x;
-  if (b < sdn) {
-    const int us = L.H / 32, ts = b / us;
-    const int r0 = ts * kMfmaSharedRows;
-    shared_down_mfma<2>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T);
-    return;
+  if constexpr (KIND == kInt8) {
+    if (b < sdn) {
+      const int us = L.H / 32, ts = b / us;
+      const int r0 = ts * kMfmaSharedRows;
+      shared_down_mfma<KIND, 2>(L, S, sm.m, b - ts * us, r0, min(kMfmaSharedRows, T - r0), T);
+      return;
+    }
   }
   Unit u;
   if (!routed_unit(S, mchunk, down_units(L.H, L.I), b - sdn, u)) return;
   if (L.I <= kSegK)
-    down_body<kInt8, false, false>(L, S, sm.b, u);
+    down_body<KIND, false, DYN>(L, S, sm.b, u);
   else
-    down_body<kInt8, true, false>(L, S, sm.b, u);
+    down_body<KIND, true, DYN>(L, S, sm.b, u);
 }
 
 // Down of the single-row W8A8 groups; HALVES as down_body (routed width
@@ -799,10 +840,12 @@ __global__ __launch_bounds__(64 * kRouteWaves) void small_route_kernel(const flo
   const int id = (int)blockIdx.x;
   if (id >= n_route) {
     if constexpr (KH <= 1280) {
-      if (wave < kMfmaWaves)
-        shared_gateup_mfma<KH>(L, S, su, id - n_route, 0, T, T, true);
-      else
+      if (wave >= kMfmaWaves)
         __syncthreads();  // the unit's one barrier
+      else if (L.quant_mode == kQuantNone)
+        shared_gateup_mfma<kBF16, KH>(L, S, su, id - n_route, 0, T, T, true);
+      else
+        shared_gateup_mfma<kInt8, KH>(L, S, su, id - n_route, 0, T, T, true);
     }
     return;
   }
@@ -869,17 +912,24 @@ dim3 singles_grid(const DeviceLayer& L, int T, int ur) {
 template <int KIND>
 void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
                         int mchunk, hipStream_t s, bool shared_only) {
-  if (KIND == kInt8 && batch_mfma_shared(L)) {
+  if (mfma_shared(L, T)) {
     const bool in_router = shared_in_router(L, T);
     const int nsh = (T + kMfmaSharedRows - 1) / kMfmaSharedRows;
     const int sdn = in_router ? L.H / 16 : 0;
     const int sgu = in_router ? 0 : nsh * ((L.S + 15) / 16);
     const int units = sdn + sgu +
                       (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * ((L.I + 15) / 16));
-    if (L.H <= 1280)
-      batch_gateup_ms_kernel<1280><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, sdn, sgu);
-    else
-      batch_gateup_ms_kernel<kWideK><<<dim3(units), dim3(256), 0, s>>>(L, S, T, mchunk, sdn, sgu);
+    const dim3 grid(units), block(256);
+    if constexpr (KIND == kBF16) {
+      batch_gateup_ms_kernel<kBF16, 1280, false><<<grid, block, 0, s>>>(L, S, T, mchunk, sdn, sgu);
+    } else if (L.quant_mode == kQuantDynamic) {
+      batch_gateup_ms_kernel<kInt8, 1280, true><<<grid, block, 0, s>>>(L, S, T, mchunk, sdn, sgu);
+    } else {
+      if (L.H <= 1280)
+        batch_gateup_ms_kernel<kInt8, 1280, false><<<grid, block, 0, s>>>(L, S, T, mchunk, sdn, sgu);
+      else
+        batch_gateup_ms_kernel<kInt8, kWideK, false><<<grid, block, 0, s>>>(L, S, T, mchunk, sdn, sgu);
+    }
     return;
   }
   const int nsh = (T + kSharedRows - 1) / kSharedRows;
@@ -900,10 +950,6 @@ void launch_gateup_kind(const DeviceLayer& L, const Scratch& S, int T, int tiles
 }
 
 }  // namespace
-
-bool batch_mfma_shared(const DeviceLayer& L) {
-  return L.quant_mode == kQuantWeightsOnly && L.S % 32 == 0 && L.S > 0;
-}
 
 bool batch_supported(const DeviceLayer& L) {
   // Down rows are held as one segment up to kSegK or as two halves.
@@ -941,12 +987,17 @@ void launch_batch_down(const DeviceLayer& L, const Scratch& S, int T, int tiles_
   const int units = nsh * down_units(L.H, L.S) +
                     (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) * down_units(L.H, L.I));
   const dim3 grid(units), block(256);
-  if (batch_mfma_shared(L)) {
+  if (mfma_shared(L, T)) {
     const int sdn = shared_in_router(L, T) ? 0
                                            : (T + kMfmaSharedRows - 1) / kMfmaSharedRows * (L.H / 32);
-    const int units16 = sdn + (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) *
-                                                     down_units(L.H, L.I));
-    batch_down_ms_kernel<<<dim3(units16), block, 0, s>>>(L, S, T, mchunk, sdn);
+    const dim3 grid16(sdn + (shared_only ? 0 : routed_bound(L, T, tiles_bound, mchunk) *
+                                                   down_units(L.H, L.I)));
+    if (L.quant_mode == kQuantNone)
+      batch_down_ms_kernel<kBF16, false><<<grid16, block, 0, s>>>(L, S, T, mchunk, sdn);
+    else if (L.quant_mode == kQuantDynamic)
+      batch_down_ms_kernel<kInt8, true><<<grid16, block, 0, s>>>(L, S, T, mchunk, sdn);
+    else
+      batch_down_ms_kernel<kInt8, false><<<grid16, block, 0, s>>>(L, S, T, mchunk, sdn);
     return;
   }
   if (L.quant_mode == 0)

@@ -159,10 +159,6 @@ void launch_dispatch(const int* ids, const float* w, int T, int E, int K, int bm
 // math, INT8 weight-only and W8A8), and the small-batch router (T <= 16):
 // logits, then one workgroup that routes and builds the dispatch.
 bool batch_supported(const DeviceLayer& L);
-// Whether the small-batch engine's shared-expert units take the MFMA form
-// (INT8 weight-only layers; up to 1280 hidden values and 16 tokens the
-// small router's launch also runs the shared gate/up units).
-bool batch_mfma_shared(const DeviceLayer& L);
 // shared_only: the shared expert's units only (the MFMA engine at one
 // token under DynamicActivations, where the shared group is a single row).
 void launch_batch_gateup(const DeviceLayer& L, const Scratch& S, int T, int tiles_bound,
