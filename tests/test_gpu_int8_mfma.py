@@ -109,6 +109,12 @@ def test_int8_mode_block_sums_and_outputs(setup, T):
     err = normwise(y[rows], ref)
     say(f"  normwise {err:.3e} over {len(rows)} rows")
     assert err <= W8A8_TOL, err
+    # Without a trace the GEMMs run as their own kernel instantiation (no
+    # block-sum stores): the same arithmetic, so the same bits.
+    y2 = torch.full_like(xd, float("nan"))
+    um.forward(ctx, layer, xd, y2, flags=um.FLAG_INT8_MFMA)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().view(np.uint32), y.view(np.uint32))
 
 
 def test_int8_mode_needs_dynamic_activations(setup):

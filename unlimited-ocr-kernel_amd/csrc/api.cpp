@@ -921,7 +921,10 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   const size_t H = L.H, I = L.I, S = L.S, E = L.E;
   const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
   void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr, *q13k = nullptr, *q2k = nullptr,
-       *s2k = nullptr;
+       *s2k = nullptr, *s13k = nullptr;
+  // Only DynamicActivations overlays can run the int8 x int8 mode, the one
+  // reader of the block-major gate/up scales.
+  const bool dynamic = mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS;
   std::vector<void*> fresh;
   auto alloc = [&](size_t bytes, void** p) -> hipError_t {
     hipError_t e = hipMalloc(p, bytes);
@@ -939,6 +942,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   if (e == hipSuccess) e = alloc(n13, &q13k);
   if (e == hipSuccess) e = alloc(n2, &q2k);
   if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2k);
+  if (e == hipSuccess && dynamic) e = alloc(n13 / 32 * 4, &s13k);
   if (e != hipSuccess) return release(hip_fail(e, "INT8 allocation"));
   const hipMemcpyKind kind = kind_of(where);
   hipStream_t st = ctx->stream;
@@ -981,6 +985,14 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   uocr::launch_transpose_f32(static_cast<const float*>(s2) + E * H * (I / 32),
                              static_cast<float*>(s2k) + E * H * (I / 32), (int)H, (int)(S / 32), 1,
                              st);
+  // The int8 x int8 mode's block-major gate/up scales ([H/32][2W] per group).
+  if (dynamic) {
+    uocr::launch_transpose_f32(static_cast<const float*>(s13), static_cast<float*>(s13k),
+                               (int)(2 * I), (int)(H / 32), (int)E, st);
+    uocr::launch_transpose_f32(static_cast<const float*>(s13) + E * 2 * I * (H / 32),
+                               static_cast<float*>(s13k) + E * 2 * I * (H / 32), (int)(2 * S),
+                               (int)(H / 32), 1, st);
+  }
   // Validate the uploaded values on the device.
   HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), st), "clear flag");
   hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q13, n13,
@@ -994,7 +1006,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   }
   // Replace any previous overlay.
   for (void* p : {(void*)L.q13, (void*)L.s13, (void*)L.q2, (void*)L.s2, (void*)L.q13k, (void*)L.q2k,
-                  (void*)L.s2k}) {
+                  (void*)L.s2k, (void*)L.s13k}) {
     if (!p) continue;
     for (auto it = layer->allocations.begin(); it != layer->allocations.end(); ++it)
       if (*it == p) {
@@ -1004,7 +1016,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     (void)hipFree(p);
   }
   for (void* p : fresh) layer->allocations.push_back(p);
-  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + 2 * (n2 / 32 * 4);
+  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + 2 * (n2 / 32 * 4) + (dynamic ? n13 / 32 * 4 : 0);
   L.q13 = static_cast<const int8_t*>(q13);
   L.s13 = static_cast<const float*>(s13);
   L.q2 = static_cast<const int8_t*>(q2);
@@ -1012,6 +1024,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   L.q13k = static_cast<const int8_t*>(q13k);
   L.q2k = static_cast<const int8_t*>(q2k);
   L.s2k = static_cast<const float*>(s2k);
+  L.s13k = static_cast<const float*>(s13k);
   L.quant_mode = mode;
   layer->quant_mode = mode;
   return UOCR_OK;

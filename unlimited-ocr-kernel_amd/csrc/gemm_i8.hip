@@ -34,6 +34,7 @@ constexpr int kI8TileM = 64;   // token rows per item
 constexpr int kI8TileN = 256;  // output features per item
 constexpr int kI8Stages = 4;   // LDS ring depth
 constexpr int kI8Threads = 256;
+constexpr int kI8WgPerCu = 3;  // 3 x 46 KB of LDS rings; <= 168 VGPRs per lane
 constexpr int kI8Xcds = 8;
 
 // Stage layout (bytes): token rows [64][32], weight rows [256][32], token
@@ -94,9 +95,12 @@ __device__ __forceinline__ int ckpt_row13(int r, int W) {
 // Items: (row tile, column tile), routed tiles first, column tile fastest;
 // workgroup ids reach the XCDs round-robin and are remapped so each XCD
 // takes a contiguous range (an expert's items share one L2).
-template <bool GATEUP>
-__global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scratch S,
-                                                              I8Planes P, int T) {
+// TRACE: the instantiation that also stores every block sum (tests); the
+// plain one carries no trace code, so it fits three workgroups per CU.
+template <bool GATEUP, bool TRACE>
+__global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(DeviceLayer L,
+                                                                          Scratch S, I8Planes P,
+                                                                          int T) {
   extern __shared__ __align__(16) char lds[];
   const int all_tiles = S.counters[0];
   const int routed_tiles = S.counters[1];
@@ -128,7 +132,8 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
   const int base = routed ? S.offsets[g] : 0;
   const int n0 = ntile * kI8TileN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar load plan
 
   // ---- sources. Token rows: gate/up reads the quantised layer input
   // (routed rows gathered through the dispatch permutation), down reads the
@@ -147,8 +152,15 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
     a_rows = routed ? (uint32_t)T * L.K : (uint32_t)T;
     a_row0 = (uint32_t)(base + r0);
   }
-  const int8_t* bq = GATEUP ? L.q13 + L.w13_offset(g) : L.q2 + L.w2_offset(g);
-  const float* bs = GATEUP ? L.s13 + L.s13_offset(g) : L.s2 + L.s2_offset(g);
+  // Weights from the k-blocked panels ([K/32][N][32] per group): stage b's
+  // 32 bytes of the tile's rows are one contiguous run, so every 128-byte
+  // line is read whole in one stage (row-major rows left each line to be
+  // read a quarter per stage, and refetched when it fell out of L2).
+  const int8_t* bq = GATEUP ? L.q13k + L.w13_offset(g) : L.q2k + L.w2_offset(g);
+  // Block scales block-major ([K/32][N] per group): one stage's scales of
+  // the tile's rows are one contiguous run.
+  const float* bs = GATEUP ? L.s13k + L.s13_offset(g) : L.s2k + L.s2_offset(g);
+  const uint32_t bs_row = 4u, bs_blk = (uint32_t)N * 4u;  // bytes per row, per block
   const i32x4 rs_aq = i8_rsrc(aq, a_rows * (uint32_t)K);
   const i32x4 rs_as = i8_rsrc(as, a_rows * (uint32_t)nblk * 4u);
   const i32x4 rs_bq = i8_rsrc(bq, (uint32_t)N * (uint32_t)K);
@@ -176,7 +188,7 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
     } else if (ld < 10) {  // weight rows
       const int r = (ld - 2) * 32 + lane / 2, c = (lane & 1) ^ ((r >> 3) & 1);
       kind[j] = 1;
-      off[j] = n0 + r < N ? (uint32_t)(n0 + r) * (uint32_t)K + 16u * c : kI8Out;
+      off[j] = n0 + r < N ? (uint32_t)(n0 + r) * 32u + 16u * c : kI8Out;
       lds_at[j] = kI8BAt + (uint32_t)(ld - 2) * 1024u;
     } else if (ld == 10) {  // token scales: 64 rows, one dword each
       const int src = a_source(lane);
@@ -186,7 +198,7 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
     } else {  // weight scales: 4 x 64 rows
       const int r = (ld - 11) * 64 + lane;
       kind[j] = 3;
-      off[j] = n0 + r < N ? (uint32_t)(n0 + r) * (uint32_t)nblk * 4u : kI8Out;
+      off[j] = n0 + r < N ? (uint32_t)(n0 + r) * bs_row : kI8Out;
       lds_at[j] = kI8BSAt + (uint32_t)(ld - 11) * 256u;
     }
   }
@@ -198,9 +210,9 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(st + lds_at[j]);
       const bool out = off[j] == kI8Out;
       if (kind[j] == 0) i8_load16(rs_aq, m0, out ? kI8Out : off[j] + 32u * b);
-      else if (kind[j] == 1) i8_load16(rs_bq, m0, out ? kI8Out : off[j] + 32u * b);
+      else if (kind[j] == 1) i8_load16(rs_bq, m0, out ? kI8Out : off[j] + 32u * N * b);
       else if (kind[j] == 2) i8_load4(rs_as, m0, out ? kI8Out : off[j] + 4u * b);
-      else i8_load4(rs_bs, m0, out ? kI8Out : off[j] + 4u * b);
+      else i8_load4(rs_bs, m0, out ? kI8Out : off[j] + bs_blk * b);
     }
   };
 
@@ -220,8 +232,10 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
   // Trace of the exact block sums (tests): routed rows by dispatched
   // position, the shared expert's only when it has a single row.
   int32_t* trace = nullptr;
-  if (routed) trace = GATEUP ? S.q8.gateup : S.q8.down;
-  else if (T == 1) trace = GATEUP ? S.q8.s_gateup : S.q8.s_down;
+  if constexpr (TRACE) {
+    if (routed) trace = GATEUP ? S.q8.gateup : S.q8.down;
+    else if (T == 1) trace = GATEUP ? S.q8.s_gateup : S.q8.s_down;
+  }
 
   constexpr int kDepth = kI8Stages - 1;
   for (int i = 0; i < kDepth; i++)
@@ -247,31 +261,38 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
       const int r = 32 * tt + fr;
       xf[tt] = *reinterpret_cast<const i32x4*>(cur + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
     }
-    float xsv[2], wsv[2][16];
+    float xsv[2];
 #pragma unroll
     for (int tt = 0; tt < 2; tt++)
       xsv[tt] = *reinterpret_cast<const float*>(cur + kI8ASAt + (32 * tt + fr) * 4);
 #pragma unroll
-    for (int ft = 0; ft < 2; ft++)
+    for (int ft = 0; ft < 2; ft++) {
+      // This feature tile's 16 weight scales (lane features 8 q + 4 fc + 0..3).
+      float wsv[16];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const float4 v = *reinterpret_cast<const float4*>(
             cur + kI8BSAt + (wcol + 32 * ft + 8 * q + 4 * fc) * 4);
-        wsv[ft][4 * q + 0] = v.x;
-        wsv[ft][4 * q + 1] = v.y;
-        wsv[ft][4 * q + 2] = v.z;
-        wsv[ft][4 * q + 3] = v.w;
+        wsv[4 * q + 0] = v.x;
+        wsv[4 * q + 1] = v.y;
+        wsv[4 * q + 2] = v.z;
+        wsv[4 * q + 3] = v.w;
       }
+      // Both token tiles' products issued before either fold, so one
+      // MFMA runs while the other's sums are scaled (the compiler otherwise
+      // serialises them on one result register set).
+      i32x16 p[2];
 #pragma unroll
-    for (int ft = 0; ft < 2; ft++)
+      for (int tt = 0; tt < 2; tt++)
+        p[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ft], xf[tt], i32x16{}, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int tt = 0; tt < 2; tt++) {
-        i32x16 p = {};
-        p = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ft], xf[tt], p, 0, 0, 0);
+        const i32x16 pv = p[tt];
 #pragma unroll
         for (int r = 0; r < 16; r++)
-          acc[ft][tt][r] = acc[ft][tt][r] + ((float)p[r] * wsv[ft][r]) * xsv[tt];
-        if (trace) {
+          acc[ft][tt][r] = acc[ft][tt][r] + ((float)pv[r] * wsv[r]) * xsv[tt];
+        if (TRACE && trace) {
           const int row = 32 * tt + fr;
           if (row < mrows) {
             const size_t pos = routed ? (size_t)(base + r0 + row) : 0;
@@ -280,11 +301,12 @@ __global__ __launch_bounds__(kI8Threads) void i8_group_kernel(DeviceLayer L, Scr
               const int n = n0 + wcol + 32 * ft + 8 * (r >> 2) + 4 * fc + (r & 3);
               if (n >= N) continue;
               const int cr = GATEUP ? ckpt_row13(n, W) : n;
-              trace[(pos * (size_t)N + cr) * nblk + b] = p[r];
+              trace[(pos * (size_t)N + cr) * nblk + b] = pv[r];
             }
           }
         }
       }
+    }
   }
 
   // ---- epilogue
@@ -406,14 +428,20 @@ static unsigned i8_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
 
 void launch_i8_gateup(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
                       int tiles_bound, hipStream_t s) {
-  hipLaunchKernelGGL(i8_group_kernel<true>, dim3(i8_grid(L, tiles_bound, true)), dim3(kI8Threads),
+  const bool trace = S.q8.gateup != nullptr || (T == 1 && S.q8.s_gateup != nullptr);
+  auto* kern = trace ? i8_group_kernel<true, true> : i8_group_kernel<true, false>;
+  hipLaunchKernelGGL(kern,
+                     dim3(i8_grid(L, tiles_bound, true)), dim3(kI8Threads),
                      kI8Stages * kI8Stage, s, L, S, P, T);
 }
 
 void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
                     int tiles_bound, hipStream_t s) {
-  hipLaunchKernelGGL(i8_group_kernel<false>, dim3(i8_grid(L, tiles_bound, false)),
-                     dim3(kI8Threads), kI8Stages * kI8Stage, s, L, S, P, T);
+  const bool trace = S.q8.down != nullptr || (T == 1 && S.q8.s_down != nullptr);
+  auto* kern = trace ? i8_group_kernel<false, true> : i8_group_kernel<false, false>;
+  hipLaunchKernelGGL(kern,
+                     dim3(i8_grid(L, tiles_bound, false)), dim3(kI8Threads),
+                     kI8Stages * kI8Stage, s, L, S, P, T);
 }
 
 }  // namespace uocr

@@ -42,6 +42,9 @@ struct DeviceLayer {
   // scales as [W/32][H] (same group offsets), so one 32-block's scales of
   // every output feature are one contiguous run.
   const float* s2k;
+  // The int8 x int8 mode's copy of s13 block-major ([H/32][2W] per group,
+  // same group offsets); DynamicActivations overlays only, else null.
+  const float* s13k;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
   __host__ __device__ size_t n13() const { return ((size_t)E * 2 * I + 2 * (size_t)S) * H; }
