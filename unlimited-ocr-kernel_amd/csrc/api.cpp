@@ -922,9 +922,6 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   const size_t n13 = (E * 2 * I + 2 * S) * H, n2 = (E * I + S) * H;
   void *q13 = nullptr, *s13 = nullptr, *q2 = nullptr, *s2 = nullptr, *q13k = nullptr, *q2k = nullptr,
        *s2k = nullptr, *s13k = nullptr;
-  // Only DynamicActivations overlays can run the int8 x int8 mode, the one
-  // reader of the block-major gate/up scales.
-  const bool dynamic = mode == UOCR_QUANT_DYNAMIC_ACTIVATIONS;
   std::vector<void*> fresh;
   auto alloc = [&](size_t bytes, void** p) -> hipError_t {
     hipError_t e = hipMalloc(p, bytes);
@@ -942,7 +939,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   if (e == hipSuccess) e = alloc(n13, &q13k);
   if (e == hipSuccess) e = alloc(n2, &q2k);
   if (e == hipSuccess) e = alloc(n2 / 32 * 4, &s2k);
-  if (e == hipSuccess && dynamic) e = alloc(n13 / 32 * 4, &s13k);
+  if (e == hipSuccess) e = alloc(n13 / 32 * 4, &s13k);
   if (e != hipSuccess) return release(hip_fail(e, "INT8 allocation"));
   const hipMemcpyKind kind = kind_of(where);
   hipStream_t st = ctx->stream;
@@ -985,14 +982,12 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
   uocr::launch_transpose_f32(static_cast<const float*>(s2) + E * H * (I / 32),
                              static_cast<float*>(s2k) + E * H * (I / 32), (int)H, (int)(S / 32), 1,
                              st);
-  // The int8 x int8 mode's block-major gate/up scales ([H/32][2W] per group).
-  if (dynamic) {
-    uocr::launch_transpose_f32(static_cast<const float*>(s13), static_cast<float*>(s13k),
-                               (int)(2 * I), (int)(H / 32), (int)E, st);
-    uocr::launch_transpose_f32(static_cast<const float*>(s13) + E * 2 * I * (H / 32),
-                               static_cast<float*>(s13k) + E * 2 * I * (H / 32), (int)(2 * S),
-                               (int)(H / 32), 1, st);
-  }
+  // The MFMA engines' block-major gate/up scales ([H/32][2W] per group).
+  uocr::launch_transpose_f32(static_cast<const float*>(s13), static_cast<float*>(s13k),
+                             (int)(2 * I), (int)(H / 32), (int)E, st);
+  uocr::launch_transpose_f32(static_cast<const float*>(s13) + E * 2 * I * (H / 32),
+                             static_cast<float*>(s13k) + E * 2 * I * (H / 32), (int)(2 * S),
+                             (int)(H / 32), 1, st);
   // Validate the uploaded values on the device.
   HIP_TRY(hipMemsetAsync(ctx->err, 0, sizeof(int), st), "clear flag");
   hipLaunchKernelGGL(check_int8_kernel, dim3(1024), dim3(256), 0, st, (const int8_t*)q13, n13,
@@ -1016,7 +1011,7 @@ int uocr_moe_layer_attach_int8(uocr_gpu_ctx* ctx, uocr_moe_layer* layer,
     (void)hipFree(p);
   }
   for (void* p : fresh) layer->allocations.push_back(p);
-  layer->bytes += 2 * n13 + n13 / 32 * 4 + 2 * n2 + 2 * (n2 / 32 * 4) + (dynamic ? n13 / 32 * 4 : 0);
+  layer->bytes += 2 * n13 + 2 * (n13 / 32 * 4) + 2 * n2 + 2 * (n2 / 32 * 4);
   L.q13 = static_cast<const int8_t*>(q13);
   L.s13 = static_cast<const float*>(s13);
   L.q2 = static_cast<const int8_t*>(q2);

@@ -248,7 +248,8 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   const float* wscale = nullptr;
   if constexpr (Q8) {
     wmat = GATEUP ? (const void*)(L.q13k + L.w13_offset(g)) : (const void*)(L.q2k + L.w2_offset(g));
-    wscale = GATEUP ? L.s13 + L.s13_offset(g) : L.s2 + L.s2_offset(g);
+    // Block scales block-major ([K/32][N] per group).
+    wscale = GATEUP ? L.s13k + L.s13_offset(g) : L.s2k + L.s2_offset(g);
   } else {
     wmat = GATEUP ? (const void*)(L.w13k + L.w13_offset(g)) : (const void*)(L.w2k + L.w2_offset(g));
   }
@@ -264,8 +265,11 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_base + b_at + (uint32_t)segB0 * 1024u);
   const uint32_t lds_a1 = lds_a + (lo_wave ? alo_at : 0u);
   // Q8 scales: part p (0..7) of group q is one dword load per wave, rows
-  // 8 (8 p + wave) .. +7 with their 8 blocks (lane l: row + l / 8, the 32
-  // contiguous bytes of blocks 8 q ..). Position j of row r holds block
+  // 8 (8 p + wave) .. +7 with their 8 blocks (lane l: row + l / 8, blocks
+  // 8 q ..). The source is block-major, so the 8 waves of one part read
+  // 64 consecutive rows of each of the 8 blocks: whole 128-byte lines in
+  // one stage (row-major rows had left each line to be read a quarter per
+  // group, and refetched when it fell out of L2). Position j of row r holds block
   // 8 q + (j ^ sws(r)), so the 32 rows a half-wave reads for one block sit
   // in 32 distinct banks. Group q + 1 travels with the loads of stages
   // 8 q .. 8 q + 7 (part = stage % 8); group 0 before the first stage.
@@ -275,7 +279,7 @@ __device__ __forceinline__ void mfma_item(const DeviceLayer& L, const Scratch& S
   auto issue_scales = [&](int q, int part) {
     const int r = (part * WAVES + wave) * 8 + lane / 8;
     const int blk = q * kSGroup + ((lane % 8) ^ sws(r));
-    const uint32_t off = n0 + r < N && blk < nblk ? ((uint32_t)(n0 + r) * nblk + blk) * 4u : kDmaOut;
+    const uint32_t off = n0 + r < N && blk < nblk ? ((uint32_t)blk * N + n0 + r) * 4u : kDmaOut;
     const uint32_t dst = lds_base + sg_at + (uint32_t)(q % 3) * sg_bytes +
                          (uint32_t)(part * WAVES + wave) * 256u;
     buffer_load_lds4(rs_s, __builtin_amdgcn_readfirstlane(dst), off);

@@ -42,8 +42,8 @@ struct DeviceLayer {
   // scales as [W/32][H] (same group offsets), so one 32-block's scales of
   // every output feature are one contiguous run.
   const float* s2k;
-  // The int8 x int8 mode's copy of s13 block-major ([H/32][2W] per group,
-  // same group offsets); DynamicActivations overlays only, else null.
+  // The MFMA engines' copy of s13 block-major ([H/32][2W] per group, same
+  // group offsets).
   const float* s13k;
 
   __host__ __device__ int width(int g) const { return g < E ? I : S; }
