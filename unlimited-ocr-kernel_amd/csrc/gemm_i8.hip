@@ -12,12 +12,13 @@
 // the blocks in ascending order as the reference does, each multiply and add
 // separately rounded.
 //
-// A workgroup of 4 waves computes a 64-row x 256-column item of one expert
-// group: the weight rows are the MFMA's first operand, so a lane holds one
-// token and 16 output features per 32 x 32 tile, and wave w's 64 columns are
-// one (gate, up) block pair of the interleaved w13 rows (SiLU(g) * u is
-// register-local). Each 32-deep stage (int8 rows of the token tile and of
-// the weight tile, and their f32 block scales) is brought into LDS by
+// A workgroup of 4 waves computes a 64-row item of one expert group: the
+// weight rows are the MFMA's first operand, so a lane holds one token and 16
+// output features per 32 x 32 tile. Gate/up items are 256 columns wide and
+// wave w's 64 columns are one (gate, up) block pair of the interleaved w13
+// rows (SiLU(g) * u is register-local); down items are 128 columns wide, 32
+// per wave. Each 32-deep stage (int8 rows of the token tile and of the
+// weight tile, and their f32 block scales) is brought into LDS by
 // global->LDS loads, NST stages ahead.
 #include "common.hpp"
 #include "moe_kernels.hpp"
@@ -31,10 +32,14 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kI8TileM = 64;   // token rows per item
-constexpr int kI8TileN = 256;  // output features per item
+// Output features per item: 256 for gate/up (each wave one gate/up block
+// pair), 128 for down (each wave one 32-feature tile), so the down launch's
+// items are short enough that the shared expert's (twice as deep) do not
+// set its end.
+constexpr int i8_nft(bool gateup) { return gateup ? 2 : 1; }  // feature tiles per wave
+constexpr int i8_tile_n(bool gateup) { return 128 * i8_nft(gateup); }
 constexpr int kI8Stages = 4;   // LDS ring depth
 constexpr int kI8Threads = 256;
-constexpr int kI8WgPerCu = 3;  // 3 x 46 KB of LDS rings; <= 168 VGPRs per lane
 constexpr int kI8Xcds = 8;
 
 // Stage layout (bytes): token rows [64][32], weight rows [256][32], token
@@ -42,12 +47,11 @@ constexpr int kI8Xcds = 8;
 // at position c ^ ((r >> 3) & 1), so the 16-byte fragment reads of 16
 // consecutive rows cover all LDS banks.
 constexpr uint32_t kI8ARows = kI8TileM * 32;
-constexpr uint32_t kI8BRows = kI8TileN * 32;
+constexpr uint32_t i8_brows(bool gateup) { return (uint32_t)i8_tile_n(gateup) * 32; }
 constexpr uint32_t kI8AScale = kI8TileM * 4;
-constexpr uint32_t kI8BScale = kI8TileN * 4;
-constexpr uint32_t kI8Stage = kI8ARows + kI8BRows + kI8AScale + kI8BScale;  // 11.5 KB
-constexpr uint32_t kI8BAt = kI8ARows, kI8ASAt = kI8ARows + kI8BRows,
-                   kI8BSAt = kI8ARows + kI8BRows + kI8AScale;
+constexpr uint32_t i8_stage(bool gateup) {  // 11.5 KB (gate/up), 6.75 KB (down)
+  return kI8ARows + i8_brows(gateup) + kI8AScale + (uint32_t)i8_tile_n(gateup) * 4;
+}
 
 __device__ __forceinline__ i32x4 i8_rsrc(const void* base, uint32_t bytes) {
   const unsigned long long a = reinterpret_cast<unsigned long long>(base);
@@ -81,7 +85,13 @@ constexpr int i8_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | 
 // rows 8 KB = 8, token scales 1, weight scales 4: 15 over 4 waves, waves
 // 0..2 take 4 and wave 3 takes 3 (+1 repeated token-scale load so every
 // wave issues 4).
-constexpr int kI8LoadsPerWave = 4;
+// Wave-loads per stage: token rows 2, weight rows 4 per feature tile pair
+// member, token scales 1, weight scales 2 per 128 features; gate/up 15
+// (4 per wave, the 16th repeats the token-scale load), down 9 (3 per wave,
+// three repeats).
+constexpr int i8_loads(bool gateup) { return 3 + 6 * i8_nft(gateup); }
+constexpr int i8_loads_per_wave(bool gateup) { return (i8_loads(gateup) + 3) / 4; }
+constexpr int i8_wg_per_cu(bool gateup) { return gateup ? 3 : 4; }
 
 // Row of w13 (interleaved in blocks of 32: gate j.., up j..) -> its row in
 // checkpoint order (gate rows 0..W-1, then up rows W..2W-1).
@@ -98,16 +108,20 @@ __device__ __forceinline__ int ckpt_row13(int r, int W) {
 // TRACE: the instantiation that also stores every block sum (tests); the
 // plain one carries no trace code, so it fits three workgroups per CU.
 template <bool GATEUP, bool TRACE>
-__global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(DeviceLayer L,
+__global__ __launch_bounds__(kI8Threads, i8_wg_per_cu(GATEUP)) void i8_group_kernel(DeviceLayer L,
                                                                           Scratch S, I8Planes P,
                                                                           int T) {
   extern __shared__ __align__(16) char lds[];
+  constexpr int NFT = i8_nft(GATEUP), kTileN = i8_tile_n(GATEUP);
+  constexpr int kLoads = i8_loads(GATEUP), kLpw = i8_loads_per_wave(GATEUP);
+  constexpr uint32_t kStage = i8_stage(GATEUP), kBAt = kI8ARows,
+                     kASAt = kI8ARows + i8_brows(GATEUP), kBSAt = kASAt + kI8AScale;
   const int all_tiles = S.counters[0];
   const int routed_tiles = S.counters[1];
   const int n_routed = GATEUP ? 2 * L.I : L.H;
   const int n_shared = GATEUP ? 2 * L.S : L.H;
-  const int nt_r = (n_routed + kI8TileN - 1) / kI8TileN;
-  const int nt_s = (n_shared + kI8TileN - 1) / kI8TileN;
+  const int nt_r = (n_routed + kTileN - 1) / kTileN;
+  const int nt_s = (n_shared + kTileN - 1) / kTileN;
   const int items = routed_tiles * nt_r + (all_tiles - routed_tiles) * nt_s;
   const int per_xcd = (items + kI8Xcds - 1) / kI8Xcds;
   const int item = (blockIdx.x % kI8Xcds) * per_xcd + blockIdx.x / kI8Xcds;
@@ -130,7 +144,7 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
   const int group_rows = routed ? S.offsets[g + 1] - S.offsets[g] : T;
   const int mrows = min(kI8TileM, group_rows - r0);
   const int base = routed ? S.offsets[g] : 0;
-  const int n0 = ntile * kI8TileN;
+  const int n0 = ntile * kTileN;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar load plan
@@ -173,40 +187,41 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
 
   // Per-lane load plan of this wave (4 wave-loads per stage): global byte
   // offsets at block 0 and the LDS position of each.
-  uint32_t off[kI8LoadsPerWave], lds_at[kI8LoadsPerWave];
-  int kind[kI8LoadsPerWave];  // 0 token rows, 1 weight rows, 2 token scales, 3 weight scales
+  uint32_t off[kLpw], lds_at[kLpw];
+  int kind[kLpw];  // 0 token rows, 1 weight rows, 2 token scales, 3 weight scales
 #pragma unroll
-  for (int j = 0; j < kI8LoadsPerWave; j++) {
-    const int L15 = wave * kI8LoadsPerWave + j;  // 0..15; 15 repeats load 10
-    const int ld = L15 < 15 ? L15 : 10;
+  for (int j = 0; j < kLpw; j++) {
+    constexpr int kNB = 4 * NFT;  // weight-row wave-loads
+    const int slot = wave * kLpw + j;  // slots past kLoads repeat the token-scale load
+    const int ld = slot < kLoads ? slot : 2 + kNB;
     if (ld < 2) {  // token rows: 32 rows of 32 B per wave-load
       const int r = ld * 32 + lane / 2, c = (lane & 1) ^ ((r >> 3) & 1);
       const int src = a_source(r);
       kind[j] = 0;
       off[j] = src >= 0 ? (uint32_t)src * (uint32_t)K + 16u * c : kI8Out;
       lds_at[j] = (uint32_t)ld * 1024u;
-    } else if (ld < 10) {  // weight rows
+    } else if (ld < 2 + kNB) {  // weight rows
       const int r = (ld - 2) * 32 + lane / 2, c = (lane & 1) ^ ((r >> 3) & 1);
       kind[j] = 1;
       off[j] = n0 + r < N ? (uint32_t)(n0 + r) * 32u + 16u * c : kI8Out;
-      lds_at[j] = kI8BAt + (uint32_t)(ld - 2) * 1024u;
-    } else if (ld == 10) {  // token scales: 64 rows, one dword each
+      lds_at[j] = kBAt + (uint32_t)(ld - 2) * 1024u;
+    } else if (ld == 2 + kNB) {  // token scales: 64 rows, one dword each
       const int src = a_source(lane);
       kind[j] = 2;
       off[j] = src >= 0 ? (uint32_t)src * (uint32_t)nblk * 4u : kI8Out;
-      lds_at[j] = kI8ASAt;
+      lds_at[j] = kASAt;
     } else {  // weight scales: 4 x 64 rows
-      const int r = (ld - 11) * 64 + lane;
+      const int r = (ld - 3 - kNB) * 64 + lane;
       kind[j] = 3;
       off[j] = n0 + r < N ? (uint32_t)(n0 + r) * bs_row : kI8Out;
-      lds_at[j] = kI8BSAt + (uint32_t)(ld - 11) * 256u;
+      lds_at[j] = kBSAt + (uint32_t)(ld - 3 - kNB) * 256u;
     }
   }
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds);
   auto issue = [&](int stage, int b) {
-    const uint32_t st = lds0 + (uint32_t)stage * kI8Stage;
+    const uint32_t st = lds0 + (uint32_t)stage * kStage;
 #pragma unroll
-    for (int j = 0; j < kI8LoadsPerWave; j++) {
+    for (int j = 0; j < kLpw; j++) {
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(st + lds_at[j]);
       const bool out = off[j] == kI8Out;
       if (kind[j] == 0) i8_load16(rs_aq, m0, out ? kI8Out : off[j] + 32u * b);
@@ -219,16 +234,16 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
   // Accumulators: [feature tile ft][token tile tt]; lane l holds token
   // 32 tt + l % 32 and features 32 ft + 8 (r / 4) + 4 (l / 32) + r % 4 of the
   // wave's 64 columns.
-  float acc[2][2][16];
+  float acc[NFT][2][16];
 #pragma unroll
-  for (int ft = 0; ft < 2; ft++)
+  for (int ft = 0; ft < NFT; ft++)
 #pragma unroll
     for (int tt = 0; tt < 2; tt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[ft][tt][r] = -0.0f;  // Rust's float sum starts at -0.0
 
   const int fr = lane & 31, fc = lane >> 5;
-  const int wcol = wave * 64;  // this wave's first feature within the item
+  const int wcol = wave * 32 * NFT;  // this wave's first feature within the item
   // Trace of the exact block sums (tests): routed rows by dispatched
   // position, the shared expert's only when it has a single row.
   int32_t* trace = nullptr;
@@ -244,17 +259,17 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
     // Stage b landed (own loads: the later stages still in flight), then the
     // barrier publishes every wave's part and retires stage b - 1's readers.
     const int ahead = min(kDepth - 1, nblk - 1 - b);
-    if (ahead >= 2) __builtin_amdgcn_s_waitcnt(i8_vmcnt(2 * kI8LoadsPerWave));
-    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(i8_vmcnt(kI8LoadsPerWave));
+    if (ahead >= 2) __builtin_amdgcn_s_waitcnt(i8_vmcnt(2 * kLpw));
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(i8_vmcnt(kLpw));
     else __builtin_amdgcn_s_waitcnt(i8_vmcnt(0));
     __syncthreads();
     if (b + kDepth < nblk) issue((b + kDepth) % kI8Stages, b + kDepth);
-    const char* cur = lds + (b % kI8Stages) * kI8Stage;
-    i32x4 wf[2], xf[2];
+    const char* cur = lds + (b % kI8Stages) * kStage;
+    i32x4 wf[NFT], xf[2];
 #pragma unroll
-    for (int ft = 0; ft < 2; ft++) {
+    for (int ft = 0; ft < NFT; ft++) {
       const int r = wcol + 32 * ft + fr;
-      wf[ft] = *reinterpret_cast<const i32x4*>(cur + kI8BAt + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
+      wf[ft] = *reinterpret_cast<const i32x4*>(cur + kBAt + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
     }
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
@@ -264,15 +279,15 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
     float xsv[2];
 #pragma unroll
     for (int tt = 0; tt < 2; tt++)
-      xsv[tt] = *reinterpret_cast<const float*>(cur + kI8ASAt + (32 * tt + fr) * 4);
+      xsv[tt] = *reinterpret_cast<const float*>(cur + kASAt + (32 * tt + fr) * 4);
 #pragma unroll
-    for (int ft = 0; ft < 2; ft++) {
+    for (int ft = 0; ft < NFT; ft++) {
       // This feature tile's 16 weight scales (lane features 8 q + 4 fc + 0..3).
       float wsv[16];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const float4 v = *reinterpret_cast<const float4*>(
-            cur + kI8BSAt + (wcol + 32 * ft + 8 * q + 4 * fc) * 4);
+            cur + kBSAt + (wcol + 32 * ft + 8 * q + 4 * fc) * 4);
         wsv[4 * q + 0] = v.x;
         wsv[4 * q + 1] = v.y;
         wsv[4 * q + 2] = v.z;
@@ -311,7 +326,7 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
 
   // ---- epilogue
   const int row_in = fr;  // token within a token tile
-  if (GATEUP) {
+  if constexpr (GATEUP) {
     // Feature tile 0 holds gate values, tile 1 the matching up values:
     // hidden column 32 (n0 + wcol) / 64 + 8 (r/4) + 4 fc + r%4.
     if (n0 + wcol >= N) return;
@@ -336,7 +351,7 @@ __global__ __launch_bounds__(kI8Threads, kI8WgPerCu) void i8_group_kernel(Device
       if (row >= mrows) continue;
       const size_t at = (size_t)(base + r0 + row) * L.H;
 #pragma unroll
-      for (int ft = 0; ft < 2; ft++)
+      for (int ft = 0; ft < NFT; ft++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int n = n0 + wcol + 32 * ft + 8 * (r >> 2) + 4 * fc + (r & 3);
@@ -422,7 +437,7 @@ bool i8_supported(const DeviceLayer& L) { return L.H % 64 == 0 && L.I % 64 == 0 
 
 static unsigned i8_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   const int n = gateup ? std::max(2 * L.I, 2 * L.S) : L.H;
-  const long long items = (long long)tiles_bound * ((n + kI8TileN - 1) / kI8TileN);
+  const long long items = (long long)tiles_bound * ((n + i8_tile_n(gateup) - 1) / i8_tile_n(gateup));
   return (unsigned)((items + kI8Xcds - 1) / kI8Xcds * kI8Xcds);
 }
 
@@ -432,7 +447,7 @@ void launch_i8_gateup(const DeviceLayer& L, const Scratch& S, const I8Planes& P,
   auto* kern = trace ? i8_group_kernel<true, true> : i8_group_kernel<true, false>;
   hipLaunchKernelGGL(kern,
                      dim3(i8_grid(L, tiles_bound, true)), dim3(kI8Threads),
-                     kI8Stages * kI8Stage, s, L, S, P, T);
+                     kI8Stages * i8_stage(true), s, L, S, P, T);
 }
 
 void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
@@ -441,7 +456,7 @@ void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, i
   auto* kern = trace ? i8_group_kernel<false, true> : i8_group_kernel<false, false>;
   hipLaunchKernelGGL(kern,
                      dim3(i8_grid(L, tiles_bound, false)), dim3(kI8Threads),
-                     kI8Stages * kI8Stage, s, L, S, P, T);
+                     kI8Stages * i8_stage(false), s, L, S, P, T);
 }
 
 }  // namespace uocr
