@@ -557,8 +557,8 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       phase_end(ctx);
     }
     if (int8) {
-      // Quantise the input rows, gate/up into FP32 hidden rows, quantise
-      // those, down.
+      // Quantise the input rows, gate/up into quantised hidden rows (FP32
+      // ones and a quantising launch when traced), down.
       uocr::I8Planes P;
       const size_t routed_rows = T * L.K;
       P.xq = S.q8x;
@@ -574,12 +574,15 @@ int enqueue_experts(const Exec& ex, const uocr_moe_layer* layer, const float* x,
       phase_begin(ctx, kGateUp);
       uocr::launch_i8_gateup(L, S, P, Ti, tiles_bound, st);
       phase_end(ctx);
-      if (int r = trace_hidden(S.h, S.hs)) return r;
-      phase_begin(ctx, kSplit);
-      uocr::launch_quantize_rows(S.h, (int)routed_rows, L.I, P.hid_q, P.hid_s, S.hs, Ti, L.S,
-                                 P.hid_q + routed_rows * L.I, P.hid_s + routed_rows * L.I / 32,
-                                 S.err, st);
-      phase_end(ctx);
+      // Untraced, the gate/up epilogue has written the hidden rows quantised.
+      if (uocr::i8_traced(S, Ti)) {
+        if (int r = trace_hidden(S.h, S.hs)) return r;
+        phase_begin(ctx, kSplit);
+        uocr::launch_quantize_rows(S.h, (int)routed_rows, L.I, P.hid_q, P.hid_s, S.hs, Ti, L.S,
+                                   P.hid_q + routed_rows * L.I, P.hid_s + routed_rows * L.I / 32,
+                                   S.err, st);
+        phase_end(ctx);
+      }
       phase_begin(ctx, kDown);
       uocr::launch_i8_down(L, S, P, Ti, tiles_bound, st);
       phase_end(ctx);

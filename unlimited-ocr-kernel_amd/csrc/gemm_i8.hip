@@ -331,16 +331,60 @@ __global__ __launch_bounds__(kI8Threads, i8_wg_per_cu(GATEUP)) void i8_group_ker
     // hidden column 32 (n0 + wcol) / 64 + 8 (r/4) + 4 fc + r%4.
     if (n0 + wcol >= N) return;
     const int hcol0 = (n0 + wcol) / 2;
-    float* hout = routed ? P.hid : P.hid_shared;
+    if constexpr (TRACE) {
+      // FP32 hidden rows (the trace copies them), quantised by their own
+      // launch.
+      float* hout = routed ? P.hid : P.hid_shared;
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-      const int row = 32 * tt + row_in;
-      if (row >= mrows) continue;
-      const size_t at = routed ? (size_t)(base + r0 + row) * L.I : (size_t)(r0 + row) * L.S;
+      for (int tt = 0; tt < 2; tt++) {
+        const int row = 32 * tt + row_in;
+        if (row >= mrows) continue;
+        const size_t at = routed ? (size_t)(base + r0 + row) * L.I : (size_t)(r0 + row) * L.S;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int col = hcol0 + 8 * (r >> 2) + 4 * fc + (r & 3);
-        hout[at + col] = silu(acc[0][tt][r]) * acc[1][tt][r];
+        for (int r = 0; r < 16; r++) {
+          const int col = hcol0 + 8 * (r >> 2) + 4 * fc + (r & 3);
+          hout[at + col] = silu(acc[0][tt][r]) * acc[1][tt][r];
+        }
+      }
+    } else {
+      // Int8Matrix::quantize (src/cpu/quantized.rs:43-74) of the hidden
+      // rows here, as quantize_rows_kernel does it: a wave's 32 hidden
+      // values of a token row are one 32-block (hcol0 is a multiple of 32),
+      // 16 in lane l and 16 in lane l ^ 32.
+      const int W = L.width(g);
+      const int nb = W / kQBlock, blk = hcol0 / kQBlock;
+      int8_t* qbase = routed ? P.hid_q : P.hid_q + (size_t)T * L.K * L.I;
+      float* sbase = routed ? P.hid_s : P.hid_s + (size_t)T * L.K * (L.I / kQBlock);
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++) {
+        const int row = 32 * tt + row_in;
+        float h[16];
+        float maximum = 0.0f;
+        int bad = 0;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          h[r] = silu(acc[0][tt][r]) * acc[1][tt][r];
+          bad |= !isfinite(h[r]);
+          maximum = fmaxf(maximum, fabsf(h[r]));
+        }
+        maximum = fmaxf(maximum, __shfl_xor(maximum, 32));
+        bad |= __shfl_xor(bad, 32);
+        const float scale = maximum / 127.0f;
+        if (row >= mrows) continue;
+        if (fc == 0 && (bad || (maximum > 0.0f && scale == 0.0f))) raise_error(S.err, kErrNumerical);
+        const size_t prow = routed ? (size_t)(base + r0 + row) : (size_t)(r0 + row);
+        if (fc == 0) sbase[prow * nb + blk] = scale;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            int qv = 0;
+            if (scale != 0.0f) qv = (int)fminf(fmaxf(rintf(h[4 * g4 + j] / scale), -127.0f), 127.0f);
+            w |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * j);
+          }
+          *reinterpret_cast<uint32_t*>(qbase + prow * W + hcol0 + 8 * g4 + 4 * fc) = w;
+        }
       }
     }
   } else {
@@ -441,9 +485,17 @@ static unsigned i8_grid(const DeviceLayer& L, int tiles_bound, bool gateup) {
   return (unsigned)((items + kI8Xcds - 1) / kI8Xcds * kI8Xcds);
 }
 
+// The traced instantiations run when the forward records any block sums or
+// hidden rows; the plain gate/up then leaves FP32 hidden rows for the
+// trace and for quantize_rows_kernel, otherwise it writes them quantised.
+bool i8_traced(const Scratch& S, int T) {
+  return S.q8.gateup || S.q8.down || S.q8.hidden ||
+         (T == 1 && (S.q8.s_gateup || S.q8.s_down || S.q8.s_hidden));
+}
+
 void launch_i8_gateup(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
                       int tiles_bound, hipStream_t s) {
-  const bool trace = S.q8.gateup != nullptr || (T == 1 && S.q8.s_gateup != nullptr);
+  const bool trace = i8_traced(S, T);
   auto* kern = trace ? i8_group_kernel<true, true> : i8_group_kernel<true, false>;
   hipLaunchKernelGGL(kern,
                      dim3(i8_grid(L, tiles_bound, true)), dim3(kI8Threads),
@@ -452,7 +504,7 @@ void launch_i8_gateup(const DeviceLayer& L, const Scratch& S, const I8Planes& P,
 
 void launch_i8_down(const DeviceLayer& L, const Scratch& S, const I8Planes& P, int T,
                     int tiles_bound, hipStream_t s) {
-  const bool trace = S.q8.down != nullptr || (T == 1 && S.q8.s_down != nullptr);
+  const bool trace = i8_traced(S, T);
   auto* kern = trace ? i8_group_kernel<false, true> : i8_group_kernel<false, false>;
   hipLaunchKernelGGL(kern,
                      dim3(i8_grid(L, tiles_bound, false)), dim3(kI8Threads),

@@ -231,6 +231,7 @@ struct I8Planes {
 };
 constexpr int kI8BM = 64;  // token rows per row tile
 bool i8_supported(const DeviceLayer& L);
+bool i8_traced(const Scratch& S, int T);  // traced GEMMs: FP32 hidden rows + quantize_rows_kernel
 void launch_quantize_rows(const float* src, int rows, int K, int8_t* dst, float* sc,
                           const float* src2, int rows2, int K2, int8_t* dst2, float* sc2,
                           int* err, hipStream_t s);
